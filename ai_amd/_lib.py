@@ -1,0 +1,102 @@
+"""ctypes binding of librv12.so (declarations in include/rv12.h).
+
+torch is imported first so that the library binds to the HIP runtime torch
+already loaded (both carry the soname libamdhip64.so.7): device pointers and
+streams from torch are then valid in the library.  Loading fails loudly when
+the library is missing; there is no fallback path.
+"""
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede loading librv12.so, see above)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librv12.so")
+
+RV12_OK = 0
+RV12_E_NULL, RV12_E_SHAPE, RV12_E_MODE, RV12_E_TOKENS = -1, -2, -3, -4
+RV12_E_WORKSPACE, RV12_E_CONFIG, RV12_E_BASE, RV12_E_ALIGN, RV12_E_SIZE = -5, -6, -7, -8, -9
+RV12_E_LAUNCH = -20
+
+# every symbol include/rv12.h declares
+EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_retile", "rv12_encode_stats",
+           "rv12_encode", "rv12_encode_exc", "rv12_workspace_bytes", "rv12_gemv", "rv12_gemm",
+           "rv12_decode_rows")
+ABI_VERSION = 1
+
+
+class Codec(ctypes.Structure):
+    _fields_ = [("m8", ctypes.c_void_p), ("e4", ctypes.c_void_p), ("rp", ctypes.c_void_p),
+                ("er", ctypes.c_void_p), ("ec", ctypes.c_void_p), ("ev", ctypes.c_void_p),
+                ("n", ctypes.c_int32), ("k", ctypes.c_int32), ("ch", ctypes.c_int32), ("base", ctypes.c_int32),
+                ("n_exc", ctypes.c_int64)]
+
+
+class Matrix(ctypes.Structure):
+    _fields_ = [("tiles", ctypes.c_void_p), ("rp", ctypes.c_void_p), ("er", ctypes.c_void_p),
+                ("ec", ctypes.c_void_p), ("ev", ctypes.c_void_p),
+                ("n", ctypes.c_int32), ("k", ctypes.c_int32), ("base", ctypes.c_int32), ("n_exc", ctypes.c_int64)]
+
+
+class Launch(ctypes.Structure):
+    _fields_ = [("rb", ctypes.c_int32), ("waves", ctypes.c_int32), ("splits", ctypes.c_int32)]
+
+
+class Rv12Error(RuntimeError):
+    def __init__(self, status, where):
+        self.status = status
+        super().__init__(f"{where}: {strerror(status)} (status {status})")
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"librv12.so not built at {LIB_PATH}: run `python -m ai_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        P, I, I64, F, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
+        L.rv12_abi_version.restype = I
+        L.rv12_abi_version.argtypes = []
+        L.rv12_strerror.restype = ctypes.c_char_p
+        L.rv12_strerror.argtypes = [I]
+        L.rv12_tiles_bytes.restype = SZ
+        L.rv12_tiles_bytes.argtypes = [I, I]
+        L.rv12_retile.restype = I
+        L.rv12_retile.argtypes = [ctypes.POINTER(Codec), P, SZ, P]
+        L.rv12_encode_stats.restype = I
+        L.rv12_encode_stats.argtypes = [P, I, I, P, P]
+        L.rv12_encode.restype = I
+        L.rv12_encode.argtypes = [P, I, I, I, I, P, P, P, P]
+        L.rv12_encode_exc.restype = I
+        L.rv12_encode_exc.argtypes = [P, I, I, I, P, P, P, P, P]
+        L.rv12_workspace_bytes.restype = SZ
+        L.rv12_workspace_bytes.argtypes = [I, I, I, I]
+        L.rv12_gemv.restype = I
+        L.rv12_gemv.argtypes = [ctypes.POINTER(Matrix), P, P, P, F, I, ctypes.POINTER(Launch), P, SZ, P]
+        L.rv12_gemm.restype = I
+        L.rv12_gemm.argtypes = [ctypes.POINTER(Matrix), P, P, I, P, F, I, ctypes.POINTER(Launch), P, SZ, P]
+        L.rv12_decode_rows.restype = I
+        L.rv12_decode_rows.argtypes = [ctypes.POINTER(Matrix), I, I, P, I, P]
+        v = L.rv12_abi_version()
+        if v != ABI_VERSION:
+            raise RuntimeError(f"librv12.so ABI version {v}, expected {ABI_VERSION}")
+        _lib = L
+    return _lib
+
+
+def strerror(status):
+    return lib().rv12_strerror(int(status)).decode()
+
+
+def check(status, where):
+    """Map a status to the exception the reference raises for the same fault:
+    ValueError for argument and shape faults (wcomp.py:122-123), RuntimeError
+    for a failed launch."""
+    if status == RV12_OK:
+        return
+    if status == RV12_E_LAUNCH:
+        raise Rv12Error(status, where)
+    raise ValueError(f"{where}: {strerror(status)} (status {status})")

@@ -1,0 +1,194 @@
+// C-ABI layer of librv12: host-side validation, launch-shape choice and
+// kernel launches.  Every check runs before any GPU call, so a bad argument
+// returns a status without touching the device.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rv12.h"
+#include "rv12_internal.h"
+
+using namespace rv12;
+
+namespace {
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int launch_status() { return hipGetLastError() == hipSuccess ? RV12_OK : RV12_E_LAUNCH; }
+
+int64_t nblocks(int n) { return ((int64_t)n + 15) / 16; }
+
+// Built-in launch shape for (N, K, T): enough workgroups to cover 256 CUs a
+// few times over, K split only when the row blocks alone are too few.
+void default_launch(int N, int K, int T, int* rb, int* waves, int* splits) {
+    const int64_t nblk = nblocks(N);
+    const int nsteps = K / 32;
+    *rb = (nblk >= 4096 && T <= 2) ? 2 : 1;
+    *waves = nsteps >= 16 ? 4 : (nsteps >= 8 ? 2 : 1);
+    const int64_t wgs = (nblk + *rb - 1) / *rb;
+    int s = 1;
+    while (wgs * s < 1024 && s * 2 <= kMaxSplits && nsteps / (s * 2) >= *waves * 4) s *= 2;
+    while (s < kMaxSplits && s < nsteps && linear_lds_bytes(K, T, *rb, *waves, s) > kMaxLds) ++s;
+    *splits = s;
+}
+
+int resolve_launch(int N, int K, int T, const rv12_launch* cfg, int* rb, int* waves, int* splits) {
+    int drb, dw, ds;
+    default_launch(N, K, T, &drb, &dw, &ds);
+    *rb = (cfg && cfg->rb) ? cfg->rb : drb;
+    *waves = (cfg && cfg->waves) ? cfg->waves : dw;
+    *splits = (cfg && cfg->splits) ? cfg->splits : ds;
+    if (cfg && (!cfg->splits) && (cfg->rb || cfg->waves)) {
+        // keep the LDS bound when only rb / waves were given
+        while (*splits < kMaxSplits && *splits < K / 32 &&
+               linear_lds_bytes(K, T, *rb, *waves, *splits) > kMaxLds)
+            ++*splits;
+    }
+    if (*rb != 1 && *rb != 2 && *rb != 4) return RV12_E_CONFIG;
+    if (*waves < 1 || *waves > kMaxWaves) return RV12_E_CONFIG;
+    if (*splits < 1 || *splits > kMaxSplits || *splits > K / 32) return RV12_E_CONFIG;
+    if (linear_lds_bytes(K, T, *rb, *waves, *splits) > kMaxLds) return RV12_E_CONFIG;
+    return RV12_OK;
+}
+
+size_t ws_bytes_for(int N, int T, int splits) {
+    if (splits <= 1) return 0;
+    return 4 * ((size_t)splits * T * (size_t)(nblocks(N) * 16) + (size_t)splits * T);
+}
+
+int check_matrix(const rv12_matrix* w) {
+    if (!w || !w->tiles || !w->rp) return RV12_E_NULL;
+    if (w->n_exc > 0 && (!w->er || !w->ec || !w->ev)) return RV12_E_NULL;
+    if (w->n < 1 || w->k < 32 || w->k % 32) return RV12_E_SHAPE;
+    if (w->base < 0 || w->base > 241) return RV12_E_BASE;
+    if (!aligned16(w->tiles)) return RV12_E_ALIGN;
+    return RV12_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rv12_abi_version(void) { return RV12_ABI_VERSION; }
+
+const char* rv12_strerror(int s) {
+    switch (s) {
+        case RV12_OK: return "ok";
+        case RV12_E_NULL: return "required pointer is NULL";
+        case RV12_E_SHAPE: return "bad shape (N >= 1, K >= 32, K % 32 == 0, K % CH == 0, CH % 16 == 0, rows in [0, N])";
+        case RV12_E_MODE: return "mode must be 0, 1 or 2";
+        case RV12_E_TOKENS: return "T must be in [1, 16]";
+        case RV12_E_WORKSPACE: return "workspace smaller than rv12_workspace_bytes()";
+        case RV12_E_CONFIG: return "launch configuration out of range";
+        case RV12_E_BASE: return "base must be in [0, 241]";
+        case RV12_E_ALIGN: return "x, y, lnw or tiles not aligned (16 bytes; lnw 8 bytes)";
+        case RV12_E_SIZE: return "output buffer smaller than rv12_tiles_bytes()";
+        case RV12_E_LAUNCH: return "kernel launch failed";
+    }
+    return "unknown rv12 status";
+}
+
+size_t rv12_tiles_bytes(int n, int k) {
+    if (n < 1 || k < 32 || k % 32) return 0;
+    return (size_t)nblocks(n) * 16 * (size_t)k * 3 / 2;
+}
+
+int rv12_retile(const rv12_codec* in, uint32_t* tiles, size_t tiles_bytes, void* stream) {
+    if (!in || !tiles || !in->m8 || !in->e4) return RV12_E_NULL;
+    if (in->n < 1 || in->k < 32 || in->k % 32 || in->ch < 16 || in->ch % 16 || in->k % in->ch) return RV12_E_SHAPE;
+    if (in->base < 0 || in->base > 241) return RV12_E_BASE;
+    if (!aligned16(tiles)) return RV12_E_ALIGN;
+    if (tiles_bytes < rv12_tiles_bytes(in->n, in->k)) return RV12_E_SIZE;
+    launch_retile(in->m8, in->e4, in->n, in->k, in->ch, in->base, tiles, (hipStream_t)stream);
+    return launch_status();
+}
+
+int rv12_encode_stats(const uint16_t* w, int n, int k, int32_t* hist, void* stream) {
+    if (!w || !hist) return RV12_E_NULL;
+    if (n < 1 || k < 1) return RV12_E_SHAPE;
+    if (!aligned16(w)) return RV12_E_ALIGN;
+    launch_encode_stats(w, (int64_t)n * k, hist, (hipStream_t)stream);
+    return launch_status();
+}
+
+int rv12_encode(const uint16_t* w, int n, int k, int ch, int base, uint8_t* m8, uint8_t* e4, int32_t* row_exc,
+                void* stream) {
+    if (!w || !m8 || !e4 || !row_exc) return RV12_E_NULL;
+    if (n < 1 || k < 2 || ch < 2 || ch % 2 || k % ch) return RV12_E_SHAPE;
+    if (base < 0 || base > 241) return RV12_E_BASE;
+    launch_encode(w, n, k, ch, base, m8, e4, row_exc, (hipStream_t)stream);
+    return launch_status();
+}
+
+int rv12_encode_exc(const uint16_t* w, int n, int k, int base, const int32_t* rp, int32_t* er, int32_t* ec,
+                    float* ev, void* stream) {
+    if (!w || !rp || !er || !ec || !ev) return RV12_E_NULL;
+    if (n < 1 || k < 1) return RV12_E_SHAPE;
+    if (base < 0 || base > 241) return RV12_E_BASE;
+    launch_encode_exc(w, n, k, base, rp, er, ec, ev, (hipStream_t)stream);
+    return launch_status();
+}
+
+size_t rv12_workspace_bytes(int n, int k, int t, int splits) {
+    if (n < 1 || k < 32 || k % 32 || t < 1 || t > 16) return 0;
+    if (splits == 0) {
+        int rb, w, s;
+        default_launch(n, k, t, &rb, &w, &s);
+        splits = s;
+    }
+    return ws_bytes_for(n, t, splits);
+}
+
+int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps, int mode,
+              const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream) {
+    int rc = check_matrix(w);
+    if (rc) return rc;
+    if (!x || !y) return RV12_E_NULL;
+    if (mode < 0 || mode > 2) return RV12_E_MODE;
+    if (t < 1 || t > 16) return RV12_E_TOKENS;
+    if (!aligned16(x) || !aligned16(y) || ((uintptr_t)lnw & 7u)) return RV12_E_ALIGN;
+    int rb, waves, splits;
+    rc = resolve_launch(w->n, w->k, t, cfg, &rb, &waves, &splits);
+    if (rc) return rc;
+    const size_t need = ws_bytes_for(w->n, t, splits);
+    if (need && (!ws || ws_bytes < need)) return RV12_E_WORKSPACE;
+    if (need && !aligned16(ws)) return RV12_E_ALIGN;
+    LinearParams p;
+    p.tiles = w->tiles;
+    p.rp = w->rp;
+    p.er = w->er;
+    p.ec = w->ec;
+    p.ev = w->ev;
+    p.x = x;
+    p.y = y;
+    p.lnw = lnw;
+    p.part = (float*)ws;
+    p.ssq = need ? (float*)ws + (size_t)splits * t * (size_t)(nblocks(w->n) * 16) : nullptr;
+    p.N = w->n;
+    p.K = w->k;
+    p.npad = (int)(nblocks(w->n) * 16);
+    p.base = w->base;
+    p.mode = mode;
+    p.xs = mode == 2 ? 2 * w->k : w->k;
+    p.n_exc = w->n_exc;
+    p.eps = eps;
+    if (launch_linear(p, t, rb, waves, splits, (hipStream_t)stream)) return RV12_E_CONFIG;
+    return launch_status();
+}
+
+int rv12_gemv(const rv12_matrix* w, const float* x, float* y, const uint16_t* lnw, float eps, int mode,
+              const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream) {
+    return rv12_gemm(w, x, y, 1, lnw, eps, mode, cfg, ws, ws_bytes, stream);
+}
+
+int rv12_decode_rows(const rv12_matrix* w, int first, int last, void* out, int out_f32, void* stream) {
+    int rc = check_matrix(w);
+    if (rc) return rc;
+    if (!out) return RV12_E_NULL;
+    if (first < 0 || last > w->n || first > last) return RV12_E_SHAPE;
+    if (!aligned16(out)) return RV12_E_ALIGN;
+    if (first == last) return RV12_OK;
+    launch_decode(*w, first, last, out, out_f32, (hipStream_t)stream, 0, w->n_exc);
+    return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,217 @@
+"""12-bit lossless bf16 weights and the fused decode-linear, on MI355X.
+
+Operator API of the reference module ramvi/engine/ramvi_engine/kernels/wcomp.py
+with the same names, argument meaning and error behaviour:
+
+    compress(W, CH=256) -> dict          wcomp.py:13-32  (same dict, bit for bit)
+    decompress(c) -> bf16[N, K]          wcomp.py:35-45
+    gemvc1(x, c, y, mode, BN, w, lnw, eps)    wcomp.py:118-126
+    gemvc_tc(x, c, y, mode, T, BN, w, S)      wcomp.py:233-242
+    CFG1, CFGT, _SK                      wcomp.py:115, 222-230
+
+plus decode_rows(c, first, last) (prefill_kernels.py:100-110) and prepare(c),
+which re-tiles a dict built elsewhere (the reference's own compress, a file)
+for the kernels.  Every call goes through librv12.so; there is no other path.
+
+The dict keeps the reference keys m8, e4, base, rp, er, ec, ev, N, K, CH and
+adds "q16": the weights re-tiled for the kernels (int32 words, 1.5 bytes per
+weight).  `compact(c)` drops m8/e4 once only the kernels read the dict.
+Launch parameters keep the reference meaning: BN = rows per workgroup
+(rounded up to 16, 32 or 64), w = waves per workgroup, S = K splits.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import Codec, Launch, Matrix, check, lib
+
+CFG1 = {}  # (N, K, MODE) -> (BN, waves) or (BN, waves, S); filled by ai_amd.tune
+CFGT = {}  # (N, K, MODE) -> (BN, waves, S); filled by ai_amd.tune
+_SK = {}   # (N, device) -> workspace tensor (split-K partial sums)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _need_cuda(t, what):
+    if not (torch.is_tensor(t) and t.is_cuda):
+        raise ValueError(f"{what} must be a tensor on the GPU")
+
+
+def _window_base(hist):
+    """First argmax of the 15-wide exponent window counts (wcomp.py:19-21)."""
+    h = hist.to(torch.int64).cpu()
+    cs = torch.cat([torch.zeros(1, dtype=torch.int64), h.cumsum(0)])
+    return int((cs[15:] - cs[:-15]).argmax())
+
+
+def compress(W, CH=256):
+    """W [N, K] bf16 on the GPU -> codec dict (wcomp.py:13-32), plus "q16"."""
+    _need_cuda(W, "W")
+    if W.dtype != torch.bfloat16 or W.dim() != 2:
+        raise ValueError("W must be a 2-D bfloat16 tensor")
+    N, K = W.shape
+    assert K % CH == 0
+    dev = W.device
+    W = W.contiguous()
+    if W.data_ptr() % 16:
+        W = W.clone()
+    st = _stream(dev)
+    L = lib()
+    hist = torch.empty(256, dtype=torch.int32, device=dev)
+    check(L.rv12_encode_stats(_ptr(W), N, K, _ptr(hist), st), "compress")
+    base = _window_base(hist)
+    m8 = torch.empty(N, K, dtype=torch.uint8, device=dev)
+    e4 = torch.empty(N, K // 2, dtype=torch.uint8, device=dev)
+    row_exc = torch.empty(N, dtype=torch.int32, device=dev)
+    check(L.rv12_encode(_ptr(W), N, K, CH, base, _ptr(m8), _ptr(e4), _ptr(row_exc), st), "compress")
+    rp = torch.zeros(N + 1, dtype=torch.int32, device=dev)
+    rp[1:] = row_exc.cumsum(0)
+    E = int(rp[-1])
+    er = torch.empty(E, dtype=torch.int32, device=dev)
+    ec = torch.empty(E, dtype=torch.int32, device=dev)
+    ev = torch.empty(E, dtype=torch.float32, device=dev)
+    if E:
+        check(L.rv12_encode_exc(_ptr(W), N, K, base, _ptr(rp), _ptr(er), _ptr(ec), _ptr(ev), st), "compress")
+    c = {"m8": m8, "e4": e4, "base": base, "rp": rp, "er": er, "ec": ec, "ev": ev, "N": N, "K": K, "CH": CH}
+    if K % 32 == 0 and CH % 16 == 0:
+        prepare(c)
+    return c
+
+
+def prepare(c, device=None):
+    """Re-tile the dict's m8/e4 into "q16" (and move CPU/numpy arrays to the
+    GPU first).  Idempotent."""
+    if "q16" in c:
+        return c
+    dev = torch.device(device) if device is not None else (
+        c["m8"].device if torch.is_tensor(c["m8"]) and c["m8"].is_cuda else torch.device("cuda"))
+    for k, dt in (("m8", torch.uint8), ("e4", torch.uint8), ("rp", torch.int32), ("er", torch.int32),
+                  ("ec", torch.int32), ("ev", torch.float32)):
+        v = c[k]
+        if not torch.is_tensor(v):
+            v = torch.as_tensor(v)
+        c[k] = v.to(device=dev, dtype=dt).contiguous()
+    N, K, CH = int(c["N"]), int(c["K"]), int(c["CH"])
+    nbytes = lib().rv12_tiles_bytes(N, K)
+    if nbytes == 0:
+        raise ValueError("K must be a positive multiple of 32")
+    tiles = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    cod = Codec(_ptr(c["m8"]), _ptr(c["e4"]), _ptr(c["rp"]), _ptr(c["er"]), _ptr(c["ec"]), _ptr(c["ev"]),
+                N, K, CH, int(c["base"]), int(c["er"].numel()))
+    check(lib().rv12_retile(ctypes.byref(cod), _ptr(tiles), nbytes, _stream(dev)), "prepare")
+    c["q16"] = tiles
+    return c
+
+
+def compact(c):
+    """Drop m8/e4 (the kernels read only q16 and the exception list)."""
+    prepare(c)
+    c.pop("m8", None)
+    c.pop("e4", None)
+    return c
+
+
+def _matrix(c):
+    if "q16" not in c:
+        prepare(c)
+    t = c["q16"]
+    return Matrix(_ptr(t), _ptr(c["rp"]), _ptr(c["er"]), _ptr(c["ec"]), _ptr(c["ev"]),
+                  int(c["N"]), int(c["K"]), int(c["base"]), int(c["er"].numel()))
+
+
+def decode_rows(c, first, last, dtype=torch.float32):
+    """Rows [first, last) decoded exactly: float32 (as prefill_kernels.decode_rows)
+    or bfloat16 (the original bit patterns, NaN payloads included)."""
+    m = _matrix(c)
+    dev = c["q16"].device
+    out = torch.empty((last - first, int(c["K"])), dtype=dtype, device=dev)
+    f32 = 1 if dtype == torch.float32 else 0
+    if dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("dtype must be float32 or bfloat16")
+    check(lib().rv12_decode_rows(ctypes.byref(m), int(first), int(last), _ptr(out), f32, _stream(dev)),
+          "decode_rows")
+    return out
+
+
+def weight_rows(c, first, last):
+    """Exact float32 rows (prefill.py:23-42, compressed branch)."""
+    return decode_rows(c, first, last, torch.float32)
+
+
+def decompress(c):
+    """bf16[N, K] (wcomp.py:35-45).  Bit-identical to the weights compress()
+    saw; the reference's final `.bfloat16()` would additionally map every NaN
+    payload to one canonical NaN."""
+    return decode_rows(c, 0, int(c["N"]), torch.bfloat16)
+
+
+def _rb(BN):
+    if not BN:
+        return 0
+    return 1 if BN <= 16 else (2 if BN <= 32 else 4)
+
+
+def _sk_buf(N, S, dev, K=None, T=16):
+    """Workspace for split partial sums, cached per (N, device) (wcomp.py:226-230)."""
+    need = lib().rv12_workspace_bytes(int(N), int(K or 32 * max(S, 1)), int(T), int(S))
+    k = (N, str(dev))
+    if k not in _SK or _SK[k].numel() < need:
+        _SK[k] = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    return _SK[k]
+
+
+def _linear(x, c, y, mode, T, BN, w, S, lnw, eps, where):
+    _need_cuda(x, "x")
+    _need_cuda(y, "y")
+    if x.dtype != torch.float32 or y.dtype != torch.float32:
+        raise ValueError(f"{where}: x and y must be float32")
+    if not (x.is_contiguous() and y.is_contiguous()):
+        raise ValueError(f"{where}: x and y must be contiguous")
+    N, K = int(c["N"]), int(c["K"])
+    if BN is not None and N % BN:
+        raise ValueError("число строк не кратно BN (N is not a multiple of BN)")  # wcomp.py:123
+    xs = 2 * K if mode == 2 else K
+    if x.numel() < T * xs or y.numel() < T * N:
+        raise ValueError(f"{where}: x needs {T}x{xs} and y {T}x{N} floats")
+    if lnw is not None:
+        _need_cuda(lnw, "lnw")
+        if lnw.dtype != torch.bfloat16 or lnw.numel() < K or not lnw.is_contiguous():
+            raise ValueError(f"{where}: lnw must be a contiguous bf16 vector of K entries")
+    m = _matrix(c)
+    cfg = Launch(_rb(BN), int(w or 0), int(S or 0))
+    splits = int(S or 0)
+    ws = _sk_buf(N, splits, x.device, K, T)
+    rc = lib().rv12_gemm(ctypes.byref(m), _ptr(x), _ptr(y), int(T), _ptr(lnw), float(eps), int(mode),
+                         ctypes.byref(cfg), _ptr(ws), ws.numel(), _stream(x.device))
+    check(rc, where)
+
+
+def gemvc1(x, c, y, mode, BN=None, w=None, lnw=None, eps=1e-6):
+    """T = 1: y (=|+=) W x' with the MODE / RMS prologue (wcomp.py:67-126)."""
+    N, K = int(c["N"]), int(c["K"])
+    S = None
+    if BN is None:
+        cfg = CFG1.get((N, K, mode))
+        if cfg:
+            BN, w = cfg[0], cfg[1]
+            S = cfg[2] if len(cfg) > 2 else None
+    _linear(x, c, y, mode, 1, BN, w, S, lnw, eps, "gemvc1")
+
+
+def gemvc_tc(x, c, y, mode, T, BN=None, w=None, S=None):
+    """1 <= T <= 16 token rows: y[t] (=|+=) W x'[t] (wcomp.py:155-242)."""
+    N, K = int(c["N"]), int(c["K"])
+    if BN is None:
+        cfg = CFGT.get((N, K, mode))
+        if cfg:
+            BN, w, S = cfg
+    if not 1 <= int(T) <= 16:
+        raise ValueError("T must be in [1, 16]")
+    _linear(x, c, y, mode, int(T), BN, w, S, None, 1e-6, "gemvc_tc")

@@ -1,0 +1,133 @@
+/* rv12 — MI355X (gfx950) kernels for the 12-bit lossless bf16 decode-linear.
+ *
+ * C ABI of ai_amd/librv12.so.  Plain pointers and sizes only; every pointer
+ * named "device" is HIP device memory, and `stream` is a hipStream_t (NULL =
+ * the legacy default stream).  Every entry point validates its arguments on
+ * the host and returns a negative status before touching the GPU; a launch
+ * failure reported by hipGetLastError() returns RV12_E_LAUNCH.  No entry point
+ * allocates device memory or synchronises the stream: the caller owns every
+ * buffer (weights, activations, outputs, workspace), so the calls are
+ * reentrant and can be captured in a HIP graph.
+ *
+ * Each entry point replaces one piece of the reference operator API for the
+ * path; reference paths are relative to the reference repository root.
+ */
+#ifndef RV12_H
+#define RV12_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RV12_ABI_VERSION 1
+
+enum rv12_status {
+    RV12_OK = 0,
+    RV12_E_NULL = -1,      /* a required pointer is NULL */
+    RV12_E_SHAPE = -2,     /* N < 1, K < 32, K % 32, K % CH, CH % 16, or row range outside [0, N] */
+    RV12_E_MODE = -3,      /* mode not in {0, 1, 2} */
+    RV12_E_TOKENS = -4,    /* T not in [1, 16] */
+    RV12_E_WORKSPACE = -5, /* workspace smaller than rv12_workspace_bytes() */
+    RV12_E_CONFIG = -6,    /* launch configuration out of range */
+    RV12_E_BASE = -7,      /* base outside [0, 241] */
+    RV12_E_ALIGN = -8,     /* x, y or tiles not 16-byte aligned */
+    RV12_E_SIZE = -9,      /* output buffer smaller than rv12_tiles_bytes() */
+    RV12_E_LAUNCH = -20    /* hipGetLastError() after a launch */
+};
+
+/* The reference codec dict of one matrix W[N, K] (device pointers), as built
+ * by compress(): ramvi/engine/ramvi_engine/kernels/wcomp.py:13-32. */
+typedef struct rv12_codec {
+    const uint8_t* m8;  /* [N, K]   sign << 7 | mantissa */
+    const uint8_t* e4;  /* [N, K/2] per CH-chunk: byte i = code[i] | code[CH/2 + i] << 4 */
+    const int32_t* rp;  /* [N + 1]  exception row pointer */
+    const int32_t* er;  /* [E]      exception rows (row-major order) */
+    const int32_t* ec;  /* [E]      exception columns */
+    const float* ev;    /* [E]      exact exception values */
+    int32_t n, k, ch, base;
+    int64_t n_exc;
+} rv12_codec;
+
+/* A matrix re-tiled for the kernels (device pointers).  `tiles` holds the
+ * weights in the Q16 layout written by rv12_retile(); the exception arrays are
+ * the codec's own rp/er/ec/ev (shared, not copied). */
+typedef struct rv12_matrix {
+    const uint32_t* tiles;
+    const int32_t* rp;
+    const int32_t* er;
+    const int32_t* ec;
+    const float* ev;
+    int32_t n, k, base;
+    int64_t n_exc;
+} rv12_matrix;
+
+/* Launch shape of a linear: rows per workgroup (16 * rb, rb in {1, 2, 4}),
+ * waves per workgroup (1..4), K splits across workgroups (1..64).  A zero
+ * field (or a NULL pointer) selects the built-in choice for the shape. */
+typedef struct rv12_launch {
+    int32_t rb, waves, splits;
+} rv12_launch;
+
+/* ABI version of the library (RV12_ABI_VERSION).  Mirrors the reference's
+ * native ABI check, ramvi/engine/ramvi_engine/native/qmm.cpp:24. */
+int rv12_abi_version(void);
+
+/* Message for a status code. */
+const char* rv12_strerror(int status);
+
+/* Bytes of the Q16 tile layout for W[n, k]: ceil(n/16) * 16 * k * 3 / 2. */
+size_t rv12_tiles_bytes(int n, int k);
+
+/* Re-tile a codec dict into the Q16 layout.  Replaces nothing in the
+ * reference (its kernels read m8/e4 directly); called once per matrix after
+ * compress(), ramvi/engine/ramvi_engine/core/engine.py:224. */
+int rv12_retile(const rv12_codec* in, uint32_t* tiles, size_t tiles_bytes, void* stream);
+
+/* Encode a bf16 matrix W[n, k] (bits, row-major, device) into the codec dict
+ * in three calls, each a device pass with no host synchronisation:
+ *   rv12_encode_stats  hist[256] = exponent histogram (int32, device)
+ *   (host: base = first argmax of the 15-wide window sums of hist)
+ *   rv12_encode        m8[n, k], e4[n, k/2], row_exc[n] = exceptions per row
+ *   (host: rp = [0, cumsum(row_exc)], E = rp[n])
+ *   rv12_encode_exc    er/ec/ev[E] in row-major order
+ * Together they replace the tensor arithmetic of compress(),
+ * ramvi/engine/ramvi_engine/kernels/wcomp.py:13-32. */
+int rv12_encode_stats(const uint16_t* w, int n, int k, int32_t* hist, void* stream);
+int rv12_encode(const uint16_t* w, int n, int k, int ch, int base, uint8_t* m8, uint8_t* e4,
+                int32_t* row_exc, void* stream);
+int rv12_encode_exc(const uint16_t* w, int n, int k, int base, const int32_t* rp, int32_t* er, int32_t* ec,
+                    float* ev, void* stream);
+
+/* Workspace bytes a linear needs: splits * t * ceil(n/16)*16 partial sums and
+ * splits * t sums of squares (0 when splits == 1).  splits == 0 asks for the
+ * built-in choice for (n, k, t). */
+size_t rv12_workspace_bytes(int n, int k, int t, int splits);
+
+/* T = 1 fused decode + GEMV:  y (=|+=) W_dec . x'
+ *   mode 0: y = W x';  1: y += W x';  2: x' = silu(x[0:K]) * x[K:2K], y += W x'
+ *   lnw != NULL: x' = lnw * (x' * rsqrt(mean(x[0:K]^2) + eps))
+ * x: float[K] (float[2K] in mode 2), y: float[N], lnw: bf16 bits [K].
+ * Replaces gemvc1 / gemvc1_k, ramvi/engine/ramvi_engine/kernels/wcomp.py:67-126. */
+int rv12_gemv(const rv12_matrix* w, const float* x, float* y, const uint16_t* lnw, float eps, int mode,
+              const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream);
+
+/* 1 <= T <= 16 tokens:  y[t] (=|+=) W_dec . x'[t], rows of x are K floats apart
+ * (2K in mode 2), rows of y N floats apart.  lnw as in rv12_gemv (NULL in the
+ * reference's batched path).  Replaces gemvc_tc / gemvc_tc_k,
+ * ramvi/engine/ramvi_engine/kernels/wcomp.py:155-242. */
+int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps, int mode,
+              const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream);
+
+/* Bit-exact decode of rows [first, last) to bf16 bits (out_f32 == 0, out is
+ * uint16[last-first, K]) or to float32 (out_f32 != 0, out is float[last-first, K]).
+ * Replaces decode_rows / dequant_k TYPE 0 + exceptions_k,
+ * ramvi/engine/ramvi_engine/kernels/prefill_kernels.py:58-110. */
+int rv12_decode_rows(const rv12_matrix* w, int first, int last, void* out, int out_f32, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RV12_H */

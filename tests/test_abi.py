@@ -1,0 +1,120 @@
+"""C-ABI checks that need no GPU: librv12.so loads, exports every entry point
+include/rv12.h declares, and rejects bad arguments with the documented status
+before any device work (so none of these calls touches a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    src = open(os.path.join(ROOT, "include", "rv12.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(rv12_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_and_binding_agree():
+    from ai_amd import _lib
+    assert sorted(_lib.EXPORTS) == _header_functions()
+
+
+def test_library_exports_every_symbol():
+    from ai_amd import _lib
+    L = _lib.lib()
+    for name in _header_functions():
+        assert hasattr(L, name), name
+
+
+def test_abi_version_and_strerror():
+    from ai_amd import _lib
+    L = _lib.lib()
+    assert L.rv12_abi_version() == 1
+    for s in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -20):
+        assert _lib.strerror(s) and _lib.strerror(s) != "unknown rv12 status"
+    assert _lib.strerror(-99) == "unknown rv12 status"
+
+
+def test_sizes():
+    from ai_amd import _lib
+    L = _lib.lib()
+    assert L.rv12_tiles_bytes(4096, 4096) == 4096 * 4096 * 3 // 2
+    assert L.rv12_tiles_bytes(17, 256) == 32 * 256 * 3 // 2
+    assert L.rv12_tiles_bytes(16, 100) == 0
+    assert L.rv12_workspace_bytes(4096, 4096, 1, 1) == 0
+    assert L.rv12_workspace_bytes(4096, 4096, 2, 4) == 4 * (4 * 2 * 4096 + 4 * 2)
+    assert L.rv12_workspace_bytes(4096, 4096, 17, 1) == 0
+
+
+def _mat(n=64, k=256, base=100, tiles=0x1000, n_exc=0):
+    from ai_amd import _lib
+    return _lib.Matrix(tiles, 0x2000, 0x3000 if n_exc else 0, 0x4000 if n_exc else 0, 0x5000 if n_exc else 0,
+                       n, k, base, n_exc)
+
+
+def test_gemm_argument_errors():
+    """Every case returns before any device work (the pointers are fake)."""
+    from ai_amd import _lib
+    L = _lib.lib()
+    x, y, ws = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x20000), ctypes.c_void_p(0x30000)
+
+    def call(m, t=1, mode=0, cfg=None, lnw=None, xx=x, yy=y, wsb=0):
+        return L.rv12_gemm(ctypes.byref(m) if m is not None else None, xx, yy, t, lnw, 1e-6, mode,
+                           ctypes.byref(cfg) if cfg else None, ws, wsb, None)
+
+    assert call(None) == _lib.RV12_E_NULL
+    assert call(_mat(tiles=0)) == _lib.RV12_E_NULL
+    assert call(_mat(), xx=None) == _lib.RV12_E_NULL
+    assert call(_mat(k=100)) == _lib.RV12_E_SHAPE
+    assert call(_mat(n=0)) == _lib.RV12_E_SHAPE
+    assert call(_mat(base=242)) == _lib.RV12_E_BASE
+    assert call(_mat(), mode=3) == _lib.RV12_E_MODE
+    assert call(_mat(), t=0) == _lib.RV12_E_TOKENS
+    assert call(_mat(), t=17) == _lib.RV12_E_TOKENS
+    assert call(_mat(tiles=0x1004)) == _lib.RV12_E_ALIGN
+    assert call(_mat(), xx=ctypes.c_void_p(0x10004)) == _lib.RV12_E_ALIGN
+    assert call(_mat(), cfg=_lib.Launch(3, 4, 1)) == _lib.RV12_E_CONFIG
+    assert call(_mat(), cfg=_lib.Launch(1, 5, 1)) == _lib.RV12_E_CONFIG
+    assert call(_mat(), cfg=_lib.Launch(1, 4, 65)) == _lib.RV12_E_CONFIG
+    assert call(_mat(k=256), cfg=_lib.Launch(1, 4, 9)) == _lib.RV12_E_CONFIG  # more splits than K steps
+    # a split launch needs a workspace of rv12_workspace_bytes()
+    need = L.rv12_workspace_bytes(64, 256, 1, 2)
+    assert call(_mat(), cfg=_lib.Launch(1, 4, 2), wsb=need - 4) == _lib.RV12_E_WORKSPACE
+    # exceptions declared without their arrays
+    m = _mat(n_exc=5)
+    m.er = 0
+    assert call(m) == _lib.RV12_E_NULL
+
+
+def test_retile_decode_encode_argument_errors():
+    from ai_amd import _lib
+    L = _lib.lib()
+    cod = _lib.Codec(0x1000, 0x2000, 0x3000, 0, 0, 0, 64, 256, 256, 100, 0)
+    need = L.rv12_tiles_bytes(64, 256)
+    assert L.rv12_retile(None, ctypes.c_void_p(0x9000), need, None) == _lib.RV12_E_NULL
+    assert L.rv12_retile(ctypes.byref(cod), None, need, None) == _lib.RV12_E_NULL
+    assert L.rv12_retile(ctypes.byref(cod), ctypes.c_void_p(0x9000), need - 1, None) == _lib.RV12_E_SIZE
+    bad = _lib.Codec(0x1000, 0x2000, 0x3000, 0, 0, 0, 64, 256, 24, 100, 0)
+    assert L.rv12_retile(ctypes.byref(bad), ctypes.c_void_p(0x9000), need, None) == _lib.RV12_E_SHAPE
+    bad = _lib.Codec(0x1000, 0x2000, 0x3000, 0, 0, 0, 64, 256, 256, 300, 0)
+    assert L.rv12_retile(ctypes.byref(bad), ctypes.c_void_p(0x9000), need, None) == _lib.RV12_E_BASE
+    m = _mat()
+    out = ctypes.c_void_p(0x40000)
+    assert L.rv12_decode_rows(ctypes.byref(m), 5, 3, out, 0, None) == _lib.RV12_E_SHAPE
+    assert L.rv12_decode_rows(ctypes.byref(m), 0, 65, out, 0, None) == _lib.RV12_E_SHAPE
+    assert L.rv12_decode_rows(ctypes.byref(m), 0, 4, None, 0, None) == _lib.RV12_E_NULL
+    assert L.rv12_decode_rows(ctypes.byref(m), 3, 3, out, 0, None) == _lib.RV12_OK  # empty range: no work
+    assert L.rv12_encode_stats(None, 4, 4, ctypes.c_void_p(0x1000), None) == _lib.RV12_E_NULL
+    assert L.rv12_encode(ctypes.c_void_p(0x1000), 4, 256, 256, 250, ctypes.c_void_p(0x2000),
+                         ctypes.c_void_p(0x3000), ctypes.c_void_p(0x4000), None) == _lib.RV12_E_BASE
+    assert L.rv12_encode(ctypes.c_void_p(0x1000), 4, 250, 256, 10, ctypes.c_void_p(0x2000),
+                         ctypes.c_void_p(0x3000), ctypes.c_void_p(0x4000), None) == _lib.RV12_E_SHAPE
+
+
+def test_python_mirror_rejects_cpu_tensors():
+    import torch
+    from ai_amd import wcomp
+    with pytest.raises(ValueError):
+        wcomp.compress(torch.zeros(4, 256, dtype=torch.bfloat16))

@@ -1,0 +1,166 @@
+"""GPU parity of the fused decode-linear (gemvc1 / gemvc_tc through librv12.so)
+against the oracle's closed form.
+
+Bar (north star): |y - y_ref| <= 1e-3 + 1e-2 |y_ref| in every output.  Each
+case is also held to the fp32 forward-error bound of the oracle
+(oracle.linear.error_bound: (K + 8) 2^-24 sum_k |w_k x'_k|), which a dropped
+exception, a wrong exponent or a transposed operand would break."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import ref_dict
+from oracle import codec, cref, linear
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-2, 1e-3
+
+
+def _close(y, ref, bound, what):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isnan(y), np.isnan(ref)), what
+    assert np.array_equal(y[np.isinf(ref)], ref[np.isinf(ref)]), what
+    err = np.abs(y[fin] - ref[fin])
+    assert np.all(err <= ATOL + RTOL * np.abs(ref[fin])), (what, float(err.max()))
+    tight = 4 * bound[fin] + 1e-30
+    bad = err > tight
+    assert not bad.any(), (what, float(err[bad].max()), float(tight[bad].min()))
+
+
+def _inputs(c, T, mode, seed, rms):
+    rng = np.random.default_rng(seed)
+    K, N = c["K"], c["N"]
+    xs = 2 * K if mode == 2 else K
+    X = rng.standard_normal((T, xs)).astype(np.float32)
+    Y0 = rng.standard_normal((T, N)).astype(np.float32)
+    lnw = None
+    if rms:
+        lnw = codec.f32_to_bf16_rne((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    return X, Y0, lnw
+
+
+def _run(c_gpu, X, Y0, mode, T, lnw=None, BN=None, w=None, S=None, eps=1e-6, use_tc=False):
+    from ai_amd import wcomp
+    x = torch.from_numpy(X).cuda()
+    y = torch.from_numpy(Y0.copy()).cuda()
+    ln = None if lnw is None else torch.from_numpy(lnw.view(np.int16).copy()).view(torch.bfloat16).cuda()
+    if T == 1 and not use_tc:
+        wcomp.gemvc1(x, c_gpu, y, mode, BN=BN, w=w, lnw=ln, eps=eps)
+    else:
+        assert ln is None
+        wcomp.gemvc_tc(x, c_gpu, y, mode, T, BN=BN, w=w, S=S)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def _check(cnp, c_gpu, T, mode, rms, seed, **kw):
+    X, Y0, lnw = _inputs(cnp, T, mode, seed, rms)
+    W = codec.decode_f32(cnp).astype(np.float64)
+    lw = None if lnw is None else codec.bf16_to_f32(lnw)
+    ref = linear.linear(cnp, X, mode, Y0, lnw=lw, W=W)
+    bound = linear.error_bound(cnp, X, mode, lnw=lw, W=W)
+    y = _run(c_gpu, X, Y0, mode, T, lnw=lnw, **kw)
+    _close(y, ref, bound, (T, mode, rms, seed, kw))
+
+
+@pytest.mark.parametrize("case", ["prefill_seed7", "special_values", "outliers_rows_cols", "chunk128",
+                                  "tie_spread", "subnormal_heavy"])
+def test_golden_matrices_all_modes(golden, case):
+    from ai_amd import wcomp
+    print("case", case, flush=True)
+    cnp = ref_dict(golden[case])
+    cg = wcomp.prepare(ref_dict(golden[case]))
+    for mode in (0, 1, 2):
+        for rms in (False, True):
+            _check(cnp, cg, 1, mode, rms, 3)
+        for T in (2, 5, 16):
+            _check(cnp, cg, T, mode, False, 4 + T, use_tc=True)
+
+
+def _random_matrix(N, K, seed, sigma=0.02, out_rows=0.0, out_cols=0.0):
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((N, K)).astype(np.float32) * sigma
+    if out_rows:
+        w[rng.choice(N, max(1, int(N * out_rows)), replace=False)] *= 20
+    if out_cols:
+        w[:, rng.choice(K, max(1, int(K * out_cols)), replace=False)] *= 20
+    return codec.f32_to_bf16_rne(w)
+
+
+@pytest.mark.parametrize("N,K", [(1, 256), (15, 256), (16, 512), (33, 1024), (100, 768), (1000, 2048)])
+def test_shapes_and_launch_shapes(N, K):
+    from ai_amd import wcomp
+    print("shape", N, K, flush=True)
+    bits = _random_matrix(N, K, N + K, out_rows=0.01, out_cols=0.01)
+    cnp = codec.compress(bits)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    nsteps = K // 32
+    for BN, w, S in ((16, 1, 1), (16, 4, 1), (32, 2, 2), (64, 4, 1), (16, 3, min(5, nsteps)), (16, 4, nsteps)):
+        if N % BN:
+            continue
+        for mode in (0, 2):
+            _check(cnp, cg, 1, mode, mode == 0, 7, BN=BN, w=w)
+            _check(cnp, cg, 4, mode, False, 8, BN=BN, w=w, S=S, use_tc=True)
+
+
+def test_bn_must_divide_rows():
+    from ai_amd import wcomp
+    bits = _random_matrix(24, 256, 1)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    x = torch.zeros(256, device="cuda")
+    y = torch.zeros(24, device="cuda")
+    with pytest.raises(ValueError):
+        wcomp.gemvc1(x, cg, y, 0, BN=16, w=4)
+    with pytest.raises(ValueError):
+        wcomp.gemvc_tc(x, cg, y, 0, 1, BN=16, w=4, S=1)
+    with pytest.raises(ValueError):
+        wcomp.gemvc1(x, cg, y, 3)
+    with pytest.raises(ValueError):
+        wcomp.gemvc_tc(x, cg, y, 0, 17)
+
+
+QWEN3_8B = [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288), (6144, 4096), (24576, 4096)]
+
+
+@pytest.mark.parametrize("N,K", QWEN3_8B)
+def test_qwen3_8b_shapes_full_size(N, K):
+    """Config-2 matrices (sigma ~ U(0.01, 0.05), 0.1% outlier rows x20) at full
+    size against the C oracle, modes 0/1/2 and RMS, T = 1 and 8."""
+    from ai_amd import wcomp
+    print("shape", N, K, flush=True)
+    rng = np.random.default_rng(N * 7 + K)
+    sigma = float(rng.uniform(0.01, 0.05))
+    bits = _random_matrix(N, K, N + 3 * K, sigma=sigma, out_rows=0.001)
+    cnp = cref.compress(bits)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    assert cg["base"] == cnp["base"] and cg["er"].numel() == cnp["er"].size
+    for T, mode, rms in ((1, 0, True), (1, 1, False), (1, 2, False), (8, 0, False), (8, 2, False)):
+        X, Y0, lnw = _inputs(cnp, T, mode, 5 + T + mode, rms)
+        ref = Y0.copy()
+        cref.gemv_12bit(cnp, X, ref, mode, lnw=lnw)
+        y = _run(cg, X, Y0, mode, T, lnw=lnw, use_tc=T > 1)
+        err = np.abs(y.astype(np.float64) - ref)
+        assert np.all(err <= ATOL + RTOL * np.abs(ref)), (N, K, T, mode, rms, float(err.max()))
+        # both sides are fp32 sums of the same exact products: agree to ~1e-5
+        assert float((err / (np.abs(ref) + 1.0)).max()) < 1e-4, (N, K, T, mode, float(err.max()))
+
+
+def test_lm_head_full_size():
+    """151936 x 4096 (the lm_head) at M=1 against the C oracle."""
+    from ai_amd import wcomp
+    N, K = 151936, 4096
+    bits = _random_matrix(N, K, 99, sigma=0.02, out_rows=0.001)
+    cnp = cref.compress(bits)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    X, Y0, _ = _inputs(cnp, 1, 0, 1, False)
+    ref = np.zeros((1, N), np.float32)
+    cref.gemv_12bit(cnp, X, ref, 0)
+    y = _run(cg, X, Y0, 0, 1)
+    err = np.abs(y.astype(np.float64) - ref)
+    assert np.all(err <= ATOL + RTOL * np.abs(ref)), float(err.max())
+    assert float((err / (np.abs(ref) + 1.0)).max()) < 1e-4
+    del cg
+    torch.cuda.empty_cache()
