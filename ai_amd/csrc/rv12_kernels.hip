@@ -316,7 +316,12 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
     // issued unconditionally at a clamped step so no load sits under a branch
     const int wu = __builtin_amdgcn_readfirstlane(wave);
     const uint32_t* tb = p.tiles + (blk0 * nsteps) * 192;
-    const int64_t bstride = (int64_t)nsteps * 192;
+    // row blocks past the last one (grid rounded up to RB) re-read the last
+    // block; their rows are >= N and are never stored
+    const int64_t nblk = (p.N + 15) / 16;
+    int64_t bofs[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) bofs[b] = (min(blk0 + b, nblk - 1) - blk0) * (int64_t)nsteps * 192;
     const int lo3 = lane * 3;
     uint32_t buf[kDepth][RB][3];
     const int s0 = s_lo + wu;
@@ -326,7 +331,7 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
         const int s = min(s0 + u * W, slast);
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
-            const uint32_t* g = tb + b * bstride + (int64_t)s * 192 + lo3;
+            const uint32_t* g = tb + bofs[b] + (int64_t)s * 192 + lo3;
             buf[u][b][0] = __builtin_nontemporal_load(g);
             buf[u][b][1] = __builtin_nontemporal_load(g + 1);
             buf[u][b][2] = __builtin_nontemporal_load(g + 2);
@@ -346,7 +351,7 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
             const int sn = min(s + kDepth * W, slast);
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
-                const uint32_t* g = tb + b * bstride + (int64_t)sn * 192 + lo3;
+                const uint32_t* g = tb + bofs[b] + (int64_t)sn * 192 + lo3;
                 buf[u][b][0] = __builtin_nontemporal_load(g);
                 buf[u][b][1] = __builtin_nontemporal_load(g + 1);
                 buf[u][b][2] = __builtin_nontemporal_load(g + 2);
