@@ -183,10 +183,10 @@ int rv12_gemv(const rv12_matrix* w, const float* x, float* y, const uint16_t* ln
 int rv12_decode_rows(const rv12_matrix* w, int first, int last, void* out, int out_f32, void* stream) {
     int rc = check_matrix(w);
     if (rc) return rc;
-    if (!out) return RV12_E_NULL;
     if (first < 0 || last > w->n || first > last) return RV12_E_SHAPE;
+    if (first == last) return RV12_OK;  // nothing to write: out may be NULL
+    if (!out) return RV12_E_NULL;
     if (!aligned16(out)) return RV12_E_ALIGN;
-    if (first == last) return RV12_OK;
     launch_decode(*w, first, last, out, out_f32, (hipStream_t)stream, 0, w->n_exc);
     return launch_status();
 }

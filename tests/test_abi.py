@@ -105,6 +105,7 @@ def test_retile_decode_encode_argument_errors():
     assert L.rv12_decode_rows(ctypes.byref(m), 5, 3, out, 0, None) == _lib.RV12_E_SHAPE
     assert L.rv12_decode_rows(ctypes.byref(m), 0, 65, out, 0, None) == _lib.RV12_E_SHAPE
     assert L.rv12_decode_rows(ctypes.byref(m), 0, 4, None, 0, None) == _lib.RV12_E_NULL
+    assert L.rv12_decode_rows(ctypes.byref(m), 2, 2, None, 0, None) == _lib.RV12_OK
     assert L.rv12_decode_rows(ctypes.byref(m), 3, 3, out, 0, None) == _lib.RV12_OK  # empty range: no work
     assert L.rv12_encode_stats(None, 4, 4, ctypes.c_void_p(0x1000), None) == _lib.RV12_E_NULL
     assert L.rv12_encode(ctypes.c_void_p(0x1000), 4, 256, 256, 250, ctypes.c_void_p(0x2000),
