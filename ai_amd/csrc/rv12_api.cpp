@@ -17,16 +17,20 @@ int launch_status() { return hipGetLastError() == hipSuccess ? RV12_OK : RV12_E_
 
 int64_t nblocks(int n) { return ((int64_t)n + 15) / 16; }
 
-// Built-in launch shape for (N, K, T): enough workgroups to cover 256 CUs a
-// few times over, K split only when the row blocks alone are too few.
+// Built-in launch shape for (N, K, T), from a sweep over the Qwen3-8B shapes
+// on MI355X: one workgroup per 16 (or 32) rows and the whole of K, no K split
+// unless the LDS copy of x' would not fit; 16 waves while there are at most
+// two row blocks per CU (each wave then has <= 16 K steps, its whole load
+// pipeline in flight), 8 waves up to 4096 row blocks, beyond that 32 rows and
+// 4 waves per workgroup.
 void default_launch(int N, int K, int T, int* rb, int* waves, int* splits) {
     const int64_t nblk = nblocks(N);
     const int nsteps = K / 32;
     *rb = (nblk >= 4096 && T <= 2) ? 2 : 1;
-    *waves = nsteps >= 16 ? 4 : (nsteps >= 8 ? 2 : 1);
-    const int64_t wgs = (nblk + *rb - 1) / *rb;
+    int w = nblk <= 512 ? 16 : (nblk < 4096 ? 8 : 4);
+    while (w > 1 && nsteps / w < 2) w >>= 1;
+    *waves = w;
     int s = 1;
-    while (wgs * s < 1024 && s * 2 <= kMaxSplits && nsteps / (s * 2) >= *waves * 4) s *= 2;
     while (s < kMaxSplits && s < nsteps && linear_lds_bytes(K, T, *rb, *waves, s) > kMaxLds) ++s;
     *splits = s;
 }

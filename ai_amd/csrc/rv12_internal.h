@@ -24,14 +24,14 @@ struct LinearParams {
 };
 
 constexpr int kMaxSplits = 64;
-constexpr int kMaxWaves = 4;
+constexpr int kMaxWaves = 16;
 constexpr size_t kMaxLds = 65536;
 
 // LDS bytes of k_linear for a launch shape (largest split)
 inline size_t linear_lds_bytes(int K, int T, int rb, int waves, int splits) {
     const int nsteps = K / 32;
     const size_t krange = (size_t)((nsteps + splits - 1) / splits) * 32;
-    return 4 * ((size_t)T * krange + (size_t)waves * rb * T * 16 + (size_t)rb * 16 * T + (size_t)waves * T);
+    return 4 * ((size_t)T * krange + (size_t)waves * rb * T * 16 + (size_t)waves * rb * 16 * T + (size_t)waves * T);
 }
 
 int launch_linear(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st);

@@ -240,23 +240,44 @@ __global__ __launch_bounds__(256) void k_decode_exc(const int32_t* __restrict__ 
 }
 
 // ------------------------------------------------------------------ linear
-// Workgroup = `waves` waves over 16*RB rows and the K steps [s_lo, s_hi) of
-// split blockIdx.y.  Prologue: x'[t][k] for the split's K range into LDS
-// (MODE / RMS transform, sum of squares for RMS).  Main loop: wave w takes
-// steps s_lo + w, s_lo + w + waves, ...; each lane keeps `kDepth` steps of
-// weights in flight, decodes 8 weights per row block and step and does 8 FMAs
-// per token into fp32 accumulators.  Epilogue: lane quarters and waves are
-// summed in a fixed order (no atomics), the sum is rescaled by 2^(base-1),
-// the exceptions of the workgroup's rows whose column falls in the split are
-// added (segmented scan in wave 0), then the result is stored (one split) or
-// written as a partial for k_splitk_reduce.
-constexpr int kDepth = 4;
+// Workgroup = `waves` waves (1..16) over 16*RB rows and the K steps
+// [s_lo, s_hi) of split blockIdx.y.  Order of work, chosen so that every
+// long-latency load is in flight before anything waits on it:
+//   1. each wave issues the loads of its first kDepth steps of weights;
+//   2. every wave fetches its 64-entry slice of the first round of the
+//      workgroup's exceptions (row, column, value; a round is waves * 64
+//      entries of the row-major exception list);
+//   3. all threads stage x'[t][k] for the split's K range in LDS (MODE / RMS
+//      transform, sum of squares for RMS), then one barrier;
+//   4. main loop: wave w takes steps s_lo + w, s_lo + w + waves, ...; per step
+//      it decodes 8 weights per row block and does 8 FMAs per token into fp32
+//      accumulators while the load kDepth steps ahead is in flight;
+//   5. epilogue: lane quarters and waves are summed in a fixed order (no
+//      atomics), rescaled by 2^(base-1); the exceptions whose column lies in
+//      the split are added (per wave a segmented scan over its slice, per-wave
+//      LDS sums added in wave order); the result is stored (one split) or
+//      written as a partial for k_splitk_reduce.
+constexpr int kDepth = 8;
+constexpr int kMaxThreads = 1024;
+
+template <int RB>
+__device__ __forceinline__ void load_step(uint32_t (&dst)[RB][3], const uint32_t* tb, const int64_t (&bofs)[RB],
+                                          int s, int lo3) {
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+        const uint32_t* g = tb + bofs[b] + (int64_t)s * 192 + lo3;
+        dst[b][0] = __builtin_nontemporal_load(g);
+        dst[b][1] = __builtin_nontemporal_load(g + 1);
+        dst[b][2] = __builtin_nontemporal_load(g + 2);
+    }
+}
 
 template <int T, int RB>
-__global__ __launch_bounds__(256) void k_linear(LinearParams p) {
+__global__ __launch_bounds__(kMaxThreads) void k_linear(LinearParams p) {
     extern __shared__ float smem[];
     const int W = blockDim.x >> 6;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
+    const int wu = __builtin_amdgcn_readfirstlane(wave);
     const int S = gridDim.y, sp = blockIdx.y;
     const int nsteps = p.K >> 5;
     const int s_lo = (int)((int64_t)sp * nsteps / S), s_hi = (int)((int64_t)(sp + 1) * nsteps / S);
@@ -266,10 +287,42 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
 
     float* xl = smem;                        // [T][krange]
     float* red = xl + T * krange;            // [W][RB][T][16]
-    float* exc = red + W * RB * T * 16;      // [RB*16][T]
-    float* ssq = exc + RB * 16 * T;          // [W][T]
+    float* exc = red + W * RB * T * 16;      // [W][RB*16][T] per-wave exception sums
+    float* ssq = exc + W * RB * 16 * T;      // [W][T]
 
-    // ---- prologue: x' into LDS
+    // ---- 1. first kDepth steps of weights
+    // wave-uniform step indices (scalar branches); loads are issued
+    // unconditionally at a clamped step so no load sits under a branch.
+    // Row blocks past the last one (grid rounded up to RB) re-read the last
+    // block; their rows are >= N and are never stored.
+    const uint32_t* tb = p.tiles + (blk0 * nsteps) * 192;
+    const int64_t nblk = (p.N + 15) / 16;
+    int64_t bofs[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) bofs[b] = (min(blk0 + b, nblk - 1) - blk0) * (int64_t)nsteps * 192;
+    const int lo3 = lane * 3;
+    const int s0 = s_lo + wu;
+    const int slast = s_hi - 1;
+    uint32_t buf[kDepth][RB][3];
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) load_step<RB>(buf[u], tb, bofs, min(s0 + u * W, slast), lo3);
+
+    // ---- 2. exception range and this wave's slice of the first round
+    int32_t e_lo = 0, e_hi = 0;
+    int er0 = 0x7FFFFFFF, ec0 = 0;
+    float ev0 = 0.0f;
+    if (p.n_exc > 0) {
+        e_lo = p.rp[n0];
+        e_hi = p.rp[min(n0 + RB * 16, p.N)];
+        const int32_t j = e_lo + wu * 64 + lane;
+        if (j < e_hi) {
+            er0 = p.er[j] - n0;
+            ec0 = p.ec[j];
+            ev0 = p.ev[j];
+        }
+    }
+
+    // ---- 3. x' into LDS
     float sq[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) sq[t] = 0.0f;
@@ -294,7 +347,7 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
             *reinterpret_cast<float4*>(xl + t * krange + i) = v;
         }
     }
-    for (int i = threadIdx.x; i < RB * 16 * T; i += blockDim.x) exc[i] = 0.0f;
+    for (int i = threadIdx.x; i < W * RB * 16 * T; i += blockDim.x) exc[i] = 0.0f;
     if (p.lnw) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
@@ -305,38 +358,13 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
     }
     __syncthreads();
 
-    // ---- main loop
+    // ---- 4. main loop
     float acc[RB][T];
 #pragma unroll
     for (int b = 0; b < RB; ++b)
 #pragma unroll
         for (int t = 0; t < T; ++t) acc[b][t] = 0.0f;
 
-    // wave-uniform step indices (scalar branches, scalar addresses); loads are
-    // issued unconditionally at a clamped step so no load sits under a branch
-    const int wu = __builtin_amdgcn_readfirstlane(wave);
-    const uint32_t* tb = p.tiles + (blk0 * nsteps) * 192;
-    // row blocks past the last one (grid rounded up to RB) re-read the last
-    // block; their rows are >= N and are never stored
-    const int64_t nblk = (p.N + 15) / 16;
-    int64_t bofs[RB];
-#pragma unroll
-    for (int b = 0; b < RB; ++b) bofs[b] = (min(blk0 + b, nblk - 1) - blk0) * (int64_t)nsteps * 192;
-    const int lo3 = lane * 3;
-    uint32_t buf[kDepth][RB][3];
-    const int s0 = s_lo + wu;
-    const int slast = s_hi - 1;
-#pragma unroll
-    for (int u = 0; u < kDepth; ++u) {
-        const int s = min(s0 + u * W, slast);
-#pragma unroll
-        for (int b = 0; b < RB; ++b) {
-            const uint32_t* g = tb + bofs[b] + (int64_t)s * 192 + lo3;
-            buf[u][b][0] = __builtin_nontemporal_load(g);
-            buf[u][b][1] = __builtin_nontemporal_load(g + 1);
-            buf[u][b][2] = __builtin_nontemporal_load(g + 2);
-        }
-    }
     for (int sb = s0; sb < s_hi; sb += kDepth * W) {
 #pragma unroll
         for (int u = 0; u < kDepth; ++u) {
@@ -348,14 +376,7 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
                 cur[b][1] = buf[u][b][1];
                 cur[b][2] = buf[u][b][2];
             }
-            const int sn = min(s + kDepth * W, slast);
-#pragma unroll
-            for (int b = 0; b < RB; ++b) {
-                const uint32_t* g = tb + bofs[b] + (int64_t)sn * 192 + lo3;
-                buf[u][b][0] = __builtin_nontemporal_load(g);
-                buf[u][b][1] = __builtin_nontemporal_load(g + 1);
-                buf[u][b][2] = __builtin_nontemporal_load(g + 2);
-            }
+            load_step<RB>(buf[u], tb, bofs, min(s + kDepth * W, slast), lo3);
             if (s < s_hi) {
                 uint32_t pr[RB][4];
 #pragma unroll
@@ -383,7 +404,7 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
         }
     }
 
-    // ---- epilogue: lane quarters, then waves
+    // ---- 5. epilogue: lane quarters, then waves
 #pragma unroll
     for (int b = 0; b < RB; ++b)
 #pragma unroll
@@ -394,26 +415,29 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
             if (lane < 16) red[((wave * RB + b) * T + t) * 16 + lane] = v;
         }
 
-    // exceptions of this workgroup's rows with a column inside the split (wave 0)
-    if (wave == 0 && p.n_exc > 0) {
-        const int n1 = min(n0 + RB * 16, p.N);
-        const int32_t e_lo = p.rp[n0], e_hi = p.rp[n1];
-        for (int32_t j0 = e_lo; j0 < e_hi; j0 += 64) {
-            const int32_t j = j0 + lane;
-            const bool valid = j < e_hi;
-            int r = 0x7FFFFFFF;
+    // exceptions of this workgroup's rows with a column inside the split:
+    // rounds of waves*64 entries, wave w takes entries [w*64, w*64+64) of each
+    float* excw = exc + wave * RB * 16 * T;
+    for (int32_t j0 = e_lo; j0 < e_hi; j0 += W * 64) {
+        const int32_t j = j0 + wu * 64 + lane;
+        const bool valid = j < e_hi;
+        int r = 0x7FFFFFFF, c = 0;
+        float v = 0.0f;
+        if (j0 == e_lo) {
+            r = er0;
+            c = ec0;
+            v = ev0;
+        } else if (valid) {
+            r = p.er[j] - n0;
+            c = p.ec[j];
+            v = p.ev[j];
+        }
+        if (__builtin_amdgcn_readfirstlane(j0 + wu * 64) < e_hi) {  // this wave has entries
             float pv[T];
+            c -= k_lo;
+            const bool in = valid && c >= 0 && c < krange;
 #pragma unroll
-            for (int t = 0; t < T; ++t) pv[t] = 0.0f;
-            if (valid) {
-                r = p.er[j] - n0;
-                const int c = p.ec[j] - k_lo;
-                if (c >= 0 && c < krange) {
-                    const float v = p.ev[j];
-#pragma unroll
-                    for (int t = 0; t < T; ++t) pv[t] = v * xl[t * krange + c];
-                }
-            }
+            for (int t = 0; t < T; ++t) pv[t] = in ? v * xl[t * krange + c] : 0.0f;
             for (int d = 1; d < 64; d <<= 1) {
                 const int rn = __shfl_up(r, d);
 #pragma unroll
@@ -425,7 +449,7 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
             const int rnext = __shfl_down(r, 1);
             if (valid && (lane == 63 || rnext != r)) {
 #pragma unroll
-                for (int t = 0; t < T; ++t) exc[r * T + t] += pv[t];
+                for (int t = 0; t < T; ++t) excw[r * T + t] += pv[t];
             }
         }
     }
@@ -447,7 +471,9 @@ __global__ __launch_bounds__(256) void k_linear(LinearParams p) {
         const int b = r >> 4, l16 = r & 15;
         float v = 0.0f;
         for (int w = 0; w < W; ++w) v += red[((w * RB + b) * T + t) * 16 + l16];
-        v = ldexpf(v, p.base - 1) + exc[r * T + t];
+        float e = 0.0f;
+        for (int w = 0; w < W; ++w) e += exc[(w * RB * 16 + r) * T + t];
+        v = ldexpf(v, p.base - 1) + e;
         const int n = n0 + r;
         if (n < p.N) {
             if (S == 1) {

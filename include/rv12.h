@@ -65,7 +65,7 @@ typedef struct rv12_matrix {
 } rv12_matrix;
 
 /* Launch shape of a linear: rows per workgroup (16 * rb, rb in {1, 2, 4}),
- * waves per workgroup (1..4), K splits across workgroups (1..64).  A zero
+ * waves per workgroup (1..16), K splits across workgroups (1..64).  A zero
  * field (or a NULL pointer) selects the built-in choice for the shape. */
 typedef struct rv12_launch {
     int32_t rb, waves, splits;

@@ -76,7 +76,7 @@ def test_gemm_argument_errors():
     assert call(_mat(tiles=0x1004)) == _lib.RV12_E_ALIGN
     assert call(_mat(), xx=ctypes.c_void_p(0x10004)) == _lib.RV12_E_ALIGN
     assert call(_mat(), cfg=_lib.Launch(3, 4, 1)) == _lib.RV12_E_CONFIG
-    assert call(_mat(), cfg=_lib.Launch(1, 5, 1)) == _lib.RV12_E_CONFIG
+    assert call(_mat(), cfg=_lib.Launch(1, 17, 1)) == _lib.RV12_E_CONFIG
     assert call(_mat(), cfg=_lib.Launch(1, 4, 65)) == _lib.RV12_E_CONFIG
     assert call(_mat(k=256), cfg=_lib.Launch(1, 4, 9)) == _lib.RV12_E_CONFIG  # more splits than K steps
     # a split launch needs a workspace of rv12_workspace_bytes()
