@@ -22,7 +22,7 @@ RV12_E_LAUNCH = -20
 EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_retile", "rv12_encode_stats",
            "rv12_encode", "rv12_encode_exc", "rv12_workspace_bytes", "rv12_gemv", "rv12_gemm",
            "rv12_decode_rows")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class Codec(ctypes.Structure):
@@ -39,7 +39,11 @@ class Matrix(ctypes.Structure):
 
 
 class Launch(ctypes.Structure):
-    _fields_ = [("rb", ctypes.c_int32), ("waves", ctypes.c_int32), ("splits", ctypes.c_int32)]
+    _fields_ = [("kernel", ctypes.c_int32), ("rb", ctypes.c_int32), ("waves", ctypes.c_int32),
+                ("splits", ctypes.c_int32)]
+
+
+KERNEL_VECTOR, KERNEL_MFMA = 1, 2
 
 
 class Rv12Error(RuntimeError):

@@ -7,6 +7,8 @@
 #include "rv12.h"
 #include "rv12_internal.h"
 
+#include <algorithm>
+
 using namespace rv12;
 
 namespace {
@@ -17,40 +19,76 @@ int launch_status() { return hipGetLastError() == hipSuccess ? RV12_OK : RV12_E_
 
 int64_t nblocks(int n) { return ((int64_t)n + 15) / 16; }
 
-// Built-in launch shape for (N, K, T), from a sweep over the Qwen3-8B shapes
-// on MI355X: one workgroup per 16 (or 32) rows and the whole of K, no K split
-// unless the LDS copy of x' would not fit; 16 waves while there are at most
-// two row blocks per CU (each wave then has <= 16 K steps, its whole load
-// pipeline in flight), 8 waves up to 4096 row blocks, beyond that 32 rows and
-// 4 waves per workgroup.
-void default_launch(int N, int K, int T, int* rb, int* waves, int* splits) {
-    const int64_t nblk = nblocks(N);
-    const int nsteps = K / 32;
-    *rb = (nblk >= 4096 && T <= 2) ? 2 : 1;
-    int w = nblk <= 512 ? 16 : (nblk < 4096 ? 8 : 4);
-    while (w > 1 && nsteps / w < 2) w >>= 1;
-    *waves = w;
-    int s = 1;
-    while (s < kMaxSplits && s < nsteps && linear_lds_bytes(K, T, *rb, *waves, s) > kMaxLds) ++s;
-    *splits = s;
+struct Shape {
+    int kernel, rb, waves, splits;
+};
+
+bool shape_fits(int K, int T, const Shape& c) {
+    if (c.kernel == 1) return T <= kMaxVectorTokens && gemv_fits(K, T, c.rb, c.waves, c.splits);
+    // MFMA: each thread stages at most 4 B-operand groups of the split's steps
+    return split_steps(K, c.splits) <= 4 * c.waves && gemm_fits(K, c.rb, c.waves, c.splits);
 }
 
-int resolve_launch(int N, int K, int T, const rv12_launch* cfg, int* rb, int* waves, int* splits) {
-    int drb, dw, ds;
-    default_launch(N, K, T, &drb, &dw, &ds);
-    *rb = (cfg && cfg->rb) ? cfg->rb : drb;
-    *waves = (cfg && cfg->waves) ? cfg->waves : dw;
-    *splits = (cfg && cfg->splits) ? cfg->splits : ds;
-    if (cfg && (!cfg->splits) && (cfg->rb || cfg->waves)) {
-        // keep the LDS bound when only rb / waves were given
-        while (*splits < kMaxSplits && *splits < K / 32 &&
-               linear_lds_bytes(K, T, *rb, *waves, *splits) > kMaxLds)
-            ++*splits;
+// Built-in launch shape for (N, K, T), from launch-shape sweeps of the
+// Qwen3-8B / 14B linear shapes on MI355X.
+//   vector kernel (T <= 4): one row block per workgroup and 8 waves (16 for
+//     K >= 8192, 4 with two row blocks beyond 4096 row blocks); K is split
+//     only when there are fewer than 128 row blocks, so the grid still
+//     covers the 256 CUs;
+//   MFMA kernel (T > 4): 8 waves of one row block each, K split so a
+//     workgroup stages at most 1024 columns of x'.
+Shape default_shape(int N, int K, int T) {
+    const int64_t nblk = nblocks(N);
+    const int nsteps = K / 32;
+    Shape c;
+    if (T <= kMaxVectorTokens) {
+        c.kernel = 1;
+        c.rb = nblk >= 4096 ? 2 : 1;
+        c.waves = nblk >= 4096 ? 4 : (K >= 8192 ? 16 : 8);
+        c.splits = 1;
+        if (nblk < 128) c.splits = (int)std::min<int64_t>(4, (256 + nblk - 1) / nblk);
+    } else {
+        c.kernel = 2;
+        c.rb = 1;
+        c.waves = 8;
+        c.splits = (nsteps + 31) / 32;
     }
-    if (*rb != 1 && *rb != 2 && *rb != 4) return RV12_E_CONFIG;
-    if (*waves < 1 || *waves > kMaxWaves) return RV12_E_CONFIG;
-    if (*splits < 1 || *splits > kMaxSplits || *splits > K / 32) return RV12_E_CONFIG;
-    if (linear_lds_bytes(K, T, *rb, *waves, *splits) > kMaxLds) return RV12_E_CONFIG;
+    while (c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
+    while (c.splits < kMaxSplits && c.splits < nsteps && !shape_fits(K, T, c)) ++c.splits;
+    // the vector kernel streams best with all activations loaded before the weights
+    while (c.kernel == 1 && c.splits < kMaxSplits && c.splits < nsteps && !gemv_prefetch_all(K, T, c.waves, c.splits))
+        ++c.splits;
+    return c;
+}
+
+int resolve_launch(int N, int K, int T, const rv12_launch* cfg, Shape* out) {
+    Shape c = default_shape(N, K, T);
+    if (cfg) {
+        if (cfg->kernel) c.kernel = cfg->kernel;
+        if (cfg->kernel && cfg->kernel != default_shape(N, K, T).kernel) {
+            // another kernel than the built-in one: its own defaults first
+            c.rb = 1;
+            c.waves = 8;
+            c.splits = c.kernel == 2 ? (K / 32 + 31) / 32 : 1;
+        }
+        if (cfg->rb) c.rb = cfg->rb;
+        if (cfg->waves) c.waves = cfg->waves;
+        if (cfg->splits) {
+            c.splits = cfg->splits;
+        } else {
+            // keep the staging / LDS bounds when only other fields were given
+            while (c.splits < kMaxSplits && c.splits < K / 32 && c.kernel >= 1 && c.kernel <= 2 &&
+                   c.rb >= 1 && c.waves >= 1 && c.waves <= kMaxWaves && !shape_fits(K, T, c))
+                ++c.splits;
+        }
+    }
+    if (c.kernel != 1 && c.kernel != 2) return RV12_E_CONFIG;
+    if (c.kernel == 1 && T > kMaxVectorTokens) return RV12_E_CONFIG;
+    if (c.rb != 1 && c.rb != 2 && c.rb != 4) return RV12_E_CONFIG;
+    if (c.waves < 1 || c.waves > kMaxWaves) return RV12_E_CONFIG;
+    if (c.splits < 1 || c.splits > kMaxSplits || c.splits > K / 32) return RV12_E_CONFIG;
+    if (!shape_fits(K, T, c)) return RV12_E_CONFIG;
+    *out = c;
     return RV12_OK;
 }
 
@@ -62,7 +100,7 @@ size_t ws_bytes_for(int N, int T, int splits) {
 int check_matrix(const rv12_matrix* w) {
     if (!w || !w->tiles || !w->rp) return RV12_E_NULL;
     if (w->n_exc > 0 && (!w->er || !w->ec || !w->ev)) return RV12_E_NULL;
-    if (w->n < 1 || w->k < 32 || w->k % 32) return RV12_E_SHAPE;
+    if (w->n < 1 || w->k < 32 || w->k % 32 || w->k > kMaxK) return RV12_E_SHAPE;
     if (w->base < 0 || w->base > 241) return RV12_E_BASE;
     if (!aligned16(w->tiles)) return RV12_E_ALIGN;
     return RV12_OK;
@@ -92,13 +130,13 @@ const char* rv12_strerror(int s) {
 }
 
 size_t rv12_tiles_bytes(int n, int k) {
-    if (n < 1 || k < 32 || k % 32) return 0;
+    if (n < 1 || k < 32 || k % 32 || k > kMaxK) return 0;
     return (size_t)nblocks(n) * 16 * (size_t)k * 3 / 2;
 }
 
 int rv12_retile(const rv12_codec* in, uint32_t* tiles, size_t tiles_bytes, void* stream) {
     if (!in || !tiles || !in->m8 || !in->e4) return RV12_E_NULL;
-    if (in->n < 1 || in->k < 32 || in->k % 32 || in->ch < 16 || in->ch % 16 || in->k % in->ch) return RV12_E_SHAPE;
+    if (in->n < 1 || in->k < 32 || in->k % 32 || in->k > kMaxK || in->ch < 16 || in->ch % 16 || in->k % in->ch) return RV12_E_SHAPE;
     if (in->base < 0 || in->base > 241) return RV12_E_BASE;
     if (!aligned16(tiles)) return RV12_E_ALIGN;
     if (tiles_bytes < rv12_tiles_bytes(in->n, in->k)) return RV12_E_SIZE;
@@ -133,12 +171,8 @@ int rv12_encode_exc(const uint16_t* w, int n, int k, int base, const int32_t* rp
 }
 
 size_t rv12_workspace_bytes(int n, int k, int t, int splits) {
-    if (n < 1 || k < 32 || k % 32 || t < 1 || t > 16) return 0;
-    if (splits == 0) {
-        int rb, w, s;
-        default_launch(n, k, t, &rb, &w, &s);
-        splits = s;
-    }
+    if (n < 1 || k < 32 || k % 32 || k > kMaxK || t < 1 || t > 16) return 0;
+    if (splits == 0) splits = default_shape(n, k, t).splits;
     return ws_bytes_for(n, t, splits);
 }
 
@@ -150,9 +184,10 @@ int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint1
     if (mode < 0 || mode > 2) return RV12_E_MODE;
     if (t < 1 || t > 16) return RV12_E_TOKENS;
     if (!aligned16(x) || !aligned16(y) || ((uintptr_t)lnw & 7u)) return RV12_E_ALIGN;
-    int rb, waves, splits;
-    rc = resolve_launch(w->n, w->k, t, cfg, &rb, &waves, &splits);
+    Shape c;
+    rc = resolve_launch(w->n, w->k, t, cfg, &c);
     if (rc) return rc;
+    const int splits = c.splits;
     const size_t need = ws_bytes_for(w->n, t, splits);
     if (need && (!ws || ws_bytes < need)) return RV12_E_WORKSPACE;
     if (need && !aligned16(ws)) return RV12_E_ALIGN;
@@ -171,11 +206,14 @@ int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint1
     p.K = w->k;
     p.npad = (int)(nblocks(w->n) * 16);
     p.base = w->base;
+    p.sc = scale_exp(w->base);
     p.mode = mode;
     p.xs = mode == 2 ? 2 * w->k : w->k;
     p.n_exc = w->n_exc;
     p.eps = eps;
-    if (launch_linear(p, t, rb, waves, splits, (hipStream_t)stream)) return RV12_E_CONFIG;
+    const int lrc = c.kernel == 1 ? launch_gemv(p, t, c.rb, c.waves, splits, (hipStream_t)stream)
+                                  : launch_gemm(p, t, c.rb, c.waves, splits, (hipStream_t)stream);
+    if (lrc) return RV12_E_CONFIG;
     return launch_status();
 }
 

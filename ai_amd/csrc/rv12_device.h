@@ -1,0 +1,77 @@
+// Device-side helpers shared by the rv12 kernels (gfx950).
+//
+// Q16 layout (written by k_retile, read by every other kernel)
+// -------------------------------------------------------------
+// Rows are grouped in blocks of 16, K in steps of 32.  For row block b, step s
+// and lane l (0..63) one 12-byte group holds the 8 weights of row 16b + l%16 at
+// k = 32s + 8(l/16) + 0..7.  The groups of one (b, s) are contiguous
+// (64 x 12 = 768 bytes, one coalesced buffer_load_dwordx3 per wave), the steps
+// of one row block follow each other (K/32 * 768 bytes per row block), and the
+// lane -> (row, k) map is the A-operand map of v_mfma_f32_16x16x32_bf16.
+//
+// Each weight is kept as a 16-bit "h" = sign << 15 | c << 7 | mantissa7 with a
+// 4-bit exponent field c in bits 7..10.  With sc = max(base - 1, 0):
+//   c = e - sc        weight in the window (e = biased exponent, code = e - base)
+//   h = 0             exception (its value is in the codec's ev list)
+// For base >= 1 every in-window weight has c = code + 1 >= 1, so h = 0 marks
+// exactly the exceptions; for base = 0, c = e and the zero / subnormal weights
+// of the window keep their own bits.  Read as the top half of a float32,
+// h << 16 is the weight times 2^-sc, exactly, so a dot product can use the raw
+// h values and rescale the sum once by 2^sc.
+// Weights 0..7 pair up as P0 = h0 | h1 << 16 ... P3 = h6 | h7 << 16.  The pairs
+// never use bits 11..14 and 27..30, so three dwords carry four pairs:
+//   D0 = P0 | (P3 & 0x000F000F) << 11
+//   D1 = P1 | (P3 & 0x00F000F0) << 7
+//   D2 = P2 | (P3 & 0x07000700) << 3 | (P3 & 0x80008000) >> 1
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rv12_internal.h"
+
+namespace rv12 {
+
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kStepBytes = 768;       // one (row block, step) tile: 16 rows x 32 k x 1.5 bytes
+constexpr int kStepWords = 192;
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format (gfx9 family)
+constexpr int kNonTemporal = 2;        // cache policy bits of a streaming load
+
+// the four h-pairs of one 12-byte group
+__device__ __forceinline__ void unpack_pairs(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t p[4]) {
+    p[0] = d0 & 0x87FF87FFu;
+    p[1] = d1 & 0x87FF87FFu;
+    p[2] = d2 & 0x87FF87FFu;
+    p[3] = ((d0 >> 11) & 0x000F000Fu) | ((d1 >> 7) & 0x00F000F0u) | ((d2 >> 3) & 0x07000700u) |
+           ((d2 << 1) & 0x80008000u);
+}
+
+__device__ __forceinline__ float lo_f(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float hi_f(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+// h -> original bf16 bits (exceptions come out as 0 and are scattered later)
+__device__ __forceinline__ uint32_t h_to_bf16(uint32_t h, int sc) {
+    const uint32_t c = (h >> 7) & 15u;
+    return c ? ((h + ((uint32_t)sc << 7)) & 0xFFFFu) : h;
+}
+
+// silu(g) * u with the hardware exp2 and reciprocal (about 2 ulp each)
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
+}
+
+// one 12-byte group; a load through a descriptor of 0 bytes (or past its
+// end) returns zeros without touching memory
+__device__ __forceinline__ u32x3 load_group(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, kNonTemporal);
+}
+
+}  // namespace rv12

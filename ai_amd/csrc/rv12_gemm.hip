@@ -1,0 +1,319 @@
+// rv12 fused 12-bit decode + skinny GEMM on bf16 MFMA, 1..16 tokens (gfx950).
+//
+// y[t] (=|+=) W_dec . x'[t] for t < T <= 16 with W in the Q16 layout
+// (rv12_device.h), whose 16 x 32 step tiles are already the A operand of
+// v_mfma_f32_16x16x32_bf16: lane l holds row l%16 at k = 8(l/16) + 0..7, and
+// the four h-pairs of a 12-byte group are those 8 bf16 values (the weights
+// times 2^-sc; MFMA keeps subnormal inputs and products).
+//
+// The activations keep float32 accuracy the way the reference's bf16 tensor
+// path does (ramvi/engine/ramvi_engine/kernels/wcomp.py:130-140): x' is split
+// into three bf16 parts hi + mid + lo (hi = bf16(x'), mid = bf16(x' - hi),
+// lo = bf16(x' - hi - mid); the sum carries 24 mantissa bits) and each weight
+// tile meets each part in its own MFMA, accumulated in float32.
+//
+// Workgroup = W waves over the K steps [s_lo, s_hi) of split blockIdx.y and
+// W * RBW row blocks; wave w owns row blocks w*RBW .. w*RBW + RBW - 1.
+//   1. every thread loads the activations of its B-operand groups (one group
+//      = one step x one lane: token l%16, k = 8(l/16) + 0..7);
+//   2. each wave issues the loads of its first kDepth weight steps;
+//   3. x' is formed (MODE / RMS transform), split into hi/mid/lo and written
+//      to LDS in B-operand lane order (tokens >= T are zeros); barrier;
+//   4. main loop: per step three ds_read_b128 fetch the B parts, each of the
+//      wave's row blocks is unpacked once and meets the three parts in three
+//      MFMAs into three independent accumulators;
+//   5. epilogue per wave: the exceptions of the wave's rows whose column is
+//      inside the split are summed per (row, token) by a segmented scan over
+//      the row-major exception list, x' taken from the LDS parts; the sum of
+//      the three accumulators is rescaled by 2^sc, the exception sums added,
+//      and stored (one split) or written as a partial for k_splitk_reduce.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rv12_device.h"
+#include "rv12_internal.h"
+
+namespace rv12 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kGroupsPerThread = 4;  // B-operand groups a thread stages; host: steps <= 4 * waves
+
+__device__ __forceinline__ uint32_t bf16_bits(float v) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v);
+}
+__device__ __forceinline__ float bf16_value(uint32_t b) { return __uint_as_float(b << 16); }
+
+// split 8 values into three bf16x8 parts (as u32x4) with hi + mid + lo = v to 24 bits
+__device__ __forceinline__ void split3(const float (&v)[8], u32x4& hi, u32x4& mid, u32x4& lo) {
+    uint32_t h[8], m[8], l[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        h[e] = bf16_bits(v[e]);
+        const float r1 = v[e] - bf16_value(h[e]);
+        m[e] = bf16_bits(r1);
+        const float r2 = r1 - bf16_value(m[e]);
+        l[e] = bf16_bits(r2);
+    }
+    hi = u32x4{h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16};
+    mid = u32x4{m[0] | m[1] << 16, m[2] | m[3] << 16, m[4] | m[5] << 16, m[6] | m[7] << 16};
+    lo = u32x4{l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16};
+}
+
+template <int RBW>
+__device__ __forceinline__ void issue_rows(u32x3 (&dst)[RBW], __amdgpu_buffer_rsrc_t rv,
+                                           __amdgpu_buffer_rsrc_t rnull, const int (&voff)[RBW], int s, int s_hi) {
+    const __amdgpu_buffer_rsrc_t r = s < s_hi ? rv : rnull;
+    const int soff = (s < s_hi ? s : 0) * kStepBytes;
+#pragma unroll
+    for (int b = 0; b < RBW; ++b) dst[b] = load_group(r, voff[b], soff);
+}
+
+__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+template <int RBW>
+__global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int T) {
+    extern __shared__ u32x4 lds4[];
+    const int W = blockDim.x >> 6;
+    const int nthr = blockDim.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wu = __builtin_amdgcn_readfirstlane(wave);
+    const int S = gridDim.y, sp = blockIdx.y;
+    const int nsteps = p.K >> 5;
+    const int s_lo = (int)((int64_t)sp * nsteps / S), s_hi = (int)((int64_t)(sp + 1) * nsteps / S);
+    const int nst = s_hi - s_lo, k_lo = s_lo * 32, krange = nst * 32;
+    const int64_t nblk = (p.N + 15) / 16;
+    const int64_t blk0 = (int64_t)blockIdx.x * W * RBW;
+    const int n0 = (int)(blk0 * 16);
+    const int64_t wblk = blk0 + wu * RBW;  // first row block of this wave
+    const int nw = (int)(wblk * 16);        // first row of this wave
+    const int nvalid = (int)max((int64_t)0, min((int64_t)RBW, nblk - wblk));
+
+    u32x4* xb = lds4;                                               // [nst][3][64]
+    float* exc = reinterpret_cast<float*>(xb + (size_t)nst * 192);  // [W*RBW*16 rows][16 tokens]
+    float* ssq = exc + W * RBW * 256;                               // [W][16]
+
+    // ---- 1. activations of this thread's B groups
+    f32x4 xa[kGroupsPerThread][2], ua[kGroupsPerThread][2];
+    u32x4 la[kGroupsPerThread];
+    const int jj = lane & 15;  // token of every group of this thread
+    const bool tok = jj < T;
+#pragma unroll
+    for (int i = 0; i < kGroupsPerThread; ++i) {
+        const int g = threadIdx.x + i * nthr;
+        const int s = g >> 6;
+        if (s < nst && tok) {
+            const int k = k_lo + s * 32 + ((g & 63) >> 4) * 8;
+            const float* xt = p.x + (int64_t)jj * p.xs + k;
+            xa[i][0] = *reinterpret_cast<const f32x4*>(xt);
+            xa[i][1] = *reinterpret_cast<const f32x4*>(xt + 4);
+            if (p.mode == 2) {
+                ua[i][0] = *reinterpret_cast<const f32x4*>(xt + p.K);
+                ua[i][1] = *reinterpret_cast<const f32x4*>(xt + p.K + 4);
+            }
+            if (p.lnw) la[i] = *reinterpret_cast<const u32x4*>(p.lnw + k);
+        }
+    }
+
+    // ---- 2. first kDepth weight steps of this wave's row blocks
+    const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
+    const char* wbase = reinterpret_cast<const char*>(p.tiles) + wblk * (int64_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, (uint32_t)nvalid * blk_bytes);
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(wbase, 0u);
+    int voff[RBW];
+#pragma unroll
+    for (int b = 0; b < RBW; ++b) voff[b] = (int)(b * blk_bytes) + lane * 12;
+    u32x3 buf[kDepth][RBW];
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) issue_rows<RBW>(buf[u], rv, rnull, voff, s_lo + u, s_hi);
+
+    // ---- 3. x' split into bf16 parts, in B-operand order
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kGroupsPerThread; ++i) {
+        const int g = threadIdx.x + i * nthr;
+        const int s = g >> 6;
+        if (s < nst) {
+            u32x4 hi = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
+            if (tok) {
+                float v[8] = {xa[i][0].x, xa[i][0].y, xa[i][0].z, xa[i][0].w,
+                              xa[i][1].x, xa[i][1].y, xa[i][1].z, xa[i][1].w};
+                if (p.lnw) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) sq += v[e] * v[e];
+                }
+                if (p.mode == 2) {
+                    const float u[8] = {ua[i][0].x, ua[i][0].y, ua[i][0].z, ua[i][0].w,
+                                        ua[i][1].x, ua[i][1].y, ua[i][1].z, ua[i][1].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = silu_mul(v[e], u[e]);
+                }
+                if (p.lnw) {
+                    const uint32_t lw[4] = {la[i].x, la[i].y, la[i].z, la[i].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[2 * e] *= __uint_as_float(lw[e] << 16);
+                        v[2 * e + 1] *= __uint_as_float(lw[e] & 0xFFFF0000u);
+                    }
+                }
+                split3(v, hi, mid, lo);
+            }
+            u32x4* d = xb + (size_t)s * 192 + (g & 63);
+            d[0] = hi;
+            d[64] = mid;
+            d[128] = lo;
+        }
+    }
+    if (p.lnw) {
+        sq += __shfl_xor(sq, 16);
+        sq += __shfl_xor(sq, 32);
+        if (lane < 16) ssq[wave * 16 + lane] = sq;
+    }
+    // this wave's exception sums start at zero
+    float* excw = exc + wu * RBW * 256;
+#pragma unroll
+    for (int i = 0; i < RBW * 4; ++i) excw[i * 64 + lane] = 0.0f;
+    __syncthreads();
+
+    // ---- 4. main loop
+    f32x4 acc[RBW][3];
+#pragma unroll
+    for (int b = 0; b < RBW; ++b)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) acc[b][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int rounds = (nst + kDepth - 1) / kDepth;
+    for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+        for (int u = 0; u < kDepth; ++u) {
+            const int sr = r * kDepth + u;  // step within the split
+            u32x3 cur[RBW];
+#pragma unroll
+            for (int b = 0; b < RBW; ++b) cur[b] = buf[u][b];
+            issue_rows<RBW>(buf[u], rv, rnull, voff, s_lo + sr + kDepth, s_hi);
+            if (sr < nst) {
+                const u32x4* bsrc = xb + (size_t)sr * 192 + lane;
+                const u32x4 b0 = bsrc[0], b1 = bsrc[64], b2 = bsrc[128];
+#pragma unroll
+                for (int b = 0; b < RBW; ++b) {
+                    uint32_t pr[4];
+                    unpack_pairs(cur[b].x, cur[b].y, cur[b].z, pr);
+                    const u32x4 a = {pr[0], pr[1], pr[2], pr[3]};
+                    acc[b][0] = mfma(a, b0, acc[b][0]);
+                    acc[b][1] = mfma(a, b1, acc[b][1]);
+                    acc[b][2] = mfma(a, b2, acc[b][2]);
+                }
+            }
+        }
+    }
+
+    // ---- 5. exceptions of this wave's rows, columns inside the split
+    const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(xb);
+    if (p.n_exc > 0 && nvalid > 0) {
+        const int32_t e_lo = p.rp[nw], e_hi = p.rp[min(nw + RBW * 16, p.N)];
+        for (int32_t j0 = e_lo; j0 < e_hi; j0 += 64) {
+            const int32_t j = j0 + lane;
+            const bool valid = j < e_hi;
+            int r = 0x7FFFFFFF, c = -1;
+            float v = 0.0f;
+            if (valid) {
+                r = p.er[j] - nw;
+                c = p.ec[j] - k_lo;
+                v = p.ev[j];
+            }
+            const bool in = valid && c >= 0 && c < krange;
+            // byte offset of x'(token 0, c) in part 0: step c/32, lane 16 * ((c%32)/8), element c%8
+            const int cb = in ? ((c >> 5) * 192 + ((c & 31) >> 3) * 16) * 16 + (c & 7) * 2 : 0;
+            float pv[16];
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                pv[t] = 0.0f;
+                if (in && t < T) {
+                    const int o = cb + t * 16;
+                    const float xv = bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o)) +
+                                     bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o + 1024)) +
+                                     bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o + 2048));
+                    pv[t] = v * xv;
+                }
+            }
+            for (int d = 1; d < 64; d <<= 1) {
+                const int rn = __shfl_up(r, d);
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    if (t < T) {
+                        const float o = __shfl_up(pv[t], d);
+                        if (lane >= d && rn == r) pv[t] += o;
+                    }
+                }
+            }
+            const int rnext = __shfl_down(r, 1);
+            if (valid && (lane == 63 || rnext != r)) {
+#pragma unroll
+                for (int t = 0; t < 16; ++t)
+                    if (t < T) excw[r * 16 + t] += pv[t];
+            }
+        }
+    }
+
+    // ---- 6. outputs: lane l holds token l%16, rows 4(l/16) + 0..3 of each row block
+    const int q = lane >> 4;
+    float rs = 1.0f;
+    if (p.lnw && S == 1 && tok) {
+        float v = 0.0f;
+        for (int w = 0; w < W; ++w) v += ssq[w * 16 + jj];
+        rs = 1.0f / sqrtf(v / (float)p.K + p.eps);
+    }
+#pragma unroll
+    for (int b = 0; b < RBW; ++b) {
+        const f32x4 a = acc[b][0] + acc[b][1] + acc[b][2];
+        const float av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rloc = b * 16 + q * 4 + i;
+            const int n = nw + rloc;
+            if (tok && n < p.N) {
+                float v = ldexpf(av[i], p.sc) + excw[rloc * 16 + jj];
+                if (S == 1) {
+                    float* y = p.y + (int64_t)jj * p.N + n;
+                    if (p.lnw) v *= rs;
+                    *y = p.mode == 0 ? v : *y + v;
+                } else {
+                    p.part[((int64_t)sp * T + jj) * p.npad + n] = v;
+                }
+            }
+        }
+    }
+    if (S > 1 && p.lnw && blockIdx.x == 0 && threadIdx.x < T) {
+        float v = 0.0f;
+        for (int w = 0; w < W; ++w) v += ssq[w * 16 + threadIdx.x];
+        p.ssq[sp * T + threadIdx.x] = v;
+    }
+    (void)n0;
+}
+
+template <int RBW>
+static void launch_r(const LinearParams& p, int T, dim3 grid, int threads, size_t lds, hipStream_t st) {
+    if (lds > kDefaultLds)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<RBW>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL((k_gemm<RBW>), grid, dim3(threads), lds, st, p, T);
+}
+
+int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st) {
+    const int64_t nblk = (p.N + 15) / 16;
+    const int64_t per_wg = (int64_t)rbw * waves;
+    dim3 grid((unsigned)((nblk + per_wg - 1) / per_wg), (unsigned)splits);
+    const size_t lds = gemm_lds_bytes(p.K, rbw, waves, splits);
+    switch (rbw) {
+        case 1: launch_r<1>(p, T, grid, waves * 64, lds, st); break;
+        case 2: launch_r<2>(p, T, grid, waves * 64, lds, st); break;
+        case 4: launch_r<4>(p, T, grid, waves * 64, lds, st); break;
+        default: return -1;
+    }
+    if (splits > 1) launch_splitk_reduce(p, T, splits, st);
+    return 0;
+}
+
+}  // namespace rv12

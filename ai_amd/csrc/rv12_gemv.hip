@@ -1,0 +1,367 @@
+// rv12 fused 12-bit decode + linear on the vector ALUs, 1..4 tokens (gfx950).
+//
+// y[t] (=|+=) W_dec . x'[t] with W in the Q16 layout (rv12_device.h).
+//
+// Workgroup = W waves over 16*RB rows (RB row blocks) and the K steps
+// [s_lo, s_hi) of split blockIdx.y.  Wave w takes the steps s_lo + w + W*i.
+// Order of work, so that every long-latency load is in flight before
+// anything waits on it:
+//   1. every thread loads its share of the activations (x, and u in mode 2,
+//      and the RMSNorm weight) for the split's K range;
+//   2. each wave issues the loads of its first kDepth weight steps (buffer
+//      loads; a step past the split's end goes through a 0-byte descriptor,
+//      which returns zeros without a memory access);
+//   3. the activation loads are waited for (the weight loads stay in flight)
+//      and x' is written to LDS: the MODE / RMS transform, and the sum of
+//      squares for RMS; the workgroup's first round of exceptions is fetched;
+//      one barrier;
+//   4. main loop: per step each wave decodes 8 weights per lane and row block
+//      and does 8 FMAs per token into fp32 accumulators, and issues the load
+//      kDepth steps ahead;
+//   5. epilogue: lane quarters and waves are summed in a fixed order (no
+//      atomics), rescaled by 2^sc, the exceptions whose column lies in the
+//      split are added (per wave a segmented scan over its slice of the
+//      row-major exception list), and the result is stored (one split) or
+//      written as a partial for k_splitk_reduce.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rv12_device.h"
+#include "rv12_internal.h"
+
+namespace rv12 {
+
+template <int RB>
+__device__ __forceinline__ void issue_step(u32x3 (&dst)[RB], __amdgpu_buffer_rsrc_t rv, __amdgpu_buffer_rsrc_t rnull,
+                                           const int (&voff)[RB], int s, int s_hi) {
+    const __amdgpu_buffer_rsrc_t r = s < s_hi ? rv : rnull;
+    const int soff = (s < s_hi ? s : 0) * kStepBytes;
+#pragma unroll
+    for (int b = 0; b < RB; ++b) dst[b] = load_group(r, voff[b], soff);
+}
+
+// NXM = float4 chunks of activations per thread loaded in step 1, before the
+// weight prefetch; columns beyond 4 * NXM * blockDim.x are staged after it.
+template <int T, int RB>
+__global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p) {
+    constexpr int NXM = gemv_chunks(T);
+    extern __shared__ float smem[];
+    const int W = blockDim.x >> 6;
+    const int nthr = blockDim.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
+    const int wu = __builtin_amdgcn_readfirstlane(wave);
+    const int S = gridDim.y, sp = blockIdx.y;
+    const int nsteps = p.K >> 5;
+    const int s_lo = (int)((int64_t)sp * nsteps / S), s_hi = (int)((int64_t)(sp + 1) * nsteps / S);
+    const int k_lo = s_lo * 32, krange = (s_hi - s_lo) * 32;
+    const int64_t blk0 = (int64_t)blockIdx.x * RB;
+    const int n0 = (int)(blk0 * 16);
+    const int64_t nblk = (p.N + 15) / 16;
+    const int nvalid = (int)min((int64_t)RB, nblk - blk0);
+
+    float* xl = smem;                      // [T][krange]
+    float* red = xl + T * krange;          // [W][RB][T][16]
+    float* exc = red + W * RB * T * 16;    // [W][RB*16][T]
+    float* ssq = exc + W * RB * 16 * T;    // [W][T]
+
+    // ---- 1. activations of this thread
+    f32x4 xr[NXM][T], ur[NXM][T];
+    uint2 lr[NXM];
+#pragma unroll
+    for (int j = 0; j < NXM; ++j) {
+        const int i = (threadIdx.x + j * nthr) * 4;
+        if (i < krange) {
+            const int k = k_lo + i;
+            if (p.lnw) lr[j] = *reinterpret_cast<const uint2*>(p.lnw + k);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const float* xt = p.x + (int64_t)t * p.xs;
+                xr[j][t] = *reinterpret_cast<const f32x4*>(xt + k);
+                if (p.mode == 2) ur[j][t] = *reinterpret_cast<const f32x4*>(xt + p.K + k);
+            }
+        }
+    }
+
+    // ---- 2. first kDepth weight steps of this wave
+    const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
+    const char* wbase = reinterpret_cast<const char*>(p.tiles) + blk0 * (int64_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, (uint32_t)nvalid * blk_bytes);
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(wbase, 0u);
+    int voff[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) voff[b] = (int)(b * blk_bytes) + lane * 12;
+    const int s0 = s_lo + wu;
+    u32x3 buf[kDepth][RB];
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) issue_step<RB>(buf[u], rv, rnull, voff, s0 + u * W, s_hi);
+
+    // ---- 3. x' into LDS
+    float sq[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) sq[t] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NXM; ++j) {
+        const int i = (threadIdx.x + j * nthr) * 4;
+        if (i < krange) {
+            f32x4 lw = {1.0f, 1.0f, 1.0f, 1.0f};
+            if (p.lnw)
+                lw = f32x4{__uint_as_float(lr[j].x << 16), __uint_as_float(lr[j].x & 0xFFFF0000u),
+                           __uint_as_float(lr[j].y << 16), __uint_as_float(lr[j].y & 0xFFFF0000u)};
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                f32x4 v = xr[j][t];
+                if (p.lnw) sq[t] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                if (p.mode == 2) {
+                    const f32x4 u = ur[j][t];
+                    v = f32x4{silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w)};
+                }
+                if (p.lnw) v = lw * v;
+                *reinterpret_cast<f32x4*>(xl + t * krange + i) = v;
+            }
+        }
+    }
+    // columns beyond the register-staged ones (large K ranges with few
+    // threads): loaded here, after the weight prefetch
+    for (int i = (threadIdx.x + NXM * nthr) * 4; i < krange; i += nthr * 4) {
+        const int k = k_lo + i;
+        f32x4 lw = {1.0f, 1.0f, 1.0f, 1.0f};
+        if (p.lnw) {
+            const uint2 b = *reinterpret_cast<const uint2*>(p.lnw + k);
+            lw = f32x4{__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xFFFF0000u), __uint_as_float(b.y << 16),
+                       __uint_as_float(b.y & 0xFFFF0000u)};
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float* xt = p.x + (int64_t)t * p.xs;
+            f32x4 v = *reinterpret_cast<const f32x4*>(xt + k);
+            if (p.lnw) sq[t] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            if (p.mode == 2) {
+                const f32x4 u = *reinterpret_cast<const f32x4*>(xt + p.K + k);
+                v = f32x4{silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w)};
+            }
+            if (p.lnw) v = lw * v;
+            *reinterpret_cast<f32x4*>(xl + t * krange + i) = v;
+        }
+    }
+    for (int i = threadIdx.x; i < W * RB * 16 * T; i += nthr) exc[i] = 0.0f;
+    if (p.lnw) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float v = sq[t];
+            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+            if (lane == 0) ssq[wave * T + t] = v;
+        }
+    }
+    // this wave's 64-entry slice of the first round of the workgroup's
+    // exceptions; the values are first used after the main loop, so these
+    // loads do not hold up the barrier
+    int32_t e_lo = 0, e_hi = 0;
+    int er0 = 0, ec0 = 0;
+    float ev0 = 0.0f;
+    if (p.n_exc > 0) {
+        e_lo = p.rp[n0];
+        e_hi = p.rp[min(n0 + RB * 16, p.N)];
+        const int32_t j = e_lo + wu * 64 + lane;
+        if (j < e_hi) {
+            er0 = p.er[j];
+            ec0 = p.ec[j];
+            ev0 = p.ev[j];
+        }
+    }
+    __syncthreads();
+
+    // ---- 4. main loop
+    float acc[RB][T];
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[b][t] = 0.0f;
+
+    const int per_wave = (s_hi - s_lo + W - 1) / W;
+    const int rounds = (per_wave + kDepth - 1) / kDepth;
+    for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+        for (int u = 0; u < kDepth; ++u) {
+            const int s = s0 + (r * kDepth + u) * W;
+            u32x3 cur[RB];
+#pragma unroll
+            for (int b = 0; b < RB; ++b) cur[b] = buf[u][b];
+            issue_step<RB>(buf[u], rv, rnull, voff, s + kDepth * W, s_hi);
+            if (s < s_hi) {
+                uint32_t pr[RB][4];
+#pragma unroll
+                for (int b = 0; b < RB; ++b) unpack_pairs(cur[b].x, cur[b].y, cur[b].z, pr[b]);
+                const float* xs = xl + (s - s_lo) * 32 + q * 8;
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const f32x4 xa = *reinterpret_cast<const f32x4*>(xs + t * krange);
+                    const f32x4 xb = *reinterpret_cast<const f32x4*>(xs + t * krange + 4);
+#pragma unroll
+                    for (int b = 0; b < RB; ++b) {
+                        float a = acc[b][t];
+                        a = fmaf(lo_f(pr[b][0]), xa.x, a);
+                        a = fmaf(hi_f(pr[b][0]), xa.y, a);
+                        a = fmaf(lo_f(pr[b][1]), xa.z, a);
+                        a = fmaf(hi_f(pr[b][1]), xa.w, a);
+                        a = fmaf(lo_f(pr[b][2]), xb.x, a);
+                        a = fmaf(hi_f(pr[b][2]), xb.y, a);
+                        a = fmaf(lo_f(pr[b][3]), xb.z, a);
+                        a = fmaf(hi_f(pr[b][3]), xb.w, a);
+                        acc[b][t] = a;
+                    }
+                }
+            }
+        }
+    }
+
+    // ---- 5. epilogue: lane quarters, then waves
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float v = acc[b][t];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            if (lane < 16) red[((wave * RB + b) * T + t) * 16 + lane] = v;
+        }
+
+    // exceptions of this workgroup's rows with a column inside the split:
+    // rounds of W*64 entries, wave w takes entries [w*64, w*64+64) of each
+    float* excw = exc + wave * RB * 16 * T;
+    for (int32_t j0 = e_lo; j0 < e_hi; j0 += W * 64) {
+        const int32_t j = j0 + wu * 64 + lane;
+        const bool valid = j < e_hi;
+        int r = 0x7FFFFFFF, c = 0;
+        float v = 0.0f;
+        if (j0 == e_lo) {
+            if (valid) {
+                r = er0 - n0;
+                c = ec0;
+                v = ev0;
+            }
+        } else if (valid) {
+            r = p.er[j] - n0;
+            c = p.ec[j];
+            v = p.ev[j];
+        }
+        if (__builtin_amdgcn_readfirstlane(j0 + wu * 64) < e_hi) {  // this wave has entries
+            float pv[T];
+            c -= k_lo;
+            const bool in = valid && c >= 0 && c < krange;
+#pragma unroll
+            for (int t = 0; t < T; ++t) pv[t] = in ? v * xl[t * krange + c] : 0.0f;
+            for (int d = 1; d < 64; d <<= 1) {
+                const int rn = __shfl_up(r, d);
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const float o = __shfl_up(pv[t], d);
+                    if (lane >= d && rn == r) pv[t] += o;
+                }
+            }
+            const int rnext = __shfl_down(r, 1);
+            if (valid && (lane == 63 || rnext != r)) {
+#pragma unroll
+                for (int t = 0; t < T; ++t) excw[r * T + t] += pv[t];
+            }
+        }
+    }
+    __syncthreads();
+
+    float rs[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) rs[t] = 1.0f;
+    if (p.lnw && S == 1) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float v = 0.0f;
+            for (int w = 0; w < W; ++w) v += ssq[w * T + t];
+            rs[t] = 1.0f / sqrtf(v / (float)p.K + p.eps);
+        }
+    }
+    for (int idx = threadIdx.x; idx < RB * 16 * T; idx += nthr) {
+        const int r = idx % (RB * 16), t = idx / (RB * 16);
+        const int b = r >> 4, l16 = r & 15;
+        float v = 0.0f;
+        for (int w = 0; w < W; ++w) v += red[((w * RB + b) * T + t) * 16 + l16];
+        float e = 0.0f;
+        for (int w = 0; w < W; ++w) e += exc[(w * RB * 16 + r) * T + t];
+        v = ldexpf(v, p.sc) + e;
+        const int n = n0 + r;
+        if (n < p.N) {
+            if (S == 1) {
+                float* y = p.y + (int64_t)t * p.N + n;
+                if (p.lnw) v *= rs[t];
+                *y = p.mode == 0 ? v : *y + v;
+            } else {
+                p.part[((int64_t)sp * T + t) * p.npad + n] = v;
+            }
+        }
+    }
+    if (S > 1 && p.lnw && blockIdx.x == 0 && threadIdx.x < T) {
+        float v = 0.0f;
+        for (int w = 0; w < W; ++w) v += ssq[w * T + threadIdx.x];
+        p.ssq[sp * T + threadIdx.x] = v;
+    }
+}
+
+// second pass of a split linear: sum the partials of each output in split order
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, const float* __restrict__ ssq,
+                                                       float* __restrict__ y, int N, int npad, int T, int S,
+                                                       int mode, int rms, float eps, int K) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)T * N) return;
+    const int t = (int)(idx / N), n = (int)(idx % N);
+    float v = 0.0f;
+    for (int s = 0; s < S; ++s) v += part[((int64_t)s * T + t) * npad + n];
+    if (rms) {
+        float q = 0.0f;
+        for (int s = 0; s < S; ++s) q += ssq[s * T + t];
+        v *= 1.0f / sqrtf(q / (float)K + eps);
+    }
+    float* o = y + (int64_t)t * N + n;
+    *o = mode == 0 ? v : *o + v;
+}
+
+// ------------------------------------------------------------------ launch
+template <int T, int RB>
+static void launch_t(const LinearParams& p, dim3 grid, int threads, size_t lds, hipStream_t st) {
+    if (lds > kDefaultLds)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<T, RB>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL((k_gemv<T, RB>), grid, dim3(threads), lds, st, p);
+}
+
+template <int RB>
+static int launch_rb(const LinearParams& p, int T, dim3 grid, int threads, size_t lds, hipStream_t st) {
+    switch (T) {
+        case 1: launch_t<1, RB>(p, grid, threads, lds, st); return 0;
+        case 2: launch_t<2, RB>(p, grid, threads, lds, st); return 0;
+        case 3: launch_t<3, RB>(p, grid, threads, lds, st); return 0;
+        case 4: launch_t<4, RB>(p, grid, threads, lds, st); return 0;
+    }
+    return -1;
+}
+
+void launch_splitk_reduce(const LinearParams& p, int T, int splits, hipStream_t st) {
+    const int64_t tot = (int64_t)T * p.N;
+    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, p.part, p.ssq, p.y,
+                       p.N, p.npad, T, splits, p.mode, p.lnw != nullptr, p.eps, p.K);
+}
+
+int launch_gemv(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st) {
+    const int64_t nblk = (p.N + 15) / 16;
+    dim3 grid((unsigned)((nblk + rb - 1) / rb), (unsigned)splits);
+    const size_t lds = gemv_lds_bytes(p.K, T, rb, waves, splits);
+    int rc;
+    switch (rb) {
+        case 1: rc = launch_rb<1>(p, T, grid, waves * 64, lds, st); break;
+        case 2: rc = launch_rb<2>(p, T, grid, waves * 64, lds, st); break;
+        case 4: rc = launch_rb<4>(p, T, grid, waves * 64, lds, st); break;
+        default: return -1;
+    }
+    if (rc) return rc;
+    if (splits > 1) launch_splitk_reduce(p, T, splits, st);
+    return 0;
+}
+
+}  // namespace rv12

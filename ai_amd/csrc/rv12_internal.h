@@ -1,6 +1,7 @@
 // Shared declarations of the rv12 kernels and the C-ABI layer.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include "rv12.h"
@@ -18,23 +19,63 @@ struct LinearParams {
     const uint16_t* lnw;
     float* part;  // split partials [splits][T][npad]
     float* ssq;   // split sums of squares [splits][T]
-    int N, K, npad, base, mode, xs;
+    int N, K, npad, base, sc, mode, xs;
     int64_t n_exc;
     float eps;
 };
 
+// scale exponent of the h values of the Q16 layout: h << 16 read as a float
+// is the weight times 2^-sc
+__host__ __device__ inline int scale_exp(int base) { return base > 0 ? base - 1 : 0; }
+
+constexpr int kDepth = 8;          // weight steps in flight per wave
+constexpr int kMaxThreads = 1024;  // 16 waves
 constexpr int kMaxSplits = 64;
 constexpr int kMaxWaves = 16;
-constexpr size_t kMaxLds = 65536;
+constexpr size_t kMaxLds = 163840;  // LDS bytes of one gfx950 workgroup (160 KB)
+constexpr size_t kDefaultLds = 65536;  // above this a kernel needs hipFuncAttributeMaxDynamicSharedMemorySize
+constexpr int kMaxK = 1 << 20;         // keeps every 32-bit buffer offset of a workgroup in range
+constexpr int kMaxVectorTokens = 4;  // k_gemv (vector FMA) serves 1..4 tokens
 
-// LDS bytes of k_linear for a launch shape (largest split)
-inline size_t linear_lds_bytes(int K, int T, int rb, int waves, int splits) {
-    const int nsteps = K / 32;
-    const size_t krange = (size_t)((nsteps + splits - 1) / splits) * 32;
+// --- vector-FMA linear (k_gemv), 1..4 tokens
+// K steps of the largest split
+inline int split_steps(int K, int splits) { return (K / 32 + splits - 1) / splits; }
+
+// float4 activation chunks per thread the kernel keeps in registers
+__host__ __device__ constexpr int gemv_chunks(int T) { return T == 1 ? 6 : (T == 2 ? 2 : 1); }
+
+inline size_t gemv_lds_bytes(int K, int T, int rb, int waves, int splits) {
+    const size_t krange = (size_t)split_steps(K, splits) * 32;
     return 4 * ((size_t)T * krange + (size_t)waves * rb * T * 16 + (size_t)waves * rb * 16 * T + (size_t)waves * T);
 }
 
-int launch_linear(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st);
+// waves per workgroup the kernel is built for (its register budget)
+__host__ __device__ constexpr int gemv_max_waves(int rb) { return rb == 4 ? 8 : 16; }
+
+// launch shape fits the kernel's register budget and LDS
+inline bool gemv_fits(int K, int T, int rb, int waves, int splits) {
+    return waves <= gemv_max_waves(rb) && gemv_lds_bytes(K, T, rb, waves, splits) <= kMaxLds;
+}
+
+// every activation column of the split is loaded before the weight prefetch
+inline bool gemv_prefetch_all(int K, int T, int waves, int splits) {
+    return (size_t)split_steps(K, splits) * 32 <= (size_t)4 * gemv_chunks(T) * waves * 64;
+}
+
+// --- MFMA linear (k_gemm), 1..16 tokens
+constexpr size_t kGemmMaxLds = 131072;
+constexpr int kGemmMaxWaves = 8;
+inline size_t gemm_lds_bytes(int K, int rbw, int waves, int splits) {
+    const size_t steps = (size_t)split_steps(K, splits);
+    return steps * 3 * 1024 + (size_t)waves * rbw * 16 * 16 * 4 + 16 * 4 * (size_t)waves;
+}
+inline bool gemm_fits(int K, int rbw, int waves, int splits) {
+    return waves <= kGemmMaxWaves && gemm_lds_bytes(K, rbw, waves, splits) <= kGemmMaxLds;
+}
+
+int launch_gemv(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st);
+int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st);
+void launch_splitk_reduce(const LinearParams& p, int T, int splits, hipStream_t st);
 void launch_retile(const uint8_t* m8, const uint8_t* e4, int N, int K, int CH, int base, uint32_t* tiles,
                    hipStream_t st);
 void launch_decode(const rv12_matrix& w, int first, int last, void* out, int out_f32, hipStream_t st, int64_t e0,

@@ -152,10 +152,15 @@ def decompress(c):
     return decode_rows(c, 0, int(c["N"]), torch.bfloat16)
 
 
-def _rb(BN):
-    if not BN:
-        return 0
-    return 1 if BN <= 16 else (2 if BN <= 32 else 4)
+def _launch(BN, w, S, T):
+    """Launch struct for the reference's tuning triple.  BN = rows per
+    workgroup: row blocks of 16 per workgroup in the vector kernel (T <= 4),
+    row blocks per wave times waves in the MFMA kernel (T > 4)."""
+    rb = 0
+    if BN:
+        per = BN // 16 if T <= 4 else BN // (16 * int(w or 8))
+        rb = 1 if per <= 1 else (2 if per <= 2 else 4)
+    return Launch(0, rb, int(w or 0), int(S or 0))
 
 
 def _sk_buf(N, S, dev, K=None, T=16):
@@ -185,7 +190,7 @@ def _linear(x, c, y, mode, T, BN, w, S, lnw, eps, where):
         if lnw.dtype != torch.bfloat16 or lnw.numel() < K or not lnw.is_contiguous():
             raise ValueError(f"{where}: lnw must be a contiguous bf16 vector of K entries")
     m = _matrix(c)
-    cfg = Launch(_rb(BN), int(w or 0), int(S or 0))
+    cfg = _launch(BN, w, S, T)
     splits = int(S or 0)
     ws = _sk_buf(N, splits, x.device, K, T)
     rc = lib().rv12_gemm(ctypes.byref(m), _ptr(x), _ptr(y), int(T), _ptr(lnw), float(eps), int(mode),

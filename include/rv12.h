@@ -22,12 +22,12 @@
 extern "C" {
 #endif
 
-#define RV12_ABI_VERSION 1
+#define RV12_ABI_VERSION 2
 
 enum rv12_status {
     RV12_OK = 0,
     RV12_E_NULL = -1,      /* a required pointer is NULL */
-    RV12_E_SHAPE = -2,     /* N < 1, K < 32, K % 32, K % CH, CH % 16, or row range outside [0, N] */
+    RV12_E_SHAPE = -2,     /* N < 1, K < 32, K % 32, K > 2^20, K % CH, CH % 16, or rows outside [0, N] */
     RV12_E_MODE = -3,      /* mode not in {0, 1, 2} */
     RV12_E_TOKENS = -4,    /* T not in [1, 16] */
     RV12_E_WORKSPACE = -5, /* workspace smaller than rv12_workspace_bytes() */
@@ -64,11 +64,17 @@ typedef struct rv12_matrix {
     int64_t n_exc;
 } rv12_matrix;
 
-/* Launch shape of a linear: rows per workgroup (16 * rb, rb in {1, 2, 4}),
- * waves per workgroup (1..16), K splits across workgroups (1..64).  A zero
- * field (or a NULL pointer) selects the built-in choice for the shape. */
+/* Launch shape of a linear.
+ *   kernel  1 = vector-FMA kernel (T <= 4), 2 = bf16-MFMA kernel (T <= 16)
+ *   rb      vector kernel: row blocks of 16 rows per workgroup (1, 2, 4);
+ *           MFMA kernel: row blocks per wave (1, 2, 4)
+ *   waves   waves per workgroup (1..16)
+ *   splits  K splits across workgroups (1..64); more than one adds a second,
+ *           atomic-free pass that sums the partials in split order
+ * A zero field (or a NULL pointer) selects the built-in choice for the shape:
+ * the vector kernel for T <= 4, the MFMA kernel above. */
 typedef struct rv12_launch {
-    int32_t rb, waves, splits;
+    int32_t kernel, rb, waves, splits;
 } rv12_launch;
 
 /* ABI version of the library (RV12_ABI_VERSION).  Mirrors the reference's

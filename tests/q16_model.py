@@ -12,14 +12,21 @@ from oracle.codec import codes
 M_PAIR = np.uint32(0x87FF87FF)
 
 
+def scale_exp(base):
+    """sc: h << 16 read as a float32 is the weight times 2^-sc."""
+    return max(int(base) - 1, 0)
+
+
 def h_values(c):
-    """16-bit h per weight: sign<<15 | c'<<7 | m7 (c' = code+1 in window,
-    0 with sign/mantissa for exponent 0 in window, 0 with zeros for exceptions)."""
+    """16-bit h per weight: sign<<15 | c'<<7 | m7 with c' = e - sc for
+    in-window weights (code + 1 when base >= 1, the exponent itself when
+    base == 0) and h = 0 for exceptions."""
     code = codes(c)
     m = np.asarray(c["m8"]).astype(np.uint32)
     sm = ((m >> 7) << 15) | (m & 0x7F)
     base = int(c["base"])
-    h = np.where(code == 15, 0, np.where(code + base == 0, sm, sm | ((code + 1).astype(np.uint32) << 7)))
+    cc = (code + base - scale_exp(base)).astype(np.uint32)
+    h = np.where(code == 15, 0, sm | (cc << 7))
     return h.astype(np.uint32)
 
 
@@ -62,15 +69,15 @@ def h_from_tiles(tiles, N, K):
 def bf16_from_h(h, base):
     """original bf16 bits from h (before the exception scatter), as h_to_bf16."""
     cc = (h >> 7) & 15
-    return np.where(cc != 0, (h.astype(np.int64) + ((base - 1) << 7)) & 0xFFFF, h).astype(np.uint16)
+    return np.where(cc != 0, (h.astype(np.int64) + (scale_exp(base) << 7)) & 0xFFFF, h).astype(np.uint16)
 
 
 def scaled_dot(c, xp):
     """sum_k h_k x'_k computed in float64 with h as a float32 value, rescaled by
-    2^(base-1), plus the exceptions: the kernels' formula in exact arithmetic."""
+    2^sc, plus the exceptions: the kernels' formula in exact arithmetic."""
     h = h_values(c)
     wh = (h.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
-    y = np.ldexp(xp @ wh.T, int(c["base"]) - 1)
+    y = np.ldexp(xp @ wh.T, scale_exp(c["base"]))
     er, ec, ev = (np.asarray(c[k]) for k in ("er", "ec", "ev"))
     for j in range(er.size):
         y[:, er[j]] += ev[j].astype(np.float64) * xp[:, ec[j]]

@@ -31,7 +31,7 @@ def test_library_exports_every_symbol():
 def test_abi_version_and_strerror():
     from ai_amd import _lib
     L = _lib.lib()
-    assert L.rv12_abi_version() == 1
+    assert L.rv12_abi_version() == 2
     for s in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -20):
         assert _lib.strerror(s) and _lib.strerror(s) != "unknown rv12 status"
     assert _lib.strerror(-99) == "unknown rv12 status"
@@ -75,13 +75,16 @@ def test_gemm_argument_errors():
     assert call(_mat(), t=17) == _lib.RV12_E_TOKENS
     assert call(_mat(tiles=0x1004)) == _lib.RV12_E_ALIGN
     assert call(_mat(), xx=ctypes.c_void_p(0x10004)) == _lib.RV12_E_ALIGN
-    assert call(_mat(), cfg=_lib.Launch(3, 4, 1)) == _lib.RV12_E_CONFIG
-    assert call(_mat(), cfg=_lib.Launch(1, 17, 1)) == _lib.RV12_E_CONFIG
-    assert call(_mat(), cfg=_lib.Launch(1, 4, 65)) == _lib.RV12_E_CONFIG
-    assert call(_mat(k=256), cfg=_lib.Launch(1, 4, 9)) == _lib.RV12_E_CONFIG  # more splits than K steps
+    assert call(_mat(), cfg=_lib.Launch(0, 3, 4, 1)) == _lib.RV12_E_CONFIG
+    assert call(_mat(), cfg=_lib.Launch(0, 1, 17, 1)) == _lib.RV12_E_CONFIG
+    assert call(_mat(), cfg=_lib.Launch(0, 1, 4, 65)) == _lib.RV12_E_CONFIG
+    assert call(_mat(k=256), cfg=_lib.Launch(0, 1, 4, 9)) == _lib.RV12_E_CONFIG  # more splits than K steps
+    assert call(_mat(), cfg=_lib.Launch(3, 1, 4, 1)) == _lib.RV12_E_CONFIG       # no kernel 3
+    assert call(_mat(), t=5, cfg=_lib.Launch(1, 1, 4, 1)) == _lib.RV12_E_CONFIG  # vector kernel: T <= 4
+    assert call(_mat(), t=2, cfg=_lib.Launch(2, 1, 16, 1)) == _lib.RV12_E_CONFIG  # MFMA kernel: <= 8 waves
     # a split launch needs a workspace of rv12_workspace_bytes()
     need = L.rv12_workspace_bytes(64, 256, 1, 2)
-    assert call(_mat(), cfg=_lib.Launch(1, 4, 2), wsb=need - 4) == _lib.RV12_E_WORKSPACE
+    assert call(_mat(), cfg=_lib.Launch(0, 1, 4, 2), wsb=need - 4) == _lib.RV12_E_WORKSPACE
     # exceptions declared without their arrays
     m = _mat(n_exc=5)
     m.er = 0

@@ -43,8 +43,9 @@ def test_scaled_dot_equals_closed_form(golden, name):
 
 def test_scaled_dot_exact_cases():
     """Identity-like rows: y picks single activations; base 0 and a window
-    reaching exponent 254 both rescale exactly."""
-    for scale in (1.0, 2.0 ** -120, 2.0 ** 100, 3.0):
+    reaching exponent 254 both rescale exactly, and with base 0 subnormal
+    weights enter with their own value."""
+    for scale in (1.0, 2.0 ** -120, 2.0 ** 100, 3.0, 2.0 ** -130, -(2.0 ** -133) * 3):
         w = np.zeros((16, 256), np.float32)
         w[np.arange(16), np.arange(16) * 7] = scale
         bits = codec.f32_to_bf16_rne(w)
