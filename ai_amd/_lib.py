@@ -19,10 +19,10 @@ RV12_E_WORKSPACE, RV12_E_CONFIG, RV12_E_BASE, RV12_E_ALIGN, RV12_E_SIZE = -5, -6
 RV12_E_LAUNCH = -20
 
 # every symbol include/rv12.h declares
-EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_retile", "rv12_encode_stats",
-           "rv12_encode", "rv12_encode_exc", "rv12_workspace_bytes", "rv12_gemv", "rv12_gemm",
-           "rv12_decode_rows")
-ABI_VERSION = 2
+EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_pack_plan", "rv12_pack",
+           "rv12_codec_to_bf16", "rv12_encode_stats", "rv12_encode", "rv12_encode_exc", "rv12_workspace_bytes",
+           "rv12_gemv", "rv12_gemm", "rv12_decode_rows")
+ABI_VERSION = 3
 
 
 class Codec(ctypes.Structure):
@@ -33,9 +33,9 @@ class Codec(ctypes.Structure):
 
 
 class Matrix(ctypes.Structure):
-    _fields_ = [("tiles", ctypes.c_void_p), ("rp", ctypes.c_void_p), ("er", ctypes.c_void_p),
-                ("ec", ctypes.c_void_p), ("ev", ctypes.c_void_p),
-                ("n", ctypes.c_int32), ("k", ctypes.c_int32), ("base", ctypes.c_int32), ("n_exc", ctypes.c_int64)]
+    _fields_ = [("tiles", ctypes.c_void_p), ("rbase", ctypes.c_void_p), ("rp", ctypes.c_void_p),
+                ("er", ctypes.c_void_p), ("ec", ctypes.c_void_p), ("ev", ctypes.c_void_p),
+                ("n", ctypes.c_int32), ("k", ctypes.c_int32), ("n_exc", ctypes.c_int64)]
 
 
 class Launch(ctypes.Structure):
@@ -68,8 +68,12 @@ def lib():
         L.rv12_strerror.argtypes = [I]
         L.rv12_tiles_bytes.restype = SZ
         L.rv12_tiles_bytes.argtypes = [I, I]
-        L.rv12_retile.restype = I
-        L.rv12_retile.argtypes = [ctypes.POINTER(Codec), P, SZ, P]
+        L.rv12_pack_plan.restype = I
+        L.rv12_pack_plan.argtypes = [P, I, I, P, P, P]
+        L.rv12_pack.restype = I
+        L.rv12_pack.argtypes = [P, I, I, P, P, I64, P, SZ, P, P, P, P]
+        L.rv12_codec_to_bf16.restype = I
+        L.rv12_codec_to_bf16.argtypes = [ctypes.POINTER(Codec), P, P]
         L.rv12_encode_stats.restype = I
         L.rv12_encode_stats.argtypes = [P, I, I, P, P]
         L.rv12_encode.restype = I

@@ -98,13 +98,14 @@ size_t ws_bytes_for(int N, int T, int splits) {
 }
 
 int check_matrix(const rv12_matrix* w) {
-    if (!w || !w->tiles || !w->rp) return RV12_E_NULL;
+    if (!w || !w->tiles || !w->rbase || !w->rp) return RV12_E_NULL;
     if (w->n_exc > 0 && (!w->er || !w->ec || !w->ev)) return RV12_E_NULL;
-    if (w->n < 1 || w->k < 32 || w->k % 32 || w->k > kMaxK) return RV12_E_SHAPE;
-    if (w->base < 0 || w->base > 241) return RV12_E_BASE;
+    if (w->n < 1 || w->k < 32 || w->k % 32 || w->k > kMaxK || w->n_exc < 0) return RV12_E_SHAPE;
     if (!aligned16(w->tiles)) return RV12_E_ALIGN;
     return RV12_OK;
 }
+
+bool shape_ok(int n, int k) { return n >= 1 && k >= 32 && k % 32 == 0 && k <= kMaxK; }
 
 }  // namespace
 
@@ -123,7 +124,7 @@ const char* rv12_strerror(int s) {
         case RV12_E_CONFIG: return "launch configuration out of range";
         case RV12_E_BASE: return "base must be in [0, 241]";
         case RV12_E_ALIGN: return "x, y, lnw or tiles not aligned (16 bytes; lnw 8 bytes)";
-        case RV12_E_SIZE: return "output buffer smaller than rv12_tiles_bytes()";
+        case RV12_E_SIZE: return "tiles buffer smaller than rv12_tiles_bytes()";
         case RV12_E_LAUNCH: return "kernel launch failed";
     }
     return "unknown rv12 status";
@@ -134,13 +135,32 @@ size_t rv12_tiles_bytes(int n, int k) {
     return (size_t)nblocks(n) * 16 * (size_t)k * 3 / 2;
 }
 
-int rv12_retile(const rv12_codec* in, uint32_t* tiles, size_t tiles_bytes, void* stream) {
-    if (!in || !tiles || !in->m8 || !in->e4) return RV12_E_NULL;
-    if (in->n < 1 || in->k < 32 || in->k % 32 || in->k > kMaxK || in->ch < 16 || in->ch % 16 || in->k % in->ch) return RV12_E_SHAPE;
+int rv12_pack_plan(const uint16_t* w, int n, int k, int32_t* rbase, int32_t* row_exc, void* stream) {
+    if (!w || !rbase || !row_exc) return RV12_E_NULL;
+    if (!shape_ok(n, k)) return RV12_E_SHAPE;
+    if (!aligned16(w)) return RV12_E_ALIGN;
+    launch_pack_plan(w, n, k, rbase, row_exc, (hipStream_t)stream);
+    return launch_status();
+}
+
+int rv12_pack(const uint16_t* w, int n, int k, const int32_t* rbase, const int32_t* rp, int64_t n_exc,
+              uint32_t* tiles, size_t tiles_bytes, int32_t* er, int32_t* ec, float* ev, void* stream) {
+    if (!w || !rbase || !rp || !tiles) return RV12_E_NULL;
+    if (n_exc > 0 && (!er || !ec || !ev)) return RV12_E_NULL;
+    if (!shape_ok(n, k) || n_exc < 0) return RV12_E_SHAPE;
+    if (!aligned16(w) || !aligned16(tiles)) return RV12_E_ALIGN;
+    if (tiles_bytes < rv12_tiles_bytes(n, k)) return RV12_E_SIZE;
+    launch_pack(w, n, k, rbase, rp, tiles, er, ec, ev, n_exc, (hipStream_t)stream);
+    return launch_status();
+}
+
+int rv12_codec_to_bf16(const rv12_codec* in, uint16_t* w, void* stream) {
+    if (!in || !w || !in->m8 || !in->e4) return RV12_E_NULL;
+    if (in->n_exc > 0 && (!in->er || !in->ec || !in->ev)) return RV12_E_NULL;
+    if (!shape_ok(in->n, in->k) || in->ch < 16 || in->ch % 16 || in->k % in->ch || in->n_exc < 0) return RV12_E_SHAPE;
     if (in->base < 0 || in->base > 241) return RV12_E_BASE;
-    if (!aligned16(tiles)) return RV12_E_ALIGN;
-    if (tiles_bytes < rv12_tiles_bytes(in->n, in->k)) return RV12_E_SIZE;
-    launch_retile(in->m8, in->e4, in->n, in->k, in->ch, in->base, tiles, (hipStream_t)stream);
+    if (!aligned16(w)) return RV12_E_ALIGN;
+    launch_codec_to_bf16(*in, w, (hipStream_t)stream);
     return launch_status();
 }
 
@@ -205,8 +225,7 @@ int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint1
     p.N = w->n;
     p.K = w->k;
     p.npad = (int)(nblocks(w->n) * 16);
-    p.base = w->base;
-    p.sc = scale_exp(w->base);
+    p.rbase = w->rbase;
     p.mode = mode;
     p.xs = mode == 2 ? 2 * w->k : w->k;
     p.n_exc = w->n_exc;

@@ -267,6 +267,7 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     }
 #pragma unroll
     for (int b = 0; b < RBW; ++b) {
+        if (b >= nvalid) break;
         const f32x4 a = acc[b][0] + acc[b][1] + acc[b][2];
         const float av[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
             const int rloc = b * 16 + q * 4 + i;
             const int n = nw + rloc;
             if (tok && n < p.N) {
-                float v = ldexpf(av[i], p.sc) + excw[rloc * 16 + jj];
+                float v = ldexpf(av[i], scale_exp(p.rbase[n])) + excw[rloc * 16 + jj];
                 if (S == 1) {
                     float* y = p.y + (int64_t)jj * p.N + n;
                     if (p.lnw) v *= rs;

@@ -285,9 +285,9 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
         for (int w = 0; w < W; ++w) v += red[((w * RB + b) * T + t) * 16 + l16];
         float e = 0.0f;
         for (int w = 0; w < W; ++w) e += exc[(w * RB * 16 + r) * T + t];
-        v = ldexpf(v, p.sc) + e;
         const int n = n0 + r;
         if (n < p.N) {
+            v = ldexpf(v, scale_exp(p.rbase[n])) + e;
             if (S == 1) {
                 float* y = p.y + (int64_t)t * p.N + n;
                 if (p.lnw) v *= rs[t];

@@ -17,9 +17,10 @@ struct LinearParams {
     const float* x;
     float* y;
     const uint16_t* lnw;
-    float* part;  // split partials [splits][T][npad]
-    float* ssq;   // split sums of squares [splits][T]
-    int N, K, npad, base, sc, mode, xs;
+    const int32_t* rbase;  // exponent window start of each row
+    float* part;           // split partials [splits][T][npad]
+    float* ssq;            // split sums of squares [splits][T]
+    int N, K, npad, mode, xs;
     int64_t n_exc;
     float eps;
 };
@@ -76,8 +77,10 @@ inline bool gemm_fits(int K, int rbw, int waves, int splits) {
 int launch_gemv(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st);
 int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st);
 void launch_splitk_reduce(const LinearParams& p, int T, int splits, hipStream_t st);
-void launch_retile(const uint8_t* m8, const uint8_t* e4, int N, int K, int CH, int base, uint32_t* tiles,
-                   hipStream_t st);
+void launch_codec_to_bf16(const rv12_codec& c, uint16_t* w, hipStream_t st);
+void launch_pack_plan(const uint16_t* w, int N, int K, int32_t* rbase, int32_t* row_exc, hipStream_t st);
+void launch_pack(const uint16_t* w, int N, int K, const int32_t* rbase, const int32_t* rp, uint32_t* tiles,
+                 int32_t* er, int32_t* ec, float* ev, int64_t n_exc, hipStream_t st);
 void launch_decode(const rv12_matrix& w, int first, int last, void* out, int out_f32, hipStream_t st, int64_t e0,
                    int64_t e1);
 void launch_encode_stats(const uint16_t* w, int64_t count, int32_t* hist, hipStream_t st);

@@ -13,9 +13,12 @@ plus decode_rows(c, first, last) (prefill_kernels.py:100-110) and prepare(c),
 which re-tiles a dict built elsewhere (the reference's own compress, a file)
 for the kernels.  Every call goes through librv12.so; there is no other path.
 
-The dict keeps the reference keys m8, e4, base, rp, er, ec, ev, N, K, CH and
-adds "q16": the weights re-tiled for the kernels (int32 words, 1.5 bytes per
-weight).  `compact(c)` drops m8/e4 once only the kernels read the dict.
+The dict keeps the reference keys m8, e4, base, rp, er, ec, ev, N, K, CH (bit
+for bit what the reference's compress builds) and adds "q16", the packed form
+the kernels read: "tiles" (the weights in the Q16 layout, 1.5 bytes per
+weight), "rbase" (one exponent window per row) and that layout's own
+exception list "rp"/"er"/"ec"/"ev".  `compact(c)` drops m8/e4 once only the
+kernels read the dict.
 Launch parameters keep the reference meaning: BN = rows per workgroup
 (rounded up to 16, 32 or 64), w = waves per workgroup, S = K splits.
 """
@@ -81,13 +84,49 @@ def compress(W, CH=256):
         check(L.rv12_encode_exc(_ptr(W), N, K, base, _ptr(rp), _ptr(er), _ptr(ec), _ptr(ev), st), "compress")
     c = {"m8": m8, "e4": e4, "base": base, "rp": rp, "er": er, "ec": ec, "ev": ev, "N": N, "K": K, "CH": CH}
     if K % 32 == 0 and CH % 16 == 0:
-        prepare(c)
+        c["q16"] = pack(W)
     return c
 
 
+def pack(W):
+    """bf16 W [N, K] on the GPU -> the kernels' packed form: Q16 tiles with one
+    exponent window per row and that layout's own exception list."""
+    N, K = W.shape
+    dev = W.device
+    L = lib()
+    st = _stream(dev)
+    rbase = torch.empty(N, dtype=torch.int32, device=dev)
+    row_exc = torch.empty(N, dtype=torch.int32, device=dev)
+    check(L.rv12_pack_plan(_ptr(W), N, K, _ptr(rbase), _ptr(row_exc), st), "pack")
+    rp = torch.zeros(N + 1, dtype=torch.int32, device=dev)
+    rp[1:] = row_exc.cumsum(0)
+    E = int(rp[-1])
+    nbytes = L.rv12_tiles_bytes(N, K)
+    if nbytes == 0:
+        raise ValueError("K must be a positive multiple of 32")
+    tiles = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    er = torch.empty(E, dtype=torch.int32, device=dev)
+    ec = torch.empty(E, dtype=torch.int32, device=dev)
+    ev = torch.empty(E, dtype=torch.float32, device=dev)
+    check(L.rv12_pack(_ptr(W), N, K, _ptr(rbase), _ptr(rp), E, _ptr(tiles), nbytes, _ptr(er), _ptr(ec), _ptr(ev),
+                      st), "pack")
+    return {"tiles": tiles, "rbase": rbase, "rp": rp, "er": er, "ec": ec, "ev": ev}
+
+
+def to_bf16(c):
+    """The bf16 matrix a codec dict encodes, bit for bit (NaN payloads kept)."""
+    dev = c["m8"].device
+    N, K = int(c["N"]), int(c["K"])
+    W = torch.empty(N, K, dtype=torch.bfloat16, device=dev)
+    cod = Codec(_ptr(c["m8"]), _ptr(c["e4"]), _ptr(c["rp"]), _ptr(c["er"]), _ptr(c["ec"]), _ptr(c["ev"]),
+                N, K, int(c["CH"]), int(c["base"]), int(c["er"].numel()))
+    check(lib().rv12_codec_to_bf16(ctypes.byref(cod), _ptr(W), _stream(dev)), "to_bf16")
+    return W
+
+
 def prepare(c, device=None):
-    """Re-tile the dict's m8/e4 into "q16" (and move CPU/numpy arrays to the
-    GPU first).  Idempotent."""
+    """Pack a dict built elsewhere (the reference's own compress, a file) for
+    the kernels, moving CPU / numpy arrays to the GPU first.  Idempotent."""
     if "q16" in c:
         return c
     dev = torch.device(device) if device is not None else (
@@ -98,20 +137,12 @@ def prepare(c, device=None):
         if not torch.is_tensor(v):
             v = torch.as_tensor(v)
         c[k] = v.to(device=dev, dtype=dt).contiguous()
-    N, K, CH = int(c["N"]), int(c["K"]), int(c["CH"])
-    nbytes = lib().rv12_tiles_bytes(N, K)
-    if nbytes == 0:
-        raise ValueError("K must be a positive multiple of 32")
-    tiles = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
-    cod = Codec(_ptr(c["m8"]), _ptr(c["e4"]), _ptr(c["rp"]), _ptr(c["er"]), _ptr(c["ec"]), _ptr(c["ev"]),
-                N, K, CH, int(c["base"]), int(c["er"].numel()))
-    check(lib().rv12_retile(ctypes.byref(cod), _ptr(tiles), nbytes, _stream(dev)), "prepare")
-    c["q16"] = tiles
+    c["q16"] = pack(to_bf16(c))
     return c
 
 
 def compact(c):
-    """Drop m8/e4 (the kernels read only q16 and the exception list)."""
+    """Drop m8/e4 (the kernels read only the packed form)."""
     prepare(c)
     c.pop("m8", None)
     c.pop("e4", None)
@@ -121,16 +152,16 @@ def compact(c):
 def _matrix(c):
     if "q16" not in c:
         prepare(c)
-    t = c["q16"]
-    return Matrix(_ptr(t), _ptr(c["rp"]), _ptr(c["er"]), _ptr(c["ec"]), _ptr(c["ev"]),
-                  int(c["N"]), int(c["K"]), int(c["base"]), int(c["er"].numel()))
+    q = c["q16"]
+    return Matrix(_ptr(q["tiles"]), _ptr(q["rbase"]), _ptr(q["rp"]), _ptr(q["er"]), _ptr(q["ec"]), _ptr(q["ev"]),
+                  int(c["N"]), int(c["K"]), int(q["er"].numel()))
 
 
 def decode_rows(c, first, last, dtype=torch.float32):
     """Rows [first, last) decoded exactly: float32 (as prefill_kernels.decode_rows)
     or bfloat16 (the original bit patterns, NaN payloads included)."""
     m = _matrix(c)
-    dev = c["q16"].device
+    dev = c["q16"]["tiles"].device
     out = torch.empty((last - first, int(c["K"])), dtype=dtype, device=dev)
     f32 = 1 if dtype == torch.float32 else 0
     if dtype not in (torch.float32, torch.bfloat16):

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define RV12_ABI_VERSION 2
+#define RV12_ABI_VERSION 3
 
 enum rv12_status {
     RV12_OK = 0,
@@ -51,16 +51,23 @@ typedef struct rv12_codec {
     int64_t n_exc;
 } rv12_codec;
 
-/* A matrix re-tiled for the kernels (device pointers).  `tiles` holds the
- * weights in the Q16 layout written by rv12_retile(); the exception arrays are
- * the codec's own rp/er/ec/ev (shared, not copied). */
+/* A matrix packed for the kernels (device pointers), written by
+ * rv12_pack_plan() + rv12_pack().  `tiles` holds the weights in the Q16
+ * layout, 12 bytes per 8 weights, with one exponent window per row: row n
+ * keeps the weights whose biased exponent lies in [rbase[n], rbase[n] + 14]
+ * in the tiles, and every other weight in the exception list rp/er/ec/ev (CSR
+ * by row, row-major order, exact float32 values).  The window of each row is
+ * chosen by the reference's rule for a whole matrix
+ * (ramvi/engine/ramvi_engine/kernels/wcomp.py:19-21), so a row of large
+ * weights does not turn into a long exception list. */
 typedef struct rv12_matrix {
-    const uint32_t* tiles;
-    const int32_t* rp;
-    const int32_t* er;
-    const int32_t* ec;
-    const float* ev;
-    int32_t n, k, base;
+    const uint32_t* tiles; /* rv12_tiles_bytes(n, k) bytes */
+    const int32_t* rbase;  /* [n] window start of each row */
+    const int32_t* rp;     /* [n + 1] */
+    const int32_t* er;     /* [n_exc] */
+    const int32_t* ec;     /* [n_exc] */
+    const float* ev;       /* [n_exc] */
+    int32_t n, k;
     int64_t n_exc;
 } rv12_matrix;
 
@@ -87,10 +94,24 @@ const char* rv12_strerror(int status);
 /* Bytes of the Q16 tile layout for W[n, k]: ceil(n/16) * 16 * k * 3 / 2. */
 size_t rv12_tiles_bytes(int n, int k);
 
-/* Re-tile a codec dict into the Q16 layout.  Replaces nothing in the
- * reference (its kernels read m8/e4 directly); called once per matrix after
- * compress(), ramvi/engine/ramvi_engine/core/engine.py:224. */
-int rv12_retile(const rv12_codec* in, uint32_t* tiles, size_t tiles_bytes, void* stream);
+/* Pack a bf16 matrix w[n, k] (bits, row-major, device) for the kernels, in
+ * two device passes with one host step between them:
+ *   rv12_pack_plan  rbase[n] = window start of each row,
+ *                   row_exc[n] = weights of each row outside its window
+ *   (host: rp = [0, cumsum(row_exc)], n_exc = rp[n])
+ *   rv12_pack       tiles (Q16 layout) and the exception list er/ec/ev[n_exc]
+ * Replaces nothing in the reference, whose kernels read m8/e4 directly; run
+ * once per matrix after compress(), ramvi/engine/ramvi_engine/core/engine.py:224. */
+int rv12_pack_plan(const uint16_t* w, int n, int k, int32_t* rbase, int32_t* row_exc, void* stream);
+int rv12_pack(const uint16_t* w, int n, int k, const int32_t* rbase, const int32_t* rp, int64_t n_exc,
+              uint32_t* tiles, size_t tiles_bytes, int32_t* er, int32_t* ec, float* ev, void* stream);
+
+/* The bf16 matrix w[n, k] a codec dict encodes (the inverse of compress(),
+ * bit for bit; the reference's decompress, wcomp.py:35-45, ends with a
+ * .bfloat16() that would also map every NaN payload to one NaN).  Used to
+ * pack a dict that was not built by rv12_encode* (the reference's own
+ * compress, a file). */
+int rv12_codec_to_bf16(const rv12_codec* in, uint16_t* w, void* stream);
 
 /* Encode a bf16 matrix W[n, k] (bits, row-major, device) into the codec dict
  * in three calls, each a device pass with no host synchronisation:

@@ -1,13 +1,13 @@
-"""numpy model of the Q16 tile layout the HIP kernels use (ai_amd/csrc/rv12_kernels.hip).
+"""numpy model of the packed form the HIP kernels read (ai_amd/csrc/rv12_device.h).
 
-Test helper: it restates, in array form, what k_retile writes and what the
-kernels read back, so the layout's arithmetic (pair packing, exponent codes,
-the 2^(base-1) rescale, the exception convention) is checked on the CPU
-against the oracle before any kernel runs.
+Test helper: it restates, in array form, what the pack kernels write and what
+the linear kernels read back, so the layout's arithmetic (row exponent
+windows, pair packing, the 2^sc rescale, the exception convention) is checked
+on the CPU against the oracle before any kernel runs.
 """
 import numpy as np
 
-from oracle.codec import codes
+from oracle.codec import choose_base
 
 M_PAIR = np.uint32(0x87FF87FF)
 
@@ -17,23 +17,33 @@ def scale_exp(base):
     return max(int(base) - 1, 0)
 
 
-def h_values(c):
-    """16-bit h per weight: sign<<15 | c'<<7 | m7 with c' = e - sc for
-    in-window weights (code + 1 when base >= 1, the exponent itself when
-    base == 0) and h = 0 for exceptions."""
-    code = codes(c)
-    m = np.asarray(c["m8"]).astype(np.uint32)
-    sm = ((m >> 7) << 15) | (m & 0x7F)
-    base = int(c["base"])
-    cc = (code + base - scale_exp(base)).astype(np.uint32)
-    h = np.where(code == 15, 0, sm | (cc << 7))
-    return h.astype(np.uint32)
+def row_bases(w_bits):
+    """Window start of each row: the reference's whole-matrix rule (first
+    argmax of the 15-wide window counts) applied to the row."""
+    w = np.asarray(w_bits, np.uint16)
+    e = (w.astype(np.int64) >> 7) & 0xFF
+    return np.array([choose_base(e[n]) for n in range(w.shape[0])], np.int64)
 
 
-def retile(c):
-    """uint32 tiles [nblk, nsteps, 64, 3] as k_retile writes them."""
-    N, K = c["N"], c["K"]
-    h = h_values(c)
+def h_values(w_bits, rbase):
+    """16-bit h per weight: sign<<15 | c<<7 | m7 with c = e - sc of the row
+    for weights inside the row window, h = 0 outside it."""
+    w = np.asarray(w_bits, np.uint16).astype(np.int64)
+    base = np.asarray(rbase, np.int64)[:, None]
+    sc = np.maximum(base - 1, 0)
+    e = (w >> 7) & 0xFF
+    code = e - base
+    inside = (code >= 0) & (code <= 14)
+    h = np.where(inside, (w & 0x807F) | ((e - sc) << 7), 0)
+    return h.astype(np.uint32), ~inside
+
+
+def pack(w_bits):
+    """(tiles [nblk, nsteps, 64, 3] uint32, rbase, rp, er, ec, ev) as the pack kernels write them."""
+    w = np.asarray(w_bits, np.uint16)
+    N, K = w.shape
+    rbase = row_bases(w)
+    h, out = h_values(w, rbase)
     nblk = (N + 15) // 16
     hp = np.zeros((nblk * 16, K), np.uint32)
     hp[:N] = h
@@ -44,7 +54,12 @@ def retile(c):
     d0 = p0 | ((p3 & 0x000F000F) << 11)
     d1 = p1 | ((p3 & 0x00F000F0) << 7)
     d2 = p2 | ((p3 & 0x07000700) << 3) | ((p3 & 0x80008000) >> 1)
-    return np.stack([d0, d1, d2], -1).astype(np.uint32)
+    tiles = np.stack([d0, d1, d2], -1).astype(np.uint32)
+    er, ec = np.nonzero(out)
+    rp = np.zeros(N + 1, np.int32)
+    rp[1:] = np.cumsum(np.bincount(er, minlength=N))
+    ev = (w[er, ec].astype(np.uint32) << 16).view(np.float32)
+    return tiles, rbase, rp, er.astype(np.int32), ec.astype(np.int32), ev
 
 
 def unpack(tiles):
@@ -56,7 +71,7 @@ def unpack(tiles):
 
 
 def h_from_tiles(tiles, N, K):
-    """h [N, K] back from the tiles (inverse of retile's permutation)."""
+    """h [N, K] back from the tiles (inverse of pack's permutation)."""
     nblk = tiles.shape[0]
     p = unpack(tiles)
     g = np.empty(p.shape[:-1] + (8,), np.uint32)
@@ -66,19 +81,31 @@ def h_from_tiles(tiles, N, K):
     return hp[:N]
 
 
-def bf16_from_h(h, base):
-    """original bf16 bits from h (before the exception scatter), as h_to_bf16."""
+def bf16_from_h(h, rbase):
+    """bf16 bits from h (before the exception scatter), as h_to_bf16."""
+    sc = np.maximum(np.asarray(rbase, np.int64) - 1, 0)[:, None]
     cc = (h >> 7) & 15
-    return np.where(cc != 0, (h.astype(np.int64) + (scale_exp(base) << 7)) & 0xFFFF, h).astype(np.uint16)
+    return np.where(cc != 0, (h.astype(np.int64) + (sc << 7)) & 0xFFFF, h).astype(np.uint16)
 
 
-def scaled_dot(c, xp):
-    """sum_k h_k x'_k computed in float64 with h as a float32 value, rescaled by
-    2^sc, plus the exceptions: the kernels' formula in exact arithmetic."""
-    h = h_values(c)
+def decode(tiles, rbase, er, ec, ev, N, K):
+    """The exact bf16 bits of the packed matrix."""
+    bits = bf16_from_h(h_from_tiles(tiles, N, K), rbase)
+    bits[np.asarray(er, np.int64), np.asarray(ec, np.int64)] = (np.asarray(ev, np.float32).view(np.uint32)
+                                                                 >> 16).astype(np.uint16)
+    return bits
+
+
+def scaled_dot(w_bits, xp):
+    """sum_k h_k x'_k in float64 with h read as a float32 value, each row
+    rescaled by 2^sc of its window, plus the row-window exceptions: the
+    kernels' formula in exact arithmetic."""
+    tiles, rbase, rp, er, ec, ev = pack(w_bits)
+    N, K = np.asarray(w_bits).shape
+    h = h_from_tiles(tiles, N, K)
     wh = (h.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
-    y = np.ldexp(xp @ wh.T, scale_exp(c["base"]))
-    er, ec, ev = (np.asarray(c[k]) for k in ("er", "ec", "ev"))
+    sc = np.maximum(rbase - 1, 0)
+    y = np.ldexp(xp @ wh.T, sc[None, :])
     for j in range(er.size):
         y[:, er[j]] += ev[j].astype(np.float64) * xp[:, ec[j]]
     return y

@@ -31,7 +31,7 @@ def test_library_exports_every_symbol():
 def test_abi_version_and_strerror():
     from ai_amd import _lib
     L = _lib.lib()
-    assert L.rv12_abi_version() == 2
+    assert L.rv12_abi_version() == 3
     for s in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -20):
         assert _lib.strerror(s) and _lib.strerror(s) != "unknown rv12 status"
     assert _lib.strerror(-99) == "unknown rv12 status"
@@ -48,10 +48,10 @@ def test_sizes():
     assert L.rv12_workspace_bytes(4096, 4096, 17, 1) == 0
 
 
-def _mat(n=64, k=256, base=100, tiles=0x1000, n_exc=0):
+def _mat(n=64, k=256, tiles=0x1000, n_exc=0, rbase=0x1800):
     from ai_amd import _lib
-    return _lib.Matrix(tiles, 0x2000, 0x3000 if n_exc else 0, 0x4000 if n_exc else 0, 0x5000 if n_exc else 0,
-                       n, k, base, n_exc)
+    return _lib.Matrix(tiles, rbase, 0x2000, 0x3000 if n_exc else 0, 0x4000 if n_exc else 0,
+                       0x5000 if n_exc else 0, n, k, n_exc)
 
 
 def test_gemm_argument_errors():
@@ -69,7 +69,8 @@ def test_gemm_argument_errors():
     assert call(_mat(), xx=None) == _lib.RV12_E_NULL
     assert call(_mat(k=100)) == _lib.RV12_E_SHAPE
     assert call(_mat(n=0)) == _lib.RV12_E_SHAPE
-    assert call(_mat(base=242)) == _lib.RV12_E_BASE
+    assert call(_mat(rbase=0)) == _lib.RV12_E_NULL
+    assert call(_mat(k=1 << 21)) == _lib.RV12_E_SHAPE
     assert call(_mat(), mode=3) == _lib.RV12_E_MODE
     assert call(_mat(), t=0) == _lib.RV12_E_TOKENS
     assert call(_mat(), t=17) == _lib.RV12_E_TOKENS
@@ -91,18 +92,27 @@ def test_gemm_argument_errors():
     assert call(m) == _lib.RV12_E_NULL
 
 
-def test_retile_decode_encode_argument_errors():
+def test_pack_decode_encode_argument_errors():
     from ai_amd import _lib
     L = _lib.lib()
-    cod = _lib.Codec(0x1000, 0x2000, 0x3000, 0, 0, 0, 64, 256, 256, 100, 0)
+    P = ctypes.c_void_p
+    w, rb, rx, rp, tl = P(0x1000), P(0x2000), P(0x3000), P(0x4000), P(0x9000)
     need = L.rv12_tiles_bytes(64, 256)
-    assert L.rv12_retile(None, ctypes.c_void_p(0x9000), need, None) == _lib.RV12_E_NULL
-    assert L.rv12_retile(ctypes.byref(cod), None, need, None) == _lib.RV12_E_NULL
-    assert L.rv12_retile(ctypes.byref(cod), ctypes.c_void_p(0x9000), need - 1, None) == _lib.RV12_E_SIZE
+    assert L.rv12_pack_plan(None, 64, 256, rb, rx, None) == _lib.RV12_E_NULL
+    assert L.rv12_pack_plan(w, 64, 100, rb, rx, None) == _lib.RV12_E_SHAPE
+    assert L.rv12_pack_plan(P(0x1002), 64, 256, rb, rx, None) == _lib.RV12_E_ALIGN
+    assert L.rv12_pack(w, 64, 256, rb, rp, 0, None, need, None, None, None, None) == _lib.RV12_E_NULL
+    assert L.rv12_pack(w, 64, 256, rb, rp, 5, tl, need, None, None, None, None) == _lib.RV12_E_NULL
+    assert L.rv12_pack(w, 64, 256, rb, rp, 0, tl, need - 1, None, None, None, None) == _lib.RV12_E_SIZE
+    assert L.rv12_pack(w, 0, 256, rb, rp, 0, tl, need, None, None, None, None) == _lib.RV12_E_SHAPE
+    cod = _lib.Codec(0x1000, 0x2000, 0x3000, 0, 0, 0, 64, 256, 256, 100, 0)
+    assert L.rv12_codec_to_bf16(ctypes.byref(cod), None, None) == _lib.RV12_E_NULL
     bad = _lib.Codec(0x1000, 0x2000, 0x3000, 0, 0, 0, 64, 256, 24, 100, 0)
-    assert L.rv12_retile(ctypes.byref(bad), ctypes.c_void_p(0x9000), need, None) == _lib.RV12_E_SHAPE
+    assert L.rv12_codec_to_bf16(ctypes.byref(bad), tl, None) == _lib.RV12_E_SHAPE
     bad = _lib.Codec(0x1000, 0x2000, 0x3000, 0, 0, 0, 64, 256, 256, 300, 0)
-    assert L.rv12_retile(ctypes.byref(bad), ctypes.c_void_p(0x9000), need, None) == _lib.RV12_E_BASE
+    assert L.rv12_codec_to_bf16(ctypes.byref(bad), tl, None) == _lib.RV12_E_BASE
+    bad = _lib.Codec(0x1000, 0x2000, 0x3000, 0, 0, 0, 64, 256, 256, 100, 3)
+    assert L.rv12_codec_to_bf16(ctypes.byref(bad), tl, None) == _lib.RV12_E_NULL
     m = _mat()
     out = ctypes.c_void_p(0x40000)
     assert L.rv12_decode_rows(ctypes.byref(m), 5, 3, out, 0, None) == _lib.RV12_E_SHAPE

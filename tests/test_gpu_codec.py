@@ -48,6 +48,24 @@ def test_retile_of_reference_dict_decodes_exactly(golden):
         assert np.array_equal(d, g["w"]), name
 
 
+def test_pack_matches_layout_model(golden):
+    """The device packer writes exactly what the CPU model of the layout
+    (tests/q16_model.py) writes: tiles, row windows and exception list."""
+    import q16_model as q
+    from ai_amd import wcomp
+    for name, g in golden.items():
+        if g["w"].shape[1] % 32:
+            continue
+        print("case", name, flush=True)
+        t, rb, rp, er, ec, ev = q.pack(g["w"])
+        got = wcomp.pack(_w(g["w"]))
+        assert np.array_equal(got["tiles"].cpu().numpy().view(np.uint32), t.reshape(-1)), name
+        assert np.array_equal(got["rbase"].cpu().numpy(), rb), name
+        for k, v in (("rp", rp), ("er", er), ("ec", ec)):
+            assert np.array_equal(got[k].cpu().numpy(), v), (name, k)
+        assert np.array_equal(got["ev"].cpu().numpy().view(np.uint32), ev.view(np.uint32)), name
+
+
 def test_decode_rows_ranges_and_f32(golden):
     from ai_amd import wcomp
     g = golden["outliers_rows_cols"]
@@ -83,6 +101,25 @@ def test_all_bit_patterns_round_trip():
             c = wcomp.compress(ww, CH=min(256, shape[1]))
             d = wcomp.decompress(c)
             assert torch.equal(d.view(torch.int16), ww.view(torch.int16)), shape
+
+
+def test_outlier_rows_stay_out_of_the_packed_exception_list():
+    """0.1% of rows x20: the reference dict holds a fifth of such a row as
+    exceptions, the packed form (one window per row) almost none; both decode
+    exactly."""
+    from ai_amd import wcomp
+    g = torch.Generator(device="cuda").manual_seed(3)
+    N, K = 4096, 4096
+    w = torch.randn(N, K, device="cuda", generator=g) * 0.02
+    rows = torch.randperm(N, device="cuda", generator=g)[:4]
+    w[rows] *= 20
+    w = w.bfloat16()
+    c = wcomp.compress(w)
+    ref_rows = torch.bincount(c["er"].long(), minlength=N)
+    own_rows = torch.diff(c["q16"]["rp"].long())
+    assert int(ref_rows[rows].min()) > 500
+    assert int(own_rows[rows].max()) < 20
+    assert torch.equal(wcomp.decompress(c).view(torch.int16), w.view(torch.int16))
 
 
 def test_large_matrix_round_trip_and_exceptions():
