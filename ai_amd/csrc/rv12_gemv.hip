@@ -13,16 +13,17 @@
 //      which returns zeros without a memory access);
 //   3. the activation loads are waited for (the weight loads stay in flight)
 //      and x' is written to LDS: the MODE / RMS transform, and the sum of
-//      squares for RMS; the workgroup's first round of exceptions is fetched;
-//      one barrier;
+//      squares for RMS; one barrier;
 //   4. main loop: per step each wave decodes 8 weights per lane and row block
 //      and does 8 FMAs per token into fp32 accumulators, and issues the load
 //      kDepth steps ahead;
-//   5. epilogue: lane quarters and waves are summed in a fixed order (no
-//      atomics), rescaled by 2^sc, the exceptions whose column lies in the
-//      split are added (per wave a segmented scan over its slice of the
-//      row-major exception list), and the result is stored (one split) or
-//      written as a partial for k_splitk_reduce.
+//   5. epilogue: one thread per output sums the lane quarters and waves in a
+//      fixed order (no atomics), rescales by 2^sc of its row, adds the
+//      products ev * x' of its row's exceptions whose column lies in the split
+//      (staged per round in LDS, added in list order), and stores the result
+//      (one split) or writes it as a partial for k_splitk_reduce.  The row's
+//      scale, exception range and old y are loaded at the very start, so the
+//      epilogue issues no global load.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -42,9 +43,11 @@ __device__ __forceinline__ void issue_step(u32x3 (&dst)[RB], __amdgpu_buffer_rsr
 
 // NXM = float4 chunks of activations per thread loaded in step 1, before the
 // weight prefetch; columns beyond 4 * NXM * blockDim.x are staged after it.
+// The host guarantees blockDim.x >= 16 * RB * T (one thread per output).
 template <int T, int RB>
 __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p) {
     constexpr int NXM = gemv_chunks(T);
+    constexpr int NO = RB * 16 * T;  // outputs of the workgroup
     extern __shared__ float smem[];
     const int W = blockDim.x >> 6;
     const int nthr = blockDim.x;
@@ -59,10 +62,29 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     const int64_t nblk = (p.N + 15) / 16;
     const int nvalid = (int)min((int64_t)RB, nblk - blk0);
 
-    float* xl = smem;                      // [T][krange]
-    float* red = xl + T * krange;          // [W][RB][T][16]
-    float* exc = red + W * RB * T * 16;    // [W][RB*16][T]
-    float* ssq = exc + W * RB * 16 * T;    // [W][T]
+    float* xl = smem;                    // [T][krange]
+    float* red = xl + T * krange;        // [W][RB][T][16]
+    float* excv = red + W * RB * T * 16; // [nthr][T] exception products of one round
+    float* ssq = excv + nthr * T;        // [W][T]
+
+    // ---- 0. what the epilogue needs, loaded first: thread i < NO owns output
+    // (row n0 + i % (16 RB), token i / (16 RB)): its row's scale exponent and
+    // exception range, and y for an accumulating single-split launch
+    const bool owner = threadIdx.x < NO;
+    const int orow = threadIdx.x % (RB * 16), otok = threadIdx.x / (RB * 16);
+    const int on = n0 + orow;
+    const bool oval = owner && on < p.N;
+    int obase = 0;  // used only in the epilogue, so this load does not stall the prologue
+    int32_t oe0 = 0, oe1 = 0;
+    float oy = 0.0f;
+    if (oval) {
+        obase = p.rbase[on];
+        if (p.n_exc > 0) {
+            oe0 = p.rp[on];
+            oe1 = p.rp[on + 1];
+        }
+        if (S == 1 && p.mode != 0) oy = p.y[(int64_t)otok * p.N + on];
+    }
 
     // ---- 1. activations of this thread
     f32x4 xr[NXM][T], ur[NXM][T];
@@ -94,6 +116,21 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     u32x3 buf[kDepth][RB];
 #pragma unroll
     for (int u = 0; u < kDepth; ++u) issue_step<RB>(buf[u], rv, rnull, voff, s0 + u * W, s_hi);
+
+    // the workgroup's first round of exceptions, one entry per thread (after
+    // the weight loads: these wait for a scalar load of the row pointers)
+    int32_t e_lo = 0, e_hi = 0;
+    int ec0 = 0;
+    float ev0 = 0.0f;
+    if (p.n_exc > 0) {
+        e_lo = p.rp[n0];
+        e_hi = p.rp[min(n0 + RB * 16, p.N)];
+        const int32_t j = e_lo + threadIdx.x;
+        if (j < e_hi) {
+            ec0 = p.ec[j];
+            ev0 = p.ev[j];
+        }
+    }
 
     // ---- 3. x' into LDS
     float sq[T];
@@ -143,29 +180,12 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
             *reinterpret_cast<f32x4*>(xl + t * krange + i) = v;
         }
     }
-    for (int i = threadIdx.x; i < W * RB * 16 * T; i += nthr) exc[i] = 0.0f;
     if (p.lnw) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             float v = sq[t];
             for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
             if (lane == 0) ssq[wave * T + t] = v;
-        }
-    }
-    // this wave's 64-entry slice of the first round of the workgroup's
-    // exceptions; the values are first used after the main loop, so these
-    // loads do not hold up the barrier
-    int32_t e_lo = 0, e_hi = 0;
-    int er0 = 0, ec0 = 0;
-    float ev0 = 0.0f;
-    if (p.n_exc > 0) {
-        e_lo = p.rp[n0];
-        e_hi = p.rp[min(n0 + RB * 16, p.N)];
-        const int32_t j = e_lo + wu * 64 + lane;
-        if (j < e_hi) {
-            er0 = p.er[j];
-            ec0 = p.ec[j];
-            ev0 = p.ev[j];
         }
     }
     __syncthreads();
@@ -214,7 +234,7 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
         }
     }
 
-    // ---- 5. epilogue: lane quarters, then waves
+    // ---- 5. epilogue: lane quarters to LDS (waves are summed by the owners)
 #pragma unroll
     for (int b = 0; b < RB; ++b)
 #pragma unroll
@@ -225,82 +245,62 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
             if (lane < 16) red[((wave * RB + b) * T + t) * 16 + lane] = v;
         }
 
-    // exceptions of this workgroup's rows with a column inside the split:
-    // rounds of W*64 entries, wave w takes entries [w*64, w*64+64) of each
-    float* excw = exc + wave * RB * 16 * T;
-    for (int32_t j0 = e_lo; j0 < e_hi; j0 += W * 64) {
-        const int32_t j = j0 + wu * 64 + lane;
-        const bool valid = j < e_hi;
-        int r = 0x7FFFFFFF, c = 0;
-        float v = 0.0f;
-        if (j0 == e_lo) {
-            if (valid) {
-                r = er0 - n0;
-                c = ec0;
-                v = ev0;
-            }
-        } else if (valid) {
-            r = p.er[j] - n0;
-            c = p.ec[j];
-            v = p.ev[j];
+    // exception products ev * x' of one round of nthr entries of the
+    // workgroup's row-major exception list (zero outside the split's columns);
+    // each owner adds its row's entries in list order
+    auto stage_round = [&](int32_t j0, int c, float v) {
+        const int32_t j = j0 + threadIdx.x;
+        c -= k_lo;
+        const bool in = j < e_hi && c >= 0 && c < krange;
+#pragma unroll
+        for (int t = 0; t < T; ++t) excv[threadIdx.x * T + t] = in ? v * xl[t * krange + c] : 0.0f;
+    };
+    float eacc = 0.0f;
+    auto add_round = [&](int32_t j0) {
+        if (oval) {
+            const int32_t a = max(oe0, j0), z = min(oe1, j0 + nthr);
+            for (int32_t j = a; j < z; ++j) eacc += excv[(j - j0) * T + otok];
         }
-        if (__builtin_amdgcn_readfirstlane(j0 + wu * 64) < e_hi) {  // this wave has entries
-            float pv[T];
-            c -= k_lo;
-            const bool in = valid && c >= 0 && c < krange;
-#pragma unroll
-            for (int t = 0; t < T; ++t) pv[t] = in ? v * xl[t * krange + c] : 0.0f;
-            for (int d = 1; d < 64; d <<= 1) {
-                const int rn = __shfl_up(r, d);
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    const float o = __shfl_up(pv[t], d);
-                    if (lane >= d && rn == r) pv[t] += o;
-                }
-            }
-            const int rnext = __shfl_down(r, 1);
-            if (valid && (lane == 63 || rnext != r)) {
-#pragma unroll
-                for (int t = 0; t < T; ++t) excw[r * T + t] += pv[t];
-            }
-        }
-    }
+    };
+    if (e_lo < e_hi) stage_round(e_lo, ec0, ev0);
     __syncthreads();
-
-    float rs[T];
-#pragma unroll
-    for (int t = 0; t < T; ++t) rs[t] = 1.0f;
-    if (p.lnw && S == 1) {
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            float v = 0.0f;
-            for (int w = 0; w < W; ++w) v += ssq[w * T + t];
-            rs[t] = 1.0f / sqrtf(v / (float)p.K + p.eps);
-        }
+    float v = 0.0f;
+    if (owner) {
+        const int b = orow >> 4, l16 = orow & 15;
+        for (int w = 0; w < W; ++w) v += red[((w * RB + b) * T + otok) * 16 + l16];
     }
-    for (int idx = threadIdx.x; idx < RB * 16 * T; idx += nthr) {
-        const int r = idx % (RB * 16), t = idx / (RB * 16);
-        const int b = r >> 4, l16 = r & 15;
-        float v = 0.0f;
-        for (int w = 0; w < W; ++w) v += red[((w * RB + b) * T + t) * 16 + l16];
-        float e = 0.0f;
-        for (int w = 0; w < W; ++w) e += exc[(w * RB * 16 + r) * T + t];
-        const int n = n0 + r;
-        if (n < p.N) {
-            v = ldexpf(v, scale_exp(p.rbase[n])) + e;
-            if (S == 1) {
-                float* y = p.y + (int64_t)t * p.N + n;
-                if (p.lnw) v *= rs[t];
-                *y = p.mode == 0 ? v : *y + v;
-            } else {
-                p.part[((int64_t)sp * T + t) * p.npad + n] = v;
+    if (e_lo < e_hi) add_round(e_lo);
+    for (int32_t j0 = e_lo + nthr; j0 < e_hi; j0 += nthr) {  // rare: more entries than threads
+        __syncthreads();
+        const int32_t j = j0 + threadIdx.x;
+        int c = 0;
+        float ev = 0.0f;
+        if (j < e_hi) {
+            c = p.ec[j];
+            ev = p.ev[j];
+        }
+        stage_round(j0, c, ev);
+        __syncthreads();
+        add_round(j0);
+    }
+
+    if (oval) {
+        v = ldexpf(v, scale_exp(obase)) + eacc;
+        if (S == 1) {
+            if (p.lnw) {
+                float sqs = 0.0f;
+                for (int w = 0; w < W; ++w) sqs += ssq[w * T + otok];
+                v *= 1.0f / sqrtf(sqs / (float)p.K + p.eps);
             }
+            p.y[(int64_t)otok * p.N + on] = p.mode == 0 ? v : oy + v;
+        } else {
+            p.part[((int64_t)sp * T + otok) * p.npad + on] = v;
         }
     }
     if (S > 1 && p.lnw && blockIdx.x == 0 && threadIdx.x < T) {
-        float v = 0.0f;
-        for (int w = 0; w < W; ++w) v += ssq[w * T + threadIdx.x];
-        p.ssq[sp * T + threadIdx.x] = v;
+        float sqs = 0.0f;
+        for (int w = 0; w < W; ++w) sqs += ssq[w * T + threadIdx.x];
+        p.ssq[sp * T + threadIdx.x] = sqs;
     }
 }
 

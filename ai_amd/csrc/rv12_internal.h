@@ -47,15 +47,16 @@ __host__ __device__ constexpr int gemv_chunks(int T) { return T == 1 ? 6 : (T ==
 
 inline size_t gemv_lds_bytes(int K, int T, int rb, int waves, int splits) {
     const size_t krange = (size_t)split_steps(K, splits) * 32;
-    return 4 * ((size_t)T * krange + (size_t)waves * rb * T * 16 + (size_t)waves * rb * 16 * T + (size_t)waves * T);
+    return 4 * ((size_t)T * krange + (size_t)waves * rb * T * 16 + (size_t)waves * 64 * T + (size_t)waves * T);
 }
 
 // waves per workgroup the kernel is built for (its register budget)
-__host__ __device__ constexpr int gemv_max_waves(int rb) { return rb == 4 ? 8 : 16; }
+__host__ __device__ constexpr int gemv_max_waves(int rb) { return rb == 1 ? 16 : 8; }
 
 // launch shape fits the kernel's register budget and LDS
 inline bool gemv_fits(int K, int T, int rb, int waves, int splits) {
-    return waves <= gemv_max_waves(rb) && gemv_lds_bytes(K, T, rb, waves, splits) <= kMaxLds;
+    return waves <= gemv_max_waves(rb) && waves * 64 >= rb * 16 * T &&
+           gemv_lds_bytes(K, T, rb, waves, splits) <= kMaxLds;
 }
 
 // every activation column of the split is loaded before the weight prefetch

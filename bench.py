@@ -29,6 +29,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM = 8000.0  # GB/s, MI355X HBM3E
+# HBM bytes per launch of the dominant kernel (vector-FMA linear over the 144
+# layer matrices of a Qwen3-8B token, mean per launch) from the rocprofv3
+# FETCH_SIZE and WRITE_SIZE counters, each scaled by what it reads for a 1 GiB
+# device copy (--copy-calibration): profiles/k_gemv_qwen3-8b_token.md
+TRAFFIC_BYTES_PER_LAUNCH = 73320227
 D, FF, L, V = 4096, 12288, 36, 151936
 QKV = (32 + 2 * 8) * 128
 LAYER = [("qkv", QKV, D, 0, True), ("o", D, 32 * 128, 1, False), ("gu", 2 * FF, D, 0, True),
@@ -111,8 +116,8 @@ def build_model(dev, seed=0):
     return layers, head
 
 
-def token_linears(layers, head, bufs):
-    """The 4 x 36 + 1 launches of one decode token, in engine order
+def token_linears(layers, head, bufs, with_head=True):
+    """The 4 x 36 (+ 1) launches of one decode token, in engine order
     (ramvi/engine/ramvi_engine/core/engine.py:335-340)."""
     from ai_amd import wcomp
     x, qkv, att, gu, ln, logits = bufs["x"], bufs["qkv"], bufs["att"], bufs["gu"], bufs["ln"], bufs["logits"]
@@ -121,10 +126,15 @@ def token_linears(layers, head, bufs):
         wcomp.gemvc1(att, lay["o"], x, 1)
         wcomp.gemvc1(x, lay["gu"], gu, 0, lnw=ln)
         wcomp.gemvc1(gu, lay["down"], x, 2)
-    wcomp.gemvc1(x, head, logits, 0)
+    if with_head:
+        wcomp.gemvc1(x, head, logits, 0)
 
 
 def run_token_bench(args, dev):
+    """Two graphs over the same resident weights: the whole token (145
+    launches: value, tok/s) and the 144 layer launches alone, which are all
+    the dominant kernel (vector-FMA linear, one row block per workgroup): the
+    roofline figure is its algorithmic bytes over its measured time."""
     layers, head = build_model(dev)
     g = torch.Generator(device=dev).manual_seed(1)
     rnd = lambda n: torch.randn(n, device=dev, generator=g).bfloat16().float()
@@ -133,18 +143,37 @@ def run_token_bench(args, dev):
             "logits": torch.zeros(V, device=dev)}
     x0 = bufs["x"].clone()
 
-    def step():
-        bufs["x"].copy_(x0)  # keep the residual stream bounded across replays
-        token_linears(layers, head, bufs)
+    def step(with_head=True):
+        bufs["x"].copy_(x0)  # keep the residual stream the same on every replay
+        token_linears(layers, head, bufs, with_head)
 
     graph = Graph(step)
     cb = sum(comp_bytes(lay[n]) for lay in layers for n, *_ in LAYER) + comp_bytes(head)
-    ab = sum(alg_bytes(lay[n], m, r) for lay in layers for n, _, _, m, r in LAYER) + alg_bytes(head, 0, False)
+    ab_layers = sum(alg_bytes(lay[n], m, r) for lay in layers for n, _, _, m, r in LAYER)
+    ab = ab_layers + alg_bytes(head, 0, False)
     for _ in range(args.warmup):
         graph.replay()
     torch.cuda.synchronize()
     ms = time_graph(graph, args.steps, warm=0)
-    return {"ms": ms, "comp_bytes": cb, "alg_bytes": ab, "layers": layers, "head": head, "bufs": bufs}
+    del graph
+    lgraph = Graph(lambda: step(False))
+    ms_layers = time_graph(lgraph, args.steps, warm=args.warmup)
+    del lgraph
+    return {"ms": ms, "comp_bytes": cb, "alg_bytes": ab, "ms_layers": ms_layers, "alg_bytes_layers": ab_layers,
+            "launches_layers": 4 * L, "layers": layers, "head": head, "bufs": bufs}
+
+
+def copy_calibration(dev, reps=20):
+    """A plain 1 GiB device copy (torch's copy kernel), for scaling the HBM
+    byte counters: FETCH_SIZE and WRITE_SIZE of this kernel should each read
+    1 GiB per launch."""
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": 4 * n, "launches": reps}), flush=True)
 
 
 def run_shape(name, reps, dev, min_bytes=1.2e9):
@@ -224,6 +253,8 @@ def main():
     ap.add_argument("--reps", type=int, default=20, help="graph replays per sweep shape")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a 1 GiB device copy (scale factor of the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the 12-bit decode-linear runs on a single MI355X "
@@ -234,6 +265,9 @@ def main():
     from ai_amd import _lib
     _lib.lib()
 
+    if args.copy_calibration:
+        copy_calibration(dev)
+        return
     if args.only:
         r = run_shape(args.only, args.reps, dev)
         print(json.dumps(r), flush=True)
@@ -242,9 +276,10 @@ def main():
     tok = run_token_bench(args, dev)
     ms = tok["ms"]
     value = tok["comp_bytes"] / ms / 1e6
-    achieved_alg = tok["alg_bytes"] / ms / 1e6
-    print(f"# token linears: {ms:.3f} ms, {value:.0f} GB/s compressed, {achieved_alg:.0f} GB/s algorithmic",
-          file=sys.stderr, flush=True)
+    achieved_alg = tok["alg_bytes_layers"] / tok["ms_layers"] / 1e6
+    us_launch = tok["ms_layers"] * 1e3 / tok["launches_layers"]
+    print(f"# token linears: {ms:.3f} ms, {value:.0f} GB/s compressed; layer launches {us_launch:.2f} us avg, "
+          f"{achieved_alg:.0f} GB/s algorithmic", file=sys.stderr, flush=True)
     del tok["layers"], tok["head"]
     torch.cuda.empty_cache()
 
@@ -276,8 +311,10 @@ def main():
                    "tokens": 1, "compressed_GB_per_step": round(tok["comp_bytes"] / 1e9, 4)},
         "linear_only_tok_s": round(1e3 / ms, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved_alg, 2), "peak": PEAK_HBM, "unit": "GB/s",
-                     "frac": round(achieved_alg / PEAK_HBM, 4), "traffic": None,
-                     "kernel": "k_linear (T=1) over the 145 matrices of one step, launch gaps included"},
+                     "frac": round(achieved_alg / PEAK_HBM, 4), "traffic": TRAFFIC_BYTES_PER_LAUNCH,
+                     "kernel": "k_gemv<1,1> (vector-FMA linear, 1 token): the 144 layer launches of one token",
+                     "avg_launch_us": round(us_launch, 3),
+                     "alg_bytes_per_launch": round(tok["alg_bytes_layers"] / tok["launches_layers"])},
         "cpu_baseline": cpu,
         "sweep_m1": sweep,
     }
