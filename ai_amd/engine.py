@@ -1,0 +1,230 @@
+"""Qwen3 greedy decoding on the 12-bit decode-linear: the reference engine's
+call contract for the path (ramvi/engine/ramvi_engine/core/engine.py).
+
+For every layer the four fused matrices are compressed once (engine.py:223-224)
+and a token runs them exactly as the reference's `_gpu_layer` does
+(engine.py:329-341):
+
+    gemvc1(x,   W.qkv,  qkv, 0, lnw=ln1)      RMSNorm fused in the prologue
+    q/k head norms, RoPE, KV write, attention  (torch here; tkernels.py:164-213)
+    gemvc1(att, W.o,    x,   1)               residual accumulate
+    gemvc1(x,   W.gu,   gu,  0, lnw=ln2)
+    gemvc1(gu,  W.down, x,   2)               silu(g) * u prologue, accumulate
+
+and 2..16 tokens of one sequence as `_batch_layer` does (engine.py:344-356),
+RMSNorm separately and `gemvc_tc` for the four matrices.  The lm_head runs
+through the same 12-bit linear with the final norm fused (new: the reference
+picks greedy tokens with an int8 bound pass and exact CPU rows,
+ramvi/engine/ramvi_engine/generation/head.py:29-88), followed by argmax, the
+smallest id on ties (head.py:76-79).
+
+A decode step is one HIP graph (the reference captures one per batch bucket,
+engine.py:432-444): the embedding row of the current token, all layers, the
+head, argmax, and the bookkeeping (next token becomes the input, position and
+output counter advance) run on the device, so the host only replays the graph.
+Attention, RoPE and the norms are plain torch with fixed shapes (the whole
+cache length, masked beyond the position) so that they can be captured; they
+are the companions of the path, not its subject.
+"""
+import torch
+
+from . import wcomp
+
+MATS = ("qkv", "o", "gu", "down")
+BATCH = 16  # largest batch of one pass, as the reference's graph buckets (engine.py:31)
+
+
+def _rms(x, w, eps):
+    return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+
+
+def _rot(t):
+    h = t.shape[-1] // 2
+    return torch.cat([-t[..., h:], t[..., :h]], -1)
+
+
+class Engine:
+    """Greedy Qwen3 decoding with every linear on the MI355X 12-bit path.
+
+    ck        checkpoint object (ai_amd.model.Ckpt / RandomCkpt)
+    maxt      context length of the KV cache
+    kv_dtype  dtype of the KV cache (the reference keeps float32,
+              engine.py:234-235; bfloat16 halves its traffic)
+    """
+
+    def __init__(self, ck, maxt=2048, kv_dtype=torch.float32, device="cuda", log=None):
+        self.ck = ck
+        self.L, self.D, self.H, self.KV, self.HD, self.FF, self.eps = ck.L, ck.D, ck.H, ck.KV, ck.HD, ck.FF, ck.eps
+        self.V, self.maxt, self.kv_dtype = ck.V, maxt, kv_dtype
+        dev = self.dev = torch.device(device)
+        H, KV, HD = self.H, self.KV, self.HD
+        self.inv = (1.0 / (ck.theta ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)  # engine.py:204
+        self.emb = ck.t("model.embed_tokens.weight", dev)
+        self.W, self.small, self.Kc, self.Vc = [], [], [], []
+        for i in range(self.L):
+            w = ck.layer(i, dev)
+            self.small.append({k: w[k] for k in ("ln1", "ln2")} | {k: w[k].float() for k in ("qn", "kn")})
+            self.W.append({n: wcomp.compact(wcomp.compress(w[n])) for n in MATS})
+            self.Kc.append(torch.zeros(KV, maxt, HD, dtype=kv_dtype, device=dev))
+            self.Vc.append(torch.zeros_like(self.Kc[-1]))
+            del w
+            if log:
+                log(f"layer {i + 1}/{self.L} compressed")
+        self.norm = ck.t("model.norm.weight", dev)
+        self.normf = self.norm.float()
+        self.head = wcomp.compact(wcomp.compress(ck.t(ck.head_name(), dev)))
+        torch.cuda.empty_cache()
+        f = lambda n: torch.zeros(BATCH, n, device=dev)
+        self.xb, self.hb, self.qkvb, self.attb, self.gub = f(self.D), f(self.D), f((H + 2 * KV) * HD), f(H * HD), f(
+            2 * self.FF)
+        self.logits = f(self.V)
+        self.pos = torch.zeros(1, dtype=torch.long, device=dev)
+        self.tok = torch.zeros(BATCH, dtype=torch.long, device=dev)
+        self.nxt = torch.zeros(BATCH, dtype=torch.long, device=dev)
+        self.steps = torch.zeros(1, dtype=torch.long, device=dev)
+        self.out = torch.zeros(maxt + 1, dtype=torch.long, device=dev)
+        self.ar = torch.arange(maxt, device=dev)
+        self.graph = None
+
+    # ---------------------------------------------------------------- layers
+    def _rope_attn(self, l, T):
+        """Rows 0..T-1 of qkv at positions pos..pos+T-1: q/k head RMSNorm,
+        RoPE, K/V into the cache (rounded to its dtype), causal attention over
+        the cache (tkernels.py:82-150, 164-213)."""
+        H, KV, HD = self.H, self.KV, self.HD
+        G = H // KV
+        qkv = self.qkvb[:T]
+        q = _rms(qkv[:, :H * HD].view(T, H, HD), self.small[l]["qn"], self.eps)
+        k = _rms(qkv[:, H * HD:(H + KV) * HD].view(T, KV, HD), self.small[l]["kn"], self.eps)
+        v = qkv[:, (H + KV) * HD:].view(T, KV, HD)
+        p = self.pos + self.ar[:T]
+        ang = p[:, None].float() * self.inv[None]
+        e = torch.cat([ang, ang], -1)
+        cos, sin = e.cos()[:, None], e.sin()[:, None]
+        q = q * cos + _rot(q) * sin
+        k = k * cos + _rot(k) * sin
+        Kc, Vc = self.Kc[l], self.Vc[l]
+        Kc.index_copy_(1, p, k.to(self.kv_dtype).transpose(0, 1))
+        Vc.index_copy_(1, p, v.to(self.kv_dtype).transpose(0, 1))
+        Kf, Vf = Kc.float(), Vc.float()
+        qg = q.view(T, KV, G, HD).permute(1, 2, 0, 3).reshape(KV, G * T, HD)
+        sc = torch.bmm(Kf, qg.transpose(1, 2).contiguous()).transpose(1, 2)  # [KV, G*T, maxt]
+        sc = sc.reshape(KV, G, T, self.maxt) * HD ** -0.5
+        sc = sc.masked_fill(self.ar[None, None, None, :] > p[None, None, :, None], float("-inf"))
+        a = torch.softmax(sc, -1).reshape(KV, G * T, self.maxt)
+        o = torch.bmm(a, Vf).view(KV, G, T, HD).permute(2, 0, 1, 3).reshape(T, H * HD)
+        self.attb[:T].copy_(o)
+
+    def _gpu_layer(self, l, x, T):
+        """engine.py:329-341: one token with the RMS prologues fused, else the batched layer."""
+        if T > 1:
+            return self._batch_layer(l, x, T)
+        W, s = self.W[l], self.small[l]
+        wcomp.gemvc1(x, W["qkv"], self.qkvb[:1], 0, lnw=s["ln1"], eps=self.eps)
+        self._rope_attn(l, 1)
+        wcomp.gemvc1(self.attb[:1], W["o"], x, 1)
+        wcomp.gemvc1(x, W["gu"], self.gub[:1], 0, lnw=s["ln2"], eps=self.eps)
+        wcomp.gemvc1(self.gub[:1], W["down"], x, 2)
+
+    def _batch_layer(self, l, x, T):
+        """engine.py:344-356: T <= 16 tokens of one sequence."""
+        W, s = self.W[l], self.small[l]
+        h = self.hb[:T]
+        h.copy_(_rms(x, s["ln1"].float(), self.eps))
+        wcomp.gemvc_tc(h, W["qkv"], self.qkvb[:T], 0, T)
+        self._rope_attn(l, T)
+        wcomp.gemvc_tc(self.attb[:T], W["o"], x, 1, T)
+        h.copy_(_rms(x, s["ln2"].float(), self.eps))
+        wcomp.gemvc_tc(h, W["gu"], self.gub[:T], 0, T)
+        wcomp.gemvc_tc(self.gub[:T], W["down"], x, 2, T)
+
+    def _layers(self, x, T):
+        for l in range(self.L):
+            self._gpu_layer(l, x, T)
+
+    def _head_row(self, x1):
+        """Greedy id of one row: the final norm fused into the 12-bit lm_head,
+        then argmax (first maximum = smallest id)."""
+        wcomp.gemvc1(x1, self.head, self.logits[:1], 0, lnw=self.norm, eps=self.eps)
+        self.nxt[:1].copy_(torch.argmax(self.logits[:1], -1))
+
+    # ---------------------------------------------------------------- passes
+    def _embed(self, T):
+        self.xb[:T].copy_(self.emb.index_select(0, self.tok[:T]).float())
+
+    def _step(self):
+        """One decode step, all on the device (graph body)."""
+        self._embed(1)
+        self._layers(self.xb[:1], 1)
+        self._head_row(self.xb[:1])
+        self.out.index_copy_(0, self.steps, self.nxt[:1])
+        self.tok[:1].copy_(self.nxt[:1])
+        self.pos.add_(1)
+        self.steps.add_(1)
+
+    def reset(self):
+        for c in self.Kc + self.Vc:
+            c.zero_()
+        self.pos.zero_()
+        self.steps.zero_()
+        self.out.zero_()
+
+    def capture(self):
+        """Record the decode step as a HIP graph: two eager warm passes on a
+        side stream (workspaces get allocated, engine.py:432-444), then the
+        capture; the state they touched is reset."""
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                self._step()
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._step()
+        torch.cuda.synchronize()
+        self.graph = g
+        self.reset()
+
+    def prefill(self, tokens):
+        """Prompt tokens at positions 0.. in passes of up to 16 (the reference's
+        chunked prefill, engine.py:471-480); returns the greedy id after the
+        last one (left in self.nxt[0])."""
+        P = len(tokens)
+        if not 1 <= P < self.maxt:
+            raise ValueError("prompt must fit the context")
+        t = torch.tensor(tokens, dtype=torch.long, device=self.dev)
+        for c0 in range(0, P, BATCH):
+            T = min(BATCH, P - c0)
+            self.pos.fill_(c0)
+            self.tok[:T].copy_(t[c0:c0 + T])
+            self._embed(T)
+            self._layers(self.xb[:T], T)
+        last = (P - 1) % BATCH
+        self._head_row(self.xb[last:last + 1])
+        self.pos.fill_(P)
+        return self.nxt[:1]
+
+    def generate(self, prompt, max_new, timing=False):
+        """Greedy ids of `max_new` tokens after `prompt`.  With timing=True also
+        (prefill ms, decode ms for the max_new - 1 graph replays)."""
+        if len(prompt) + max_new > self.maxt:
+            raise ValueError("prompt + max_new exceed the context")
+        if self.graph is None:
+            self.capture()
+        self.reset()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        first = self.prefill(prompt)
+        self.out[:1].copy_(first)
+        self.tok[:1].copy_(first)
+        self.steps.fill_(1)
+        e[1].record()
+        for _ in range(max_new - 1):
+            self.graph.replay()
+        e[2].record()
+        torch.cuda.synchronize()
+        ids = self.out[:max_new].tolist()
+        if timing:
+            return ids, e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
+        return ids

@@ -194,11 +194,22 @@ def _launch(BN, w, S, T):
     return Launch(0, rb, int(w or 0), int(S or 0))
 
 
+_SK_RETIRED = []  # workspaces replaced by larger ones: kept alive for graphs that captured them
+
+
 def _sk_buf(N, S, dev, K=None, T=16):
-    """Workspace for split partial sums, cached per (N, device) (wcomp.py:226-230)."""
-    need = lib().rv12_workspace_bytes(int(N), int(K or 32 * max(S, 1)), int(T), int(S))
+    """Workspace for split partial sums, cached per (N, device) (wcomp.py:226-230).
+    Sized, as the reference's, for 16 tokens and at least 8 splits, so one
+    buffer serves every batch size; a buffer that must grow is retired, not
+    freed, because a captured HIP graph may still hold its address."""
+    L = lib()
+    K = int(K or 32 * max(S, 1))
+    need = max(L.rv12_workspace_bytes(int(N), K, int(T), int(S)), L.rv12_workspace_bytes(int(N), K, 16, 0),
+               L.rv12_workspace_bytes(int(N), K, 16, min(max(int(S), 8), K // 32)))
     k = (N, str(dev))
     if k not in _SK or _SK[k].numel() < need:
+        if k in _SK:
+            _SK_RETIRED.append(_SK[k])
         _SK[k] = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
     return _SK[k]
 
