@@ -176,6 +176,28 @@ def copy_calibration(dev, reps=20):
     print(json.dumps({"copy_bytes": 4 * n, "launches": reps}), flush=True)
 
 
+def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0):
+    """Greedy decode of a random-init Qwen3 (BASELINE config 3 for 8b: a
+    2048-token random-id prompt, 256 new tokens, bf16 KV cache): decode-only
+    tok/s from the graph replays after the prefill."""
+    from ai_amd.engine import Engine
+    from ai_amd.model import QWEN3, RandomCkpt
+    ck = RandomCkpt(QWEN3[size], seed=seed)
+    t0 = time.time()
+    eng = Engine(ck, maxt=prompt_len + new, kv_dtype=torch.bfloat16)
+    load_s = time.time() - t0
+    prompt = [int(t) for t in np.random.default_rng(seed).integers(0, ck.V, prompt_len)]
+    eng.generate(prompt[:64], 8)  # capture + warm
+    ids, prefill_ms, decode_ms = eng.generate(prompt, new, timing=True)
+    per_tok = decode_ms / (new - 1)
+    out = {"model": f"qwen3-{size} random init", "prompt": prompt_len, "new_tokens": new, "kv_cache": "bf16",
+           "tok_s": round(1e3 / per_tok, 2), "ms_per_token": round(per_tok, 4), "prefill_ms": round(prefill_ms, 1),
+           "load_s": round(load_s, 1), "first_ids": ids[:8]}
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_shape(name, reps, dev, min_bytes=1.2e9):
     """Config-2 sweep entry: one shape, distinct copies totalling > 1 GB
     replayed round-robin from a graph; ms per launch."""
@@ -253,6 +275,7 @@ def main():
     ap.add_argument("--reps", type=int, default=20, help="graph replays per sweep shape")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the Qwen3-8B end-to-end decode")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (scale factor of the HBM byte counters)")
     args = ap.parse_args()
@@ -291,6 +314,12 @@ def main():
                   file=sys.stderr, flush=True)
             sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
 
+    e2e = None
+    if not args.no_e2e:
+        e2e = run_e2e(dev)
+        print(f"# qwen3-8b decode: {e2e['tok_s']} tok/s ({e2e['ms_per_token']} ms/token), prefill "
+              f"{e2e['prefill_ms']} ms for {e2e['prompt']} tokens", file=sys.stderr, flush=True)
+
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": "Qwen3-8B bs1 decode tok/s; fused GEMV effective HBM GB/s vs peak",
@@ -315,6 +344,7 @@ def main():
                      "kernel": "k_gemv<1,1> (vector-FMA linear, 1 token): the 144 layer launches of one token",
                      "avg_launch_us": round(us_launch, 3),
                      "alg_bytes_per_launch": round(tok["alg_bytes_layers"] / tok["launches_layers"])},
+        "e2e_decode": e2e,
         "cpu_baseline": cpu,
         "sweep_m1": sweep,
     }

@@ -172,3 +172,22 @@ def test_lm_head_full_size():
     assert float((err / (np.abs(ref) + 1.0)).max()) < 1e-4
     del cg
     torch.cuda.empty_cache()
+
+
+def test_tuned_launch_shapes_keep_parity(tmp_path):
+    """tune() fills CFG1 / CFGT on the GPU; the linears then run with those
+    launch shapes and still match the closed form."""
+    from ai_amd import tune, wcomp
+    N, K = 1024, 1024
+    tune.tune([(N, K, 0), (N, K, 2)], log=lambda *a: None, cache=str(tmp_path / "tune.json"))
+    try:
+        assert (N, K, 0) in wcomp.CFG1 and (N, K, 2) in wcomp.CFGT
+        bits = _random_matrix(N, K, 5, out_rows=0.01)
+        cnp = codec.compress(bits)
+        cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+        for mode in (0, 2):
+            _check(cnp, cg, 1, mode, False, 21)
+            _check(cnp, cg, 16, mode, False, 22, use_tc=True)
+    finally:
+        wcomp.CFG1.clear()
+        wcomp.CFGT.clear()
