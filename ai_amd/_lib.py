@@ -21,7 +21,7 @@ RV12_E_LAUNCH = -20
 # every symbol include/rv12.h declares
 EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_pack_plan", "rv12_pack",
            "rv12_codec_to_bf16", "rv12_encode_stats", "rv12_encode", "rv12_encode_exc", "rv12_workspace_bytes",
-           "rv12_gemv", "rv12_gemm", "rv12_decode_rows")
+           "rv12_gemv", "rv12_gemm", "rv12_decode_rows", "rv12_attn_workspace_bytes", "rv12_rope_attn")
 ABI_VERSION = 3
 
 
@@ -44,6 +44,12 @@ class Launch(ctypes.Structure):
 
 
 KERNEL_VECTOR, KERNEL_MFMA = 1, 2
+
+
+class Attn(ctypes.Structure):
+    _fields_ = [("n_heads", ctypes.c_int32), ("n_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("maxt", ctypes.c_int32), ("kv_bf16", ctypes.c_int32), ("splits", ctypes.c_int32),
+                ("eps", ctypes.c_float), ("scale", ctypes.c_float)]
 
 
 class Rv12Error(RuntimeError):
@@ -88,6 +94,10 @@ def lib():
         L.rv12_gemm.argtypes = [ctypes.POINTER(Matrix), P, P, I, P, F, I, ctypes.POINTER(Launch), P, SZ, P]
         L.rv12_decode_rows.restype = I
         L.rv12_decode_rows.argtypes = [ctypes.POINTER(Matrix), I, I, P, I, P]
+        L.rv12_attn_workspace_bytes.restype = SZ
+        L.rv12_attn_workspace_bytes.argtypes = [ctypes.POINTER(Attn)]
+        L.rv12_rope_attn.restype = I
+        L.rv12_rope_attn.argtypes = [ctypes.POINTER(Attn), P, P, P, P, P, P, P, P, P, SZ, P]
         v = L.rv12_abi_version()
         if v != ABI_VERSION:
             raise RuntimeError(f"librv12.so ABI version {v}, expected {ABI_VERSION}")

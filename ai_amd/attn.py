@@ -1,0 +1,47 @@
+"""Decode-step attention of one layer through librv12.so (rv12_rope_attn):
+q/k head RMSNorm, RoPE at a device-side position, K/V into the cache,
+grouped-query attention over positions 0..pos.  The MI355X kernel for the
+reference's rope_attn_k (ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213)."""
+import ctypes
+
+import torch
+
+from ._lib import Attn, check, lib
+
+
+SPAN = 128  # positions one workgroup covers at most
+
+
+def default_splits(n_kv, maxt):
+    """Position splits: each workgroup covers at most 128 positions, and there
+    are at least 128 workgroups while each keeps >= 32 positions."""
+    need = -(-maxt // SPAN)
+    want = min(-(-128 // n_kv), -(-maxt // 32))
+    s = max(1, need, want)
+    if s > 64:
+        raise ValueError("the attention kernel covers at most 8192 positions")
+    return int(s)
+
+
+class RopeAttn:
+    """Launch parameters and workspace for one model's caches."""
+
+    def __init__(self, n_heads, n_kv, head_dim, maxt, kv_dtype, eps, device, splits=None):
+        if kv_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("the cache must be float32 or bfloat16")
+        self.a = Attn(n_heads, n_kv, head_dim, maxt, 1 if kv_dtype == torch.bfloat16 else 0,
+                      splits or default_splits(n_kv, maxt), float(eps), float(head_dim ** -0.5))
+        need = lib().rv12_attn_workspace_bytes(ctypes.byref(self.a))
+        self.ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+
+    def __call__(self, qkv, qn, kn, inv, pos, kc, vc, out):
+        for t in (qkv, qn, kn, inv, out):
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                raise ValueError("qkv, qn, kn, inv and out must be contiguous float32")
+        if pos.dtype != torch.int64:
+            raise ValueError("pos must be int64")
+        p = lambda t: ctypes.c_void_p(t.data_ptr())
+        rc = lib().rv12_rope_attn(ctypes.byref(self.a), p(qkv), p(qn), p(kn), p(inv), p(pos), p(kc), p(vc), p(out),
+                                  p(self.ws), self.ws.numel(),
+                                  ctypes.c_void_p(torch.cuda.current_stream(qkv.device).cuda_stream))
+        check(rc, "rope_attn")

@@ -252,4 +252,52 @@ int rv12_decode_rows(const rv12_matrix* w, int first, int last, void* out, int o
     return launch_status();
 }
 
+static int check_attn(const rv12_attn* a) {
+    if (!a) return RV12_E_NULL;
+    if (a->head_dim != 64 && a->head_dim != 128) return RV12_E_SHAPE;
+    if (a->n_kv < 1 || a->n_heads < a->n_kv || a->n_heads % a->n_kv) return RV12_E_SHAPE;
+    const int g = a->n_heads / a->n_kv;
+    if (g != 1 && g != 2 && g != 4 && g != 8) return RV12_E_SHAPE;
+    if (a->maxt < 1) return RV12_E_SHAPE;
+    if (a->splits < 1 || a->splits > kMaxSplits) return RV12_E_CONFIG;
+    // a split covers at most kAttnSpan positions of 0..maxt-1
+    if ((a->maxt + a->splits - 1) / a->splits > kAttnSpan) return RV12_E_CONFIG;
+    if (attn_lds_bytes(a->head_dim, g) > kMaxLds) return RV12_E_CONFIG;
+    return RV12_OK;
+}
+
+size_t rv12_attn_workspace_bytes(const rv12_attn* a) {
+    if (check_attn(a) || a->splits == 1) return 0;
+    return 4 * (size_t)a->n_heads * a->splits * (a->head_dim + 2);
+}
+
+int rv12_rope_attn(const rv12_attn* a, const float* qkv, const float* qn, const float* kn, const float* inv,
+                   const int64_t* pos, void* kc, void* vc, float* out, void* ws, size_t ws_bytes, void* stream) {
+    int rc = check_attn(a);
+    if (rc) return rc;
+    if (!qkv || !qn || !kn || !inv || !pos || !kc || !vc || !out) return RV12_E_NULL;
+    if (!aligned16(qkv) || !aligned16(kc) || !aligned16(vc) || !aligned16(out)) return RV12_E_ALIGN;
+    const size_t need = rv12_attn_workspace_bytes(a);
+    if (need && (!ws || ws_bytes < need)) return RV12_E_WORKSPACE;
+    AttnParams p;
+    p.qkv = qkv;
+    p.qn = qn;
+    p.kn = kn;
+    p.inv = inv;
+    p.pos = pos;
+    p.kc = kc;
+    p.vc = vc;
+    p.out = out;
+    p.part = (float*)ws;
+    p.n_heads = a->n_heads;
+    p.n_kv = a->n_kv;
+    p.head_dim = a->head_dim;
+    p.maxt = a->maxt;
+    p.kv_bf16 = a->kv_bf16 ? 1 : 0;
+    p.eps = a->eps;
+    p.scale = a->scale;
+    if (launch_attn(p, a->splits, (hipStream_t)stream)) return RV12_E_CONFIG;
+    return launch_status();
+}
+
 }  // extern "C"

@@ -75,6 +75,27 @@ inline bool gemm_fits(int K, int rbw, int waves, int splits) {
     return waves <= kGemmMaxWaves && gemm_lds_bytes(K, rbw, waves, splits) <= kGemmMaxLds;
 }
 
+// --- decode-step attention (k_rope_attn)
+struct AttnParams {
+    const float* qkv;
+    const float* qn;
+    const float* kn;
+    const float* inv;
+    const int64_t* pos;
+    void* kc;
+    void* vc;
+    float* out;
+    float* part;  // split partials [H][splits][HD + 2]
+    int n_heads, n_kv, head_dim, maxt, kv_bf16;
+    float eps, scale;
+};
+constexpr int kAttnSpan = 128;  // positions one attention workgroup covers at most
+inline size_t attn_lds_bytes(int hd, int g) {
+    return 4 * ((size_t)g * hd + 2 * (size_t)hd + 4 * (size_t)g + 2 * (size_t)g + (size_t)g * kAttnSpan +
+                4 * (size_t)g * hd);
+}
+int launch_attn(const AttnParams& p, int splits, hipStream_t st);
+
 int launch_gemv(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st);
 int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st);
 void launch_splitk_reduce(const LinearParams& p, int T, int splits, hipStream_t st);

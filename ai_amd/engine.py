@@ -6,7 +6,7 @@ and a token runs them exactly as the reference's `_gpu_layer` does
 (engine.py:329-341):
 
     gemvc1(x,   W.qkv,  qkv, 0, lnw=ln1)      RMSNorm fused in the prologue
-    q/k head norms, RoPE, KV write, attention  (torch here; tkernels.py:164-213)
+    q/k head norms, RoPE, KV write, attention  (one HIP kernel; tkernels.py:164-213)
     gemvc1(att, W.o,    x,   1)               residual accumulate
     gemvc1(x,   W.gu,   gu,  0, lnw=ln2)
     gemvc1(gu,  W.down, x,   2)               silu(g) * u prologue, accumulate
@@ -22,13 +22,14 @@ A decode step is one HIP graph (the reference captures one per batch bucket,
 engine.py:432-444): the embedding row of the current token, all layers, the
 head, argmax, and the bookkeeping (next token becomes the input, position and
 output counter advance) run on the device, so the host only replays the graph.
-Attention, RoPE and the norms are plain torch with fixed shapes (the whole
-cache length, masked beyond the position) so that they can be captured; they
-are the companions of the path, not its subject.
+The step's attention (head norms, RoPE, KV write, grouped-query attention)
+is one HIP kernel per layer (ai_amd.attn); the batched prefill passes use the
+same math in torch.
 """
 import torch
 
 from . import wcomp
+from .attn import RopeAttn
 
 MATS = ("qkv", "o", "gu", "down")
 BATCH = 16  # largest batch of one pass, as the reference's graph buckets (engine.py:31)
@@ -84,13 +85,22 @@ class Engine:
         self.steps = torch.zeros(1, dtype=torch.long, device=dev)
         self.out = torch.zeros(maxt + 1, dtype=torch.long, device=dev)
         self.ar = torch.arange(maxt, device=dev)
+        self.attn = RopeAttn(H, KV, HD, maxt, kv_dtype, self.eps, dev)
         self.graph = None
 
     # ---------------------------------------------------------------- layers
     def _rope_attn(self, l, T):
         """Rows 0..T-1 of qkv at positions pos..pos+T-1: q/k head RMSNorm,
         RoPE, K/V into the cache (rounded to its dtype), causal attention over
-        the cache (tkernels.py:82-150, 164-213)."""
+        the cache (tkernels.py:82-150, 164-213).  One token: the HIP kernel;
+        a batch (prefill): torch."""
+        if T == 1:
+            s = self.small[l]
+            self.attn(self.qkvb[0], s["qn"], s["kn"], self.inv, self.pos, self.Kc[l], self.Vc[l], self.attb[0])
+            return
+        self._rope_attn_torch(l, T)
+
+    def _rope_attn_torch(self, l, T):
         H, KV, HD = self.H, self.KV, self.HD
         G = H // KV
         qkv = self.qkvb[:T]

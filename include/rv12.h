@@ -154,6 +154,31 @@ int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint1
  * ramvi/engine/ramvi_engine/kernels/prefill_kernels.py:58-110. */
 int rv12_decode_rows(const rv12_matrix* w, int first, int last, void* out, int out_f32, void* stream);
 
+/* Decode-step attention of one layer, one token.  The step's q (n_heads
+ * heads), k and v (n_kv heads) are read from the qkv linear's output
+ * (float[(n_heads + 2 n_kv) * head_dim]); q and k get their head RMSNorm
+ * (weights qn, kn: float[head_dim]) and the rotate-half RoPE at position *pos
+ * (angle *pos * inv[i], inv: float[head_dim / 2]); k and v, rounded to the cache
+ * dtype, go into the caches kc / vc ([n_kv, maxt, head_dim], bf16 bits or
+ * float32) at *pos; out (float[n_heads * head_dim]) is the grouped-query
+ * attention of each head over positions 0..*pos (softmax(q.K * scale) V).
+ * *pos is read on the device, so a captured graph can advance it; a *pos
+ * outside [0, maxt) gives zeros and touches no cache.  The positions are spread
+ * over `splits` workgroups per kv head, each covering at most 128 of them
+ * (so splits >= maxt / 128, at most 64: maxt <= 8192); splits > 1 adds a
+ * combine pass (workspace from rv12_attn_workspace_bytes).  Replaces rope_attn_k,
+ * ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213. */
+typedef struct rv12_attn {
+    int32_t n_heads, n_kv, head_dim, maxt;
+    int32_t kv_bf16; /* 1: bf16 cache, 0: float32 cache */
+    int32_t splits;  /* 1..64 */
+    float eps, scale;
+} rv12_attn;
+
+size_t rv12_attn_workspace_bytes(const rv12_attn* a);
+int rv12_rope_attn(const rv12_attn* a, const float* qkv, const float* qn, const float* kn, const float* inv,
+                   const int64_t* pos, void* kc, void* vc, float* out, void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,109 @@
+"""The decode-step attention kernel (rv12_rope_attn) against the same math in
+float32 torch: head RMSNorm, rotate-half RoPE, the cache write rounded to the
+cache dtype, grouped-query softmax attention over 0..pos."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch_ref(qkv, qn, kn, inv, pos, kc, vc, H, KV, HD, eps, k_at_pos=None):
+    """k_at_pos: the step's key as the kernel stored it (one bf16 rounding of
+    the same fp32 value can land one ulp away; the test checks that apart)."""
+    G = H // KV
+    q = qkv[:H * HD].view(H, HD)
+    k = qkv[H * HD:(H + KV) * HD].view(KV, HD)
+    v = qkv[(H + KV) * HD:].view(KV, HD)
+    rms = lambda x, w: w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+    q, k = rms(q, qn), rms(k, kn)
+    ang = (torch.tensor(float(pos), device=inv.device) * inv).double()  # the angle in float32, as the kernel forms it
+    cos = torch.cat([ang, ang]).cos().float()
+    sin = torch.cat([ang, ang]).sin().float()
+    rot = lambda t: torch.cat([-t[..., HD // 2:], t[..., :HD // 2]], -1)
+    q, k = q * cos + rot(q) * sin, k * cos + rot(k) * sin
+    kr, vr = k.to(kc.dtype), v.to(vc.dtype)
+    K = kc[:, :pos + 1].float().clone()
+    V = vc[:, :pos + 1].float().clone()
+    K[:, pos], V[:, pos] = (kr if k_at_pos is None else k_at_pos).float(), vr.float()
+    s = torch.matmul(q.view(KV, G, HD).double(), K.double().transpose(1, 2).contiguous()) * HD ** -0.5
+    a = torch.softmax(s, -1)
+    out = torch.matmul(a, V.double().contiguous()).reshape(H * HD).float()
+    return out, kr, vr
+
+
+@pytest.mark.parametrize("H,KV,HD", [(32, 8, 128), (16, 8, 128), (8, 4, 64), (64, 8, 128), (8, 8, 64)])
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16])
+def test_rope_attn_matches_torch(H, KV, HD, kv_dtype):
+    from ai_amd.attn import RopeAttn
+    dev = "cuda"
+    maxt = 300
+    g = torch.Generator(device=dev).manual_seed(H * 100 + HD)
+    eps = 1e-6
+    inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+    qn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    kn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    for splits in (3, 4, 16):
+        for pos in (0, 1, 37, maxt - 1):
+            print("case", H, KV, HD, kv_dtype, splits, pos, flush=True)
+            qkv = torch.randn((H + 2 * KV) * HD, device=dev, generator=g) * 3
+            kc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+            vc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+            kc0, vc0 = kc.clone(), vc.clone()
+            out = torch.zeros(H * HD, device=dev)
+            att = RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev, splits=splits)
+            att(qkv, qn, kn, inv, torch.tensor([pos], device=dev), kc, vc, out)
+            torch.cuda.synchronize()
+            ref, kr, vr = _torch_ref(qkv, qn, kn, inv, pos, kc0, vc0, H, KV, HD, eps, k_at_pos=kc[:, pos].clone())
+            assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), float((out - ref).abs().max())
+            # the cache: slot pos holds the rounded k (within one bf16 ulp) and v,
+            # every other slot is untouched
+            tol = 2.0 ** -7 if kv_dtype == torch.bfloat16 else 1e-5  # one bf16 ulp
+            assert torch.allclose(kc[:, pos].float(), kr.float(), rtol=tol, atol=1e-6)
+            assert torch.equal(vc[:, pos].float(), vr.float())
+            keep = torch.ones(maxt, dtype=torch.bool)
+            keep[pos] = False
+            assert torch.equal(kc[:, keep], kc0[:, keep]) and torch.equal(vc[:, keep], vc0[:, keep])
+
+
+def test_position_outside_cache_gives_zeros():
+    from ai_amd.attn import RopeAttn
+    dev = "cuda"
+    H, KV, HD, maxt = 8, 4, 64, 32
+    att = RopeAttn(H, KV, HD, maxt, torch.float32, 1e-6, dev, splits=4)
+    kc = torch.randn(KV, maxt, HD, device=dev)
+    vc = torch.randn(KV, maxt, HD, device=dev)
+    kc0, vc0 = kc.clone(), vc.clone()
+    out = torch.full((H * HD,), 7.0, device=dev)
+    inv = torch.ones(HD // 2, device=dev)
+    ones = torch.ones(HD, device=dev)
+    att(torch.randn((H + 2 * KV) * HD, device=dev), ones, ones, inv, torch.tensor([maxt], device=dev), kc, vc, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.zeros_like(out))
+    assert torch.equal(kc, kc0) and torch.equal(vc, vc0)
+
+
+def test_single_split_and_split_limits():
+    """One split (a short cache) matches several; more than 128 positions per
+    split is rejected before any launch."""
+    from ai_amd.attn import RopeAttn
+    dev = "cuda"
+    H, KV, HD, maxt = 16, 8, 128, 128
+    g = torch.Generator(device=dev).manual_seed(5)
+    inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+    ones = torch.ones(HD, device=dev)
+    qkv = torch.randn((H + 2 * KV) * HD, device=dev, generator=g)
+    kc = torch.randn(KV, maxt, HD, device=dev, generator=g)
+    vc = torch.randn(KV, maxt, HD, device=dev, generator=g)
+    outs = []
+    for splits in (1, 2, 5):
+        k, v = kc.clone(), vc.clone()
+        out = torch.zeros(H * HD, device=dev)
+        RopeAttn(H, KV, HD, maxt, torch.float32, 1e-6, dev, splits=splits)(
+            qkv, ones, ones, inv, torch.tensor([maxt - 1], device=dev), k, v, out)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.allclose(outs[0], outs[1], rtol=1e-5, atol=1e-6)
+    assert torch.allclose(outs[0], outs[2], rtol=1e-5, atol=1e-6)
+    with pytest.raises(ValueError):
+        RopeAttn(H, KV, HD, 300, torch.float32, 1e-6, dev, splits=2)(
+            qkv, ones, ones, inv, torch.tensor([0], device=dev), kc, vc, torch.zeros(H * HD, device=dev))
