@@ -9,16 +9,17 @@ import torch
 from ._lib import Attn, check, lib
 
 
-SPAN = 128  # positions one workgroup covers at most
+SPAN = 64  # positions one workgroup covers at most
+MAX_SPLITS = 128
 
 
 def default_splits(n_kv, maxt):
-    """Position splits: each workgroup covers at most 128 positions, and there
-    are at least 128 workgroups while each keeps >= 32 positions."""
+    """Position splits: each workgroup covers at most 64 positions, and there
+    are at least 256 workgroups while each keeps >= 16 positions."""
     need = -(-maxt // SPAN)
-    want = min(-(-128 // n_kv), -(-maxt // 32))
+    want = min(-(-256 // n_kv), -(-maxt // 16))
     s = max(1, need, want)
-    if s > 64:
+    if s > MAX_SPLITS:
         raise ValueError("the attention kernel covers at most 8192 positions")
     return int(s)
 

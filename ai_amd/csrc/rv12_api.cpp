@@ -100,7 +100,8 @@ size_t ws_bytes_for(int N, int T, int splits) {
 int check_matrix(const rv12_matrix* w) {
     if (!w || !w->tiles || !w->rbase || !w->rp) return RV12_E_NULL;
     if (w->n_exc > 0 && (!w->er || !w->ec || !w->ev)) return RV12_E_NULL;
-    if (w->n < 1 || w->k < 32 || w->k % 32 || w->k > kMaxK || w->n_exc < 0) return RV12_E_SHAPE;
+    if (w->n < 1 || w->k < 32 || w->k % 32 || w->k > kMaxK || w->n_exc < 0 || w->n_exc > kMaxExc)
+        return RV12_E_SHAPE;
     if (!aligned16(w->tiles)) return RV12_E_ALIGN;
     return RV12_OK;
 }
@@ -259,7 +260,7 @@ static int check_attn(const rv12_attn* a) {
     const int g = a->n_heads / a->n_kv;
     if (g != 1 && g != 2 && g != 4 && g != 8) return RV12_E_SHAPE;
     if (a->maxt < 1) return RV12_E_SHAPE;
-    if (a->splits < 1 || a->splits > kMaxSplits) return RV12_E_CONFIG;
+    if (a->splits < 1 || a->splits > kAttnMaxSplits) return RV12_E_CONFIG;
     // a split covers at most kAttnSpan positions of 0..maxt-1
     if ((a->maxt + a->splits - 1) / a->splits > kAttnSpan) return RV12_E_CONFIG;
     if (attn_lds_bytes(a->head_dim, g) > kMaxLds) return RV12_E_CONFIG;
@@ -268,7 +269,7 @@ static int check_attn(const rv12_attn* a) {
 
 size_t rv12_attn_workspace_bytes(const rv12_attn* a) {
     if (check_attn(a) || a->splits == 1) return 0;
-    return 4 * (size_t)a->n_heads * a->splits * (a->head_dim + 2);
+    return 4 * attn_part_floats(a->n_kv, a->n_heads / a->n_kv, a->head_dim, a->splits);
 }
 
 int rv12_rope_attn(const rv12_attn* a, const float* qkv, const float* qn, const float* kn, const float* inv,

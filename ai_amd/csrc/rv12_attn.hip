@@ -2,25 +2,25 @@
 // the 12-bit linears in a decode step (replaces rope_attn_k,
 // ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213).
 //
-// Grid (KV heads, splits), 256 threads.  Workgroup (g, sp):
-//   0. first of all the step's own q/k/v values and then every cache value the
-//      workgroup reads are loaded: the key row of one position per thread and
-//      the values of 32 positions per wave (a split covers at most 128
-//      positions), so the kernel waits for memory about once, and the head
-//      transforms below run while the cache values are still in flight;
-//   1. the G query heads of group g and the step's key and value are read
-//      from the qkv linear's output; q and k get their head RMSNorm and the
-//      rotate-half RoPE at position pos (angle pos * inv[i], precise sin/cos),
-//      one wave per head;
+// Grid (KV heads, splits), 256 threads.  Workgroup (g, sp) covers the
+// positions [lo, hi) of 0..pos, at most 64 of them:
+//   0. first the step's own q/k/v values, then every cache value the
+//      workgroup reads are loaded: a quarter key row (HD/4 dims) per thread,
+//      4 threads per position, and the values of 16 (8) positions at a dim
+//      pair per thread.  The cache loads go through descriptors that end at
+//      min(hi, pos), so the positions beyond the split and the step's own slot
+//      (written by split 0 in step 1) read as zeros without a memory access;
+//   1. q (G heads) and k get their head RMSNorm and the rotate-half RoPE at
+//      position pos (angle pos * inv[i], precise sin/cos), one wave per head;
 //      k and v are rounded to the cache dtype (as the reference rounds them,
 //      tkernels.py:187-190); split 0 writes them into the cache at pos;
-//   2. scores s[i][j] = scale * q_i . K[j] for the split's positions
-//      j in [lo, hi) of 0..pos, one position per thread; j == pos uses the
-//      step's own k (so no workgroup reads the slot split 0 writes);
+//   2. scores s[i][j] = scale * q_i . K[j]: each of the 4 threads of a
+//      position sums its quarter of the dims, two lane exchanges add them;
+//      j == pos uses the step's own k;
 //   3. per head the split's max m and sum l of exp(s - m);
-//   4. acc[i][d] = sum_j exp(s[i][j] - m_i) V[j][d], each wave over its 32
-//      positions from registers, the waves added through LDS;
-//   5. one split: out = acc / l; several: (acc, m, l) partials, combined by
+//   4. acc[i][d] = sum_j exp(s[i][j] - m_i) V[j][d]: threads over dim pairs and
+//      position groups, the groups added through LDS in a fixed order;
+//   5. one split: out = acc / l.  Several: (acc, m, l) partials, combined by
 //      k_attn_combine in split order.
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -30,8 +30,6 @@
 
 namespace rv12 {
 
-constexpr int kAttnThreads = 256;
-
 __device__ __forceinline__ float bf16f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 __device__ __forceinline__ uint16_t f2bf16(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
 
@@ -39,51 +37,31 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)0x00020000);
 }
 
-// Raw cache words one thread keeps between the loads at kernel start and their
-// first use (no conversion on load, so no wait): a key row of HD values, and
-// DPL = HD / 64 values of one position at a lane's dims.
-template <int HD, bool BF16>
-struct KRow {
-    static constexpr int N = BF16 ? HD / 8 : HD / 4;  // 16-byte words
-    uint32_t w[N][4];
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int off) {
+template <int N>
+__device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t r, int off, uint32_t (&w)[N][4]) {
 #pragma unroll
-        for (int c = 0; c < N; ++c) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off + c * 16, 0, 0);
-            w[c][0] = v[0];
-            w[c][1] = v[1];
-            w[c][2] = v[2];
-            w[c][3] = v[3];
-        }
-    }
-    __device__ __forceinline__ float at(int i) const {  // value i of the row
-        if constexpr (BF16) {
-            const uint32_t u = w[i >> 3][(i >> 1) & 3];
-            return __uint_as_float((i & 1) ? (u & 0xFFFF0000u) : (u << 16));
-        } else {
-            return __uint_as_float(w[i >> 2][i & 3]);
-        }
-    }
-};
-
-template <int HD, bool BF16>
-__device__ __forceinline__ void load_vals(__amdgpu_buffer_rsrc_t r, int off, uint32_t (&u)[2]) {
-    constexpr int DPL = HD / 64;
-    if constexpr (BF16 && DPL == 2) {
-        u[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-    } else if constexpr (BF16) {
-        u[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-    } else if constexpr (DPL == 2) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-        u[0] = v[0];
-        u[1] = v[1];
-    } else {
-        u[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    for (int c = 0; c < N; ++c) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off + c * 16, 0, 0);
+        w[c][0] = v[0];
+        w[c][1] = v[1];
+        w[c][2] = v[2];
+        w[c][3] = v[3];
     }
 }
 
-template <int HD, bool BF16>
-__device__ __forceinline__ float val_at(const uint32_t (&u)[2], int e) {
+// value i of raw cache words (bf16 pairs or float32)
+template <bool BF16, int N>
+__device__ __forceinline__ float word_val(const uint32_t (&w)[N][4], int i) {
+    if constexpr (BF16) {
+        const uint32_t u = w[i >> 3][(i >> 1) & 3];
+        return __uint_as_float((i & 1) ? (u & 0xFFFF0000u) : (u << 16));
+    } else {
+        return __uint_as_float(w[i >> 2][i & 3]);
+    }
+}
+
+template <bool BF16>
+__device__ __forceinline__ float pair_val(const uint32_t (&u)[2], int e) {
     if constexpr (BF16) return __uint_as_float(e ? (u[0] & 0xFFFF0000u) : (u[0] << 16));
     else return __uint_as_float(u[e]);
 }
@@ -116,54 +94,52 @@ template <int HD, int G, bool BF16>
 __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
     extern __shared__ float lds[];
     constexpr int NW = kAttnThreads / 64;
-    constexpr int PW = kAttnSpan / NW;  // positions per wave in the value sum
-    constexpr int DPL = HD / 64;        // value dims per lane
+    constexpr int P = kAttnSpan;           // positions of one workgroup at most
+    constexpr int EB = BF16 ? 2 : 4;       // cache bytes per value
+    constexpr int QD = HD / 4;             // dims per thread in the scores
+    constexpr int KW = QD * EB / 16;       // 16-byte words of a thread's key quarter
+    constexpr int DP = HD / 2;             // dim pairs
+    constexpr int PG = kAttnThreads / DP;  // position groups of the value sums
+    constexpr int PPG = P / PG;            // positions per group
+    constexpr int half = HD / 2, HPW = (G + NW) / NW;
     const int g = blockIdx.x, sp = blockIdx.y, S = gridDim.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int H = p.n_kv * G;
     const int64_t pos = *p.pos;
-    float* qs = lds;                   // [G][HD]
-    float* kn = qs + G * HD;           // [HD] step key (normed, roped, rounded)
-    float* vn = kn + HD;               // [HD] step value (rounded)
-    float* red = vn + HD;              // [NW][G] per-wave maxima / sums
-    float* stat = red + NW * G;        // [2 G] m, l
-    float* sc = stat + 2 * G;          // [G][kAttnSpan] scores, then weights
-    float* wacc = sc + G * kAttnSpan;  // [NW][G][HD] per-wave value sums
-    if (pos < 0 || pos >= p.maxt) {    // a position outside the cache: defined output, no access
-        for (int o = t; o < G * HD; o += kAttnThreads) {
-            const int i = o / HD, d = o % HD;
-            if (S == 1) p.out[(g * G + i) * HD + d] = 0.0f;
-            else p.part[(((int64_t)(g * G + i) * S + sp) * (HD + 2)) + d] = 0.0f;
-        }
-        if (S > 1 && t < G) {
-            float* pp = p.part + ((int64_t)(g * G + t) * S + sp) * (HD + 2);
-            pp[HD] = sp == 0 ? 0.0f : -INFINITY;
-            pp[HD + 1] = sp == 0 ? 1.0f : 0.0f;
+    float* qs = lds;                // [G][HD]
+    float* kn = qs + G * HD;        // [HD] step key (normed, roped, rounded)
+    float* vn = kn + HD;            // [HD] step value (rounded)
+    float* wt = vn + HD;            // [P][G] weights exp(s - m)
+    float* red = wt + P * G;        // [NW][G] per-wave maxima / sums
+    float* stat = red + NW * G;     // [2 G] m, l
+    float* wacc = stat + 2 * G;     // [PG][G][HD] value sums of the position groups
+    if (pos < 0 || pos >= p.maxt) {  // a position outside the cache: zeros out, no cache access
+        if (S == 1) {
+            for (int o = t; o < G * HD; o += kAttnThreads) p.out[(int64_t)g * G * HD + o] = 0.0f;
+        } else {  // partials that combine to zeros: acc 0, and l = 1 on split 0 only
+            float* part = p.part + ((int64_t)g * S + sp) * G * (HD + 2);
+            for (int o = t; o < G * (HD + 2); o += kAttnThreads) {
+                const int d = o % (HD + 2);
+                part[o] = d < HD ? 0.0f : (d == HD ? (sp == 0 ? 0.0f : -INFINITY) : (sp == 0 ? 1.0f : 0.0f));
+            }
         }
         return;
     }
-    const int64_t n = pos + 1;
-    const int64_t lo = sp * n / S, hi = (sp + 1) * n / S;  // hi - lo <= kAttnSpan (host)
-    const int span = (int)(hi - lo);
+    const int n = (int)pos + 1;  // n <= 8192 and S <= 128: 32-bit products
+    const int lo = (int)((uint32_t)(sp * n) / (uint32_t)S), hi = (int)((uint32_t)((sp + 1) * n) / (uint32_t)S);
+    const int span = hi - lo;  // <= P (host)
     const int64_t row0 = (int64_t)g * p.maxt * HD;
 
-    // ---- 0. every cache value this workgroup reads, loaded first: thread t
-    // the key row of position lo + t, wave w the values of positions
-    // lo + PW w .. lo + PW w + PW - 1 at its lanes' dims.  The loads go through
-    // descriptors that end at position pos: the step's own slot (written by
-    // split 0, taken from the qkv output instead) and anything beyond read as
-    // zeros without a memory access.
-    // the step's values: wave w the heads w, w + NW, .. of q (0..G-1) and k (G),
-    // lane l < HD/2 the pair (l, l + HD/2), thread d < HD the value v[d]
-    constexpr int half = HD / 2, HPW = (G + NW) / NW;
+    // ---- 0. the step's values: wave w the heads w, w + NW, .. of q (0..G-1)
+    // and k (G), lane l < HD/2 the pair (l, l + HD/2), thread d < HD v[d]
     const int la = lane < half ? lane : 0;
+    const float msk = lane < half ? 1.0f : 0.0f;
     const __amdgpu_buffer_rsrc_t qr = attn_rsrc(p.qkv, (uint32_t)((H + 2 * p.n_kv) * HD * 4));
     float qa[HPW], qb[HPW];
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
         const int i = min(wave + j * NW, G);
         const int off = ((i < G ? g * G + i : H + g) * HD + la) * 4;
-        const float msk = lane < half ? 1.0f : 0.0f;
         qa[j] = msk * __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(qr, off, 0, 0));
         qb[j] = msk * __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(qr, off + half * 4, 0, 0));
     }
@@ -171,16 +147,27 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
         __builtin_amdgcn_raw_buffer_load_b32(qr, ((H + p.n_kv + g) * HD + (t < HD ? t : 0)) * 4, 0, 0));
     const float wqa = p.qn[la], wqb = p.qn[la + half], wka = p.kn[la], wkb = p.kn[la + half], iv = p.inv[la];
 
-    constexpr int EB = BF16 ? 2 : 4;
-    const char* kbase = reinterpret_cast<const char*>(p.kc) + row0 * EB;
-    const char* vbase = reinterpret_cast<const char*>(p.vc) + row0 * EB;
-    const __amdgpu_buffer_rsrc_t kr = attn_rsrc(kbase, (uint32_t)(pos * HD * EB));
-    const __amdgpu_buffer_rsrc_t vr = attn_rsrc(vbase, (uint32_t)(pos * HD * EB));
-    KRow<HD, BF16> krow;
-    krow.load(kr, (int)((lo + t) * HD * EB));
-    uint32_t vraw[PW][2];
+    // the cache values: positions [0, min(hi, pos)) are in range
+    const uint32_t cbytes = (uint32_t)min(hi, n - 1) * HD * EB;
+    const __amdgpu_buffer_rsrc_t kr = attn_rsrc(reinterpret_cast<const char*>(p.kc) + row0 * EB, cbytes);
+    const __amdgpu_buffer_rsrc_t vr = attn_rsrc(reinterpret_cast<const char*>(p.vc) + row0 * EB, cbytes);
+    const int pl = t >> 2, qq = t & 3;  // score thread: position lo + pl, dims [qq QD, qq QD + QD)
+    uint32_t kw[KW][4];
+    load_words<KW>(kr, ((lo + pl) * HD + qq * QD) * EB, kw);
+    const int dp = t % DP, pg = t / DP;  // value thread: dims 2 dp, 2 dp + 1 of positions pg PPG ..
+    uint32_t vw[PPG][2];
 #pragma unroll
-    for (int r = 0; r < PW; ++r) load_vals<HD, BF16>(vr, (int)((lo + wave * PW + r) * HD + lane * DPL) * EB, vraw[r]);
+    for (int r = 0; r < PPG; ++r) {
+        const int off = ((lo + pg * PPG + r) * HD + 2 * dp) * EB;
+        if constexpr (BF16) {
+            vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(vr, off, 0, 0);
+            vw[r][1] = 0;
+        } else {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(vr, off, 0, 0);
+            vw[r][0] = v[0];
+            vw[r][1] = v[1];
+        }
+    }
 
     // ---- 1. the step's q (G heads) and k, one wave per head; v as read
     float sn, cs;
@@ -209,40 +196,40 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
     }
     __syncthreads();
 
-    // ---- 2. scores, one position per thread
-    float mloc[G];
+    // ---- 2. scores: thread (pl, qq) sums its quarter of the dims
+    const bool valid = pl < span;
+    const bool own = lo + pl == pos;
+    float sc[G];
 #pragma unroll
-    for (int i = 0; i < G; ++i) mloc[i] = -INFINITY;
-    if (t < span) {
-        const bool own = lo + t == pos;
+    for (int i = 0; i < G; ++i) {
+        const float* qrow = qs + i * HD + qq * QD;
+        float s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < G; ++i) {
-            float s = 0.0f;
-#pragma unroll
-            for (int c = 0; c < HD; c += 4) {
-                const float4 q = *reinterpret_cast<const float4*>(qs + i * HD + c);
-                if (own) {
-                    s = fmaf(q.x, kn[c], s);
-                    s = fmaf(q.y, kn[c + 1], s);
-                    s = fmaf(q.z, kn[c + 2], s);
-                    s = fmaf(q.w, kn[c + 3], s);
-                } else {
-                    s = fmaf(q.x, krow.at(c), s);
-                    s = fmaf(q.y, krow.at(c + 1), s);
-                    s = fmaf(q.z, krow.at(c + 2), s);
-                    s = fmaf(q.w, krow.at(c + 3), s);
-                }
-            }
-            s *= p.scale;
-            sc[i * kAttnSpan + t] = s;
-            mloc[i] = s;
+        for (int d = 0; d < QD; d += 4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(qrow + d);
+            s = fmaf(q4.x, word_val<BF16>(kw, d), s);
+            s = fmaf(q4.y, word_val<BF16>(kw, d + 1), s);
+            s = fmaf(q4.z, word_val<BF16>(kw, d + 2), s);
+            s = fmaf(q4.w, word_val<BF16>(kw, d + 3), s);
         }
+        if (own) {  // the step's own key (its cache slot read as zeros)
+            s = 0.0f;
+            for (int d = 0; d < QD; ++d) s = fmaf(qrow[d], kn[qq * QD + d], s);
+        }
+        sc[i] = s;
+    }
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        float s = sc[i];
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        sc[i] = valid ? s * p.scale : -INFINITY;
     }
 
     // ---- 3. per-head max, then the weights exp(s - m) and their sum
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-        const float m = wave_max(mloc[i]);
+        const float m = wave_max(sc[i]);
         if (lane == 0) red[wave * G + i] = m;
     }
     __syncthreads();
@@ -252,20 +239,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
         stat[t] = m;
     }
     __syncthreads();
-    float lloc[G];
+    float lsum[G];
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-        float e = 0.0f;
-        if (t < span) {
-            e = expf(sc[i * kAttnSpan + t] - stat[i]);
-            sc[i * kAttnSpan + t] = e;
-        }
-        lloc[i] = wave_sum(e);
+        const float e = valid ? expf(sc[i] - stat[i]) : 0.0f;
+        if (qq == 0) wt[pl * G + i] = e;
+        lsum[i] = wave_sum(qq == 0 ? e : 0.0f);
     }
     __syncthreads();  // every thread has read stat[] and red[] of the max step
+    if (lane == 0)
 #pragma unroll
-    for (int i = 0; i < G; ++i)
-        if (lane == 0) red[wave * G + i] = lloc[i];
+        for (int i = 0; i < G; ++i) red[wave * G + i] = lsum[i];
     __syncthreads();
     if (t < G) {
         float l = 0.0f;
@@ -273,78 +257,85 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
         stat[G + t] = l;
     }
 
-    // ---- 4. weighted values: wave w sums its PW positions from registers
-    // for every head at its lanes' dims, then the waves are added
-    float acc[G][DPL];
+    // ---- 4. weighted values: thread (dp, pg) over its PPG positions
+    float acc[G][2];
 #pragma unroll
-    for (int i = 0; i < G; ++i)
+    for (int i = 0; i < G; ++i) acc[i][0] = acc[i][1] = 0.0f;
+    const float vn0 = vn[2 * dp], vn1 = vn[2 * dp + 1];
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[i][e] = 0.0f;
-    const int wv = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform: scalar loop bounds
-    float vnl[DPL];
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) vnl[e] = vn[lane * DPL + e];
-#pragma unroll
-    for (int r = 0; r < PW; ++r) {
-        const int jj = wv * PW + r;
-        if (jj >= span) break;
-        const bool own = lo + jj == pos;
+    for (int r = 0; r < PPG; ++r) {
+        const int pj = pg * PPG + r;
+        const bool ownj = lo + pj == pos;
+        const float v0 = ownj ? vn0 : pair_val<BF16>(vw[r], 0);
+        const float v1 = ownj ? vn1 : pair_val<BF16>(vw[r], 1);
 #pragma unroll
         for (int i = 0; i < G; ++i) {
-            const float w8 = sc[i * kAttnSpan + jj];
-#pragma unroll
-            for (int e = 0; e < DPL; ++e)
-                acc[i][e] = fmaf(w8, own ? vnl[e] : val_at<HD, BF16>(vraw[r], e), acc[i][e]);
+            const float w8 = wt[pj * G + i];  // zero beyond the span
+            acc[i][0] = fmaf(w8, v0, acc[i][0]);
+            acc[i][1] = fmaf(w8, v1, acc[i][1]);
         }
     }
 #pragma unroll
-    for (int i = 0; i < G; ++i)
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) wacc[(wave * G + i) * HD + lane * DPL + e] = acc[i][e];
+    for (int i = 0; i < G; ++i) {
+        wacc[(pg * G + i) * HD + 2 * dp] = acc[i][0];
+        wacc[(pg * G + i) * HD + 2 * dp + 1] = acc[i][1];
+    }
     __syncthreads();
 
     // ---- 5. output or partials
+    float* part = p.part + ((int64_t)g * S + sp) * G * (HD + 2);  // [n_kv][S][G][HD + 2]
     for (int o = t; o < G * HD; o += kAttnThreads) {
         const int i = o / HD, d = o % HD;
         float v = 0.0f;
-        for (int w = 0; w < NW; ++w) v += wacc[(w * G + i) * HD + d];
-        if (S == 1) p.out[(g * G + i) * HD + d] = v / stat[G + i];
-        else p.part[((int64_t)(g * G + i) * S + sp) * (HD + 2) + d] = v;
+#pragma unroll
+        for (int w = 0; w < PG; ++w) v += wacc[(w * G + i) * HD + d];
+        if (S == 1) p.out[((int64_t)g * G + i) * HD + d] = v / stat[G + i];
+        else part[i * (HD + 2) + d] = v;
     }
     if (S > 1 && t < G) {
-        float* pp = p.part + ((int64_t)(g * G + t) * S + sp) * (HD + 2);
-        pp[HD] = stat[t];
-        pp[HD + 1] = stat[G + t];
+        part[t * (HD + 2) + HD] = stat[t];
+        part[t * (HD + 2) + HD + 1] = stat[G + t];
     }
 }
 
-// combine the splits of each head: M = max m_s, out = sum acc_s e^(m_s - M) / sum l_s e^(m_s - M);
-// one workgroup per head, every partial loaded at once (a descriptor over the
-// head's S partials reads zeros beyond them)
-__global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out, int S, int HD) {
+// combine the splits of each head in split order: M = max m_s,
+// out = sum acc_s e^(m_s - M) / sum l_s e^(m_s - M).  One workgroup per head,
+// one thread per dim; 16 partials in flight at a time (a descriptor over the
+// group's partials reads zeros past the last split)
+__global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out, int S,
+                                                      int G, int HD) {
     const int h = blockIdx.x, d = threadIdx.x;
-    const int stride = (HD + 2) * 4;
-    const __amdgpu_buffer_rsrc_t r = attn_rsrc(part + (int64_t)h * S * (HD + 2), (uint32_t)(S * stride));
-    float a[kMaxSplits], m[kMaxSplits], l[kMaxSplits];
-#pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s) {
-        a[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, s * stride + d * 4, 0, 0));
-        const auto ml = __builtin_amdgcn_raw_buffer_load_b64(r, s * stride + HD * 4, 0, 0);
-        m[s] = __uint_as_float(ml[0]);
-        l[s] = __uint_as_float(ml[1]);
-    }
+    const int g = h / G, i = h % G;
+    const int stride = G * (HD + 2) * 4;  // bytes from one split's partial of head h to the next
+    const __amdgpu_buffer_rsrc_t r =
+        attn_rsrc(part + ((int64_t)g * S * G + i) * (HD + 2), (uint32_t)((S - 1) * stride + (HD + 2) * 4));
     float M = -INFINITY;
+    for (int s0 = 0; s0 < S; s0 += 16) {
+        float m[16];
 #pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s)
-        if (s < S) M = fmaxf(M, m[s]);
-    float num = 0.0f, den = 0.0f;
+        for (int u = 0; u < 16; ++u) m[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (s0 + u) * stride + HD * 4, 0, 0));
 #pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s) {
-        const float w = (s < S && l[s] > 0.0f) ? expf(m[s] - M) : 0.0f;
-        num = fmaf(a[s], w, num);
-        den = fmaf(l[s], w, den);
+        for (int u = 0; u < 16; ++u)
+            if (s0 + u < S) M = fmaxf(M, m[u]);
     }
-    out[h * HD + d] = num / den;
+    float num = 0.0f, den = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += 16) {
+        float a[16], m[16], l[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            a[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (s0 + u) * stride + d * 4, 0, 0));
+            const auto ml = __builtin_amdgcn_raw_buffer_load_b64(r, (s0 + u) * stride + HD * 4, 0, 0);
+            m[u] = __uint_as_float(ml[0]);
+            l[u] = __uint_as_float(ml[1]);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const float w = (s0 + u < S && l[u] > 0.0f) ? expf(m[u] - M) : 0.0f;
+            num = fmaf(a[u], w, num);
+            den = fmaf(l[u], w, den);
+        }
+    }
+    out[(int64_t)h * HD + d] = num / den;
 }
 
 template <int HD, int G, bool BF16>
@@ -378,7 +369,8 @@ int launch_attn(const AttnParams& p, int S, hipStream_t st) {
     int rc = p.head_dim == 128 ? launch_attn_hd<128>(p, G, S, lds, st)
                                : (p.head_dim == 64 ? launch_attn_hd<64>(p, G, S, lds, st) : -1);
     if (rc) return rc;
-    if (S > 1) hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads), dim3(p.head_dim), 0, st, p.part, p.out, S, p.head_dim);
+    if (S > 1)
+        hipLaunchKernelGGL(k_attn_combine, dim3(p.n_heads), dim3(p.head_dim), 0, st, p.part, p.out, S, G, p.head_dim);
     return 0;
 }
 

@@ -7,7 +7,9 @@
 // Order of work, so that every long-latency load is in flight before
 // anything waits on it:
 //   1. every thread loads its share of the activations (x, and u in mode 2,
-//      and the RMSNorm weight) for the split's K range;
+//      and the RMSNorm weight) for the split's K range, as straight-line code
+//      (the prologue variants are template arguments); a bare barrier puts
+//      every wave's activation loads ahead of the weight loads;
 //   2. each wave issues the loads of its first kDepth weight steps (buffer
 //      loads; a step past the split's end goes through a 0-byte descriptor,
 //      which returns zeros without a memory access);
@@ -43,11 +45,17 @@ __device__ __forceinline__ void issue_step(u32x3 (&dst)[RB], __amdgpu_buffer_rsr
 
 // NXM = float4 chunks of activations per thread loaded in step 1, before the
 // weight prefetch; columns beyond 4 * NXM * blockDim.x are staged after it.
+// M2: silu(g) * u prologue (MODE 2); LN: RMSNorm weight.  Both are template
+// arguments so that the loads of step 1 are straight-line code, issued without
+// waiting for any kernel argument test.
 // The host guarantees blockDim.x >= 16 * RB * T (one thread per output).
-template <int T, int RB>
+template <int T, int RB, bool M2, bool LN>
 __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p) {
     constexpr int NXM = gemv_chunks(T);
     constexpr int NO = RB * 16 * T;  // outputs of the workgroup
+    // weight steps in flight per wave: deeper prefetch delays the activation
+    // loads, which the memory system serves behind the weight stream
+    constexpr int D = kDepth;
     extern __shared__ float smem[];
     const int W = blockDim.x >> 6;
     const int nthr = blockDim.x;
@@ -55,7 +63,9 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     const int wu = __builtin_amdgcn_readfirstlane(wave);
     const int S = gridDim.y, sp = blockIdx.y;
     const int nsteps = p.K >> 5;
-    const int s_lo = (int)((int64_t)sp * nsteps / S), s_hi = (int)((int64_t)(sp + 1) * nsteps / S);
+    // split bounds in 32 bits: nsteps <= 2^15 and S <= 64
+    const int s_lo = (int)((uint32_t)(sp * nsteps) / (uint32_t)S);
+    const int s_hi = (int)((uint32_t)((sp + 1) * nsteps) / (uint32_t)S);
     const int k_lo = s_lo * 32, krange = (s_hi - s_lo) * 32;
     const int64_t blk0 = (int64_t)blockIdx.x * RB;
     const int n0 = (int)(blk0 * 16);
@@ -69,42 +79,42 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
 
     // ---- 0. what the epilogue needs, loaded first: thread i < NO owns output
     // (row n0 + i % (16 RB), token i / (16 RB)): its row's scale exponent and
-    // exception range, and y for an accumulating single-split launch
+    // exception range, and y for an accumulating single-split launch.  Every
+    // thread loads (row and token clamped into range, so the loads need no
+    // branch); only the owners' values are used, in the epilogue.
     const bool owner = threadIdx.x < NO;
     const int orow = threadIdx.x % (RB * 16), otok = threadIdx.x / (RB * 16);
     const int on = n0 + orow;
     const bool oval = owner && on < p.N;
-    int obase = 0;  // used only in the epilogue, so this load does not stall the prologue
-    int32_t oe0 = 0, oe1 = 0;
-    float oy = 0.0f;
-    if (oval) {
-        obase = p.rbase[on];
-        if (p.n_exc > 0) {
-            oe0 = p.rp[on];
-            oe1 = p.rp[on + 1];
-        }
-        if (S == 1 && p.mode != 0) oy = p.y[(int64_t)otok * p.N + on];
-    }
+    const int onc = min(on, p.N - 1);
+    const int obase = p.rbase[onc];  // raw: the scale exponent is formed in the epilogue
+    const int32_t oe0 = p.rp[onc], oe1 = p.rp[onc + 1];
+    const float oy = p.y[(int64_t)min(otok, T - 1) * p.N + onc];
 
-    // ---- 1. activations of this thread
+    // ---- 1. activations of this thread: the chunks j < nxm hold the split's
+    // columns (lanes past its end load column k_lo again, unused)
+    const int nxm = min(NXM, (krange + 4 * nthr - 1) / (4 * nthr));
     f32x4 xr[NXM][T], ur[NXM][T];
     uint2 lr[NXM];
 #pragma unroll
     for (int j = 0; j < NXM; ++j) {
-        const int i = (threadIdx.x + j * nthr) * 4;
-        if (i < krange) {
-            const int k = k_lo + i;
-            if (p.lnw) lr[j] = *reinterpret_cast<const uint2*>(p.lnw + k);
+        if (j < nxm) {
+            const int i = (threadIdx.x + j * nthr) * 4;
+            const int k = k_lo + (i < krange ? i : 0);
+            if constexpr (LN) lr[j] = *reinterpret_cast<const uint2*>(p.lnw + k);
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 const float* xt = p.x + (int64_t)t * p.xs;
                 xr[j][t] = *reinterpret_cast<const f32x4*>(xt + k);
-                if (p.mode == 2) ur[j][t] = *reinterpret_cast<const f32x4*>(xt + p.K + k);
+                if constexpr (M2) ur[j][t] = *reinterpret_cast<const f32x4*>(xt + p.K + k);
             }
         }
     }
+    // every wave's activation loads enter the memory pipeline before any
+    // weight load (a bare barrier: it orders the issue, it waits for no data)
+    __builtin_amdgcn_s_barrier();
 
-    // ---- 2. first kDepth weight steps of this wave
+    // ---- 2. first D weight steps of this wave
     const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
     const char* wbase = reinterpret_cast<const char*>(p.tiles) + blk0 * (int64_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, (uint32_t)nvalid * blk_bytes);
@@ -113,24 +123,21 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
 #pragma unroll
     for (int b = 0; b < RB; ++b) voff[b] = (int)(b * blk_bytes) + lane * 12;
     const int s0 = s_lo + wu;
-    u32x3 buf[kDepth][RB];
+    u32x3 buf[D][RB];
 #pragma unroll
-    for (int u = 0; u < kDepth; ++u) issue_step<RB>(buf[u], rv, rnull, voff, s0 + u * W, s_hi);
+    for (int u = 0; u < D; ++u) issue_step<RB>(buf[u], rv, rnull, voff, s0 + u * W, s_hi);
 
     // the workgroup's first round of exceptions, one entry per thread (after
-    // the weight loads: these wait for a scalar load of the row pointers)
-    int32_t e_lo = 0, e_hi = 0;
-    int ec0 = 0;
-    float ev0 = 0.0f;
-    if (p.n_exc > 0) {
-        e_lo = p.rp[n0];
-        e_hi = p.rp[min(n0 + RB * 16, p.N)];
-        const int32_t j = e_lo + threadIdx.x;
-        if (j < e_hi) {
-            ec0 = p.ec[j];
-            ev0 = p.ev[j];
-        }
-    }
+    // the weight loads: these wait for a scalar load of the row pointers); a
+    // descriptor over the n_exc entries reads zeros past the list's end
+    const int32_t e_lo = p.rp[n0];
+    const int32_t e_hi = p.rp[min(n0 + RB * 16, p.N)];
+    const uint32_t exc_bytes = (uint32_t)min(p.n_exc, (int64_t)(1 << 28)) * 4u;
+    const __amdgpu_buffer_rsrc_t r_ec = make_rsrc(p.ec, exc_bytes), r_ev = make_rsrc(p.ev, exc_bytes);
+    const int32_t j_exc = e_lo + (int32_t)threadIdx.x;
+    const uint32_t exc_off = j_exc < e_hi ? (uint32_t)j_exc * 4u : 0xFFFFFFF0u;
+    const int ec0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_ec, (int)exc_off, 0, 0);
+    const float ev0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_ev, (int)exc_off, 0, 0));
 
     // ---- 3. x' into LDS
     float sq[T];
@@ -139,20 +146,20 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
 #pragma unroll
     for (int j = 0; j < NXM; ++j) {
         const int i = (threadIdx.x + j * nthr) * 4;
-        if (i < krange) {
+        if (j < nxm && i < krange) {
             f32x4 lw = {1.0f, 1.0f, 1.0f, 1.0f};
-            if (p.lnw)
+            if constexpr (LN)
                 lw = f32x4{__uint_as_float(lr[j].x << 16), __uint_as_float(lr[j].x & 0xFFFF0000u),
                            __uint_as_float(lr[j].y << 16), __uint_as_float(lr[j].y & 0xFFFF0000u)};
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 f32x4 v = xr[j][t];
-                if (p.lnw) sq[t] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-                if (p.mode == 2) {
+                if constexpr (LN) sq[t] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                if constexpr (M2) {
                     const f32x4 u = ur[j][t];
                     v = f32x4{silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w)};
                 }
-                if (p.lnw) v = lw * v;
+                if constexpr (LN) v = lw * v;
                 *reinterpret_cast<f32x4*>(xl + t * krange + i) = v;
             }
         }
@@ -162,7 +169,7 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     for (int i = (threadIdx.x + NXM * nthr) * 4; i < krange; i += nthr * 4) {
         const int k = k_lo + i;
         f32x4 lw = {1.0f, 1.0f, 1.0f, 1.0f};
-        if (p.lnw) {
+        if constexpr (LN) {
             const uint2 b = *reinterpret_cast<const uint2*>(p.lnw + k);
             lw = f32x4{__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xFFFF0000u), __uint_as_float(b.y << 16),
                        __uint_as_float(b.y & 0xFFFF0000u)};
@@ -171,16 +178,16 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
         for (int t = 0; t < T; ++t) {
             const float* xt = p.x + (int64_t)t * p.xs;
             f32x4 v = *reinterpret_cast<const f32x4*>(xt + k);
-            if (p.lnw) sq[t] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-            if (p.mode == 2) {
+            if constexpr (LN) sq[t] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            if constexpr (M2) {
                 const f32x4 u = *reinterpret_cast<const f32x4*>(xt + p.K + k);
                 v = f32x4{silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w)};
             }
-            if (p.lnw) v = lw * v;
+            if constexpr (LN) v = lw * v;
             *reinterpret_cast<f32x4*>(xl + t * krange + i) = v;
         }
     }
-    if (p.lnw) {
+    if constexpr (LN) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             float v = sq[t];
@@ -198,15 +205,15 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
         for (int t = 0; t < T; ++t) acc[b][t] = 0.0f;
 
     const int per_wave = (s_hi - s_lo + W - 1) / W;
-    const int rounds = (per_wave + kDepth - 1) / kDepth;
+    const int rounds = (per_wave + D - 1) / D;
     for (int r = 0; r < rounds; ++r) {
 #pragma unroll
-        for (int u = 0; u < kDepth; ++u) {
-            const int s = s0 + (r * kDepth + u) * W;
+        for (int u = 0; u < D; ++u) {
+            const int s = s0 + (r * D + u) * W;
             u32x3 cur[RB];
 #pragma unroll
             for (int b = 0; b < RB; ++b) cur[b] = buf[u][b];
-            issue_step<RB>(buf[u], rv, rnull, voff, s + kDepth * W, s_hi);
+            issue_step<RB>(buf[u], rv, rnull, voff, s + D * W, s_hi);
             if (s < s_hi) {
                 uint32_t pr[RB][4];
 #pragma unroll
@@ -287,7 +294,7 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     if (oval) {
         v = ldexpf(v, scale_exp(obase)) + eacc;
         if (S == 1) {
-            if (p.lnw) {
+            if constexpr (LN) {
                 float sqs = 0.0f;
                 for (int w = 0; w < W; ++w) sqs += ssq[w * T + otok];
                 v *= 1.0f / sqrtf(sqs / (float)p.K + p.eps);
@@ -297,7 +304,7 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
             p.part[((int64_t)sp * T + otok) * p.npad + on] = v;
         }
     }
-    if (S > 1 && p.lnw && blockIdx.x == 0 && threadIdx.x < T) {
+    if (LN && S > 1 && blockIdx.x == 0 && threadIdx.x < T) {
         float sqs = 0.0f;
         for (int w = 0; w < W; ++w) sqs += ssq[w * T + threadIdx.x];
         p.ssq[sp * T + threadIdx.x] = sqs;
@@ -323,21 +330,30 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 }
 
 // ------------------------------------------------------------------ launch
-template <int T, int RB>
+template <int T, int RB, bool M2, bool LN>
 static void launch_t(const LinearParams& p, dim3 grid, int threads, size_t lds, hipStream_t st) {
     if (lds > kDefaultLds)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<T, RB>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<T, RB, M2, LN>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((k_gemv<T, RB>), grid, dim3(threads), lds, st, p);
+    hipLaunchKernelGGL((k_gemv<T, RB, M2, LN>), grid, dim3(threads), lds, st, p);
+}
+
+template <int T, int RB>
+static void launch_pro(const LinearParams& p, dim3 grid, int threads, size_t lds, hipStream_t st) {
+    const bool m2 = p.mode == 2, ln = p.lnw != nullptr;
+    if (m2 && ln) launch_t<T, RB, true, true>(p, grid, threads, lds, st);
+    else if (m2) launch_t<T, RB, true, false>(p, grid, threads, lds, st);
+    else if (ln) launch_t<T, RB, false, true>(p, grid, threads, lds, st);
+    else launch_t<T, RB, false, false>(p, grid, threads, lds, st);
 }
 
 template <int RB>
 static int launch_rb(const LinearParams& p, int T, dim3 grid, int threads, size_t lds, hipStream_t st) {
     switch (T) {
-        case 1: launch_t<1, RB>(p, grid, threads, lds, st); return 0;
-        case 2: launch_t<2, RB>(p, grid, threads, lds, st); return 0;
-        case 3: launch_t<3, RB>(p, grid, threads, lds, st); return 0;
-        case 4: launch_t<4, RB>(p, grid, threads, lds, st); return 0;
+        case 1: launch_pro<1, RB>(p, grid, threads, lds, st); return 0;
+        case 2: launch_pro<2, RB>(p, grid, threads, lds, st); return 0;
+        case 3: launch_pro<3, RB>(p, grid, threads, lds, st); return 0;
+        case 4: launch_pro<4, RB>(p, grid, threads, lds, st); return 0;
     }
     return -1;
 }

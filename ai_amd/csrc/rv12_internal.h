@@ -35,7 +35,8 @@ constexpr int kMaxSplits = 64;
 constexpr int kMaxWaves = 16;
 constexpr size_t kMaxLds = 163840;  // LDS bytes of one gfx950 workgroup (160 KB)
 constexpr size_t kDefaultLds = 65536;  // above this a kernel needs hipFuncAttributeMaxDynamicSharedMemorySize
-constexpr int kMaxK = 1 << 20;         // keeps every 32-bit buffer offset of a workgroup in range
+constexpr int kMaxK = 1 << 20;             // keeps every 32-bit buffer offset of a workgroup in range
+constexpr int64_t kMaxExc = (int64_t)1 << 28;  // exception entries of one matrix (read through 32-bit buffer ranges)
 constexpr int kMaxVectorTokens = 4;  // k_gemv (vector FMA) serves 1..4 tokens
 
 // --- vector-FMA linear (k_gemv), 1..4 tokens
@@ -85,14 +86,20 @@ struct AttnParams {
     void* kc;
     void* vc;
     float* out;
-    float* part;  // split partials [H][splits][HD + 2]
+    float* part;  // split partials [n_kv][splits][G][HD + 2]
     int n_heads, n_kv, head_dim, maxt, kv_bf16;
     float eps, scale;
 };
-constexpr int kAttnSpan = 128;  // positions one attention workgroup covers at most
+constexpr int kAttnThreads = 256;
+constexpr int kAttnSpan = 64;         // positions one attention workgroup covers at most
+constexpr int kAttnMaxSplits = 128;   // so the context is at most 8192 positions
 inline size_t attn_lds_bytes(int hd, int g) {
-    return 4 * ((size_t)g * hd + 2 * (size_t)hd + 4 * (size_t)g + 2 * (size_t)g + (size_t)g * kAttnSpan +
-                4 * (size_t)g * hd);
+    const size_t pg = kAttnThreads / (hd / 2);  // position groups of the value sums
+    return 4 * ((size_t)g * hd + 2 * (size_t)hd + (size_t)kAttnSpan * g + 4 * (size_t)g + 2 * (size_t)g +
+                pg * g * hd);
+}
+inline size_t attn_part_floats(int n_kv, int g, int hd, int splits) {
+    return (size_t)n_kv * splits * g * (hd + 2);
 }
 int launch_attn(const AttnParams& p, int splits, hipStream_t st);
 

@@ -27,7 +27,7 @@ extern "C" {
 enum rv12_status {
     RV12_OK = 0,
     RV12_E_NULL = -1,      /* a required pointer is NULL */
-    RV12_E_SHAPE = -2,     /* N < 1, K < 32, K % 32, K > 2^20, K % CH, CH % 16, or rows outside [0, N] */
+    RV12_E_SHAPE = -2,     /* N < 1, K < 32, K % 32, K > 2^20, n_exc > 2^28, K % CH, CH % 16, or rows outside [0, N] */
     RV12_E_MODE = -3,      /* mode not in {0, 1, 2} */
     RV12_E_TOKENS = -4,    /* T not in [1, 16] */
     RV12_E_WORKSPACE = -5, /* workspace smaller than rv12_workspace_bytes() */
@@ -164,14 +164,15 @@ int rv12_decode_rows(const rv12_matrix* w, int first, int last, void* out, int o
  * attention of each head over positions 0..*pos (softmax(q.K * scale) V).
  * *pos is read on the device, so a captured graph can advance it; a *pos
  * outside [0, maxt) gives zeros and touches no cache.  The positions are spread
- * over `splits` workgroups per kv head, each covering at most 128 of them
- * (so splits >= maxt / 128, at most 64: maxt <= 8192); splits > 1 adds a
- * combine pass (workspace from rv12_attn_workspace_bytes).  Replaces rope_attn_k,
+ * over `splits` workgroups per kv head, each covering at most 64 of them (so
+ * splits >= maxt / 64, at most 128: maxt <= 8192); splits > 1 adds a combine
+ * pass over partials in the workspace (rv12_attn_workspace_bytes).  Calls
+ * sharing a workspace must be ordered on one stream.  Replaces rope_attn_k,
  * ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213. */
 typedef struct rv12_attn {
     int32_t n_heads, n_kv, head_dim, maxt;
     int32_t kv_bf16; /* 1: bf16 cache, 0: float32 cache */
-    int32_t splits;  /* 1..64 */
+    int32_t splits;  /* 1..128 */
     float eps, scale;
 } rv12_attn;
 

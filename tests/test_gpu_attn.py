@@ -42,15 +42,17 @@ def test_rope_attn_matches_torch(H, KV, HD, kv_dtype):
     inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
     qn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
     kn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
-    for splits in (3, 4, 16):
-        for pos in (0, 1, 37, maxt - 1):
+    for splits in (5, 8, 19):
+        # one object per split count: its workspace serves every call, as in
+        # a decode loop
+        att = RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev, splits=splits)
+        for pos in (0, 1, 37, 130, maxt - 1):
             print("case", H, KV, HD, kv_dtype, splits, pos, flush=True)
             qkv = torch.randn((H + 2 * KV) * HD, device=dev, generator=g) * 3
             kc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
             vc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
             kc0, vc0 = kc.clone(), vc.clone()
             out = torch.zeros(H * HD, device=dev)
-            att = RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev, splits=splits)
             att(qkv, qn, kn, inv, torch.tensor([pos], device=dev), kc, vc, out)
             torch.cuda.synchronize()
             ref, kr, vr = _torch_ref(qkv, qn, kn, inv, pos, kc0, vc0, H, KV, HD, eps, k_at_pos=kc[:, pos].clone())
@@ -83,11 +85,11 @@ def test_position_outside_cache_gives_zeros():
 
 
 def test_single_split_and_split_limits():
-    """One split (a short cache) matches several; more than 128 positions per
-    split is rejected before any launch."""
+    """One split (a short cache) matches several; more than 64 positions per
+    split, or more than 128 splits, is rejected before any launch."""
     from ai_amd.attn import RopeAttn
     dev = "cuda"
-    H, KV, HD, maxt = 16, 8, 128, 128
+    H, KV, HD, maxt = 16, 8, 128, 64
     g = torch.Generator(device=dev).manual_seed(5)
     inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
     ones = torch.ones(HD, device=dev)
@@ -104,6 +106,75 @@ def test_single_split_and_split_limits():
     torch.cuda.synchronize()
     assert torch.allclose(outs[0], outs[1], rtol=1e-5, atol=1e-6)
     assert torch.allclose(outs[0], outs[2], rtol=1e-5, atol=1e-6)
-    with pytest.raises(ValueError):
-        RopeAttn(H, KV, HD, 300, torch.float32, 1e-6, dev, splits=2)(
-            qkv, ones, ones, inv, torch.tensor([0], device=dev), kc, vc, torch.zeros(H * HD, device=dev))
+    for mt, splits in ((300, 2), (9000, 128), (300, 129)):
+        with pytest.raises(ValueError):
+            RopeAttn(H, KV, HD, mt, torch.float32, 1e-6, dev, splits=splits)(
+                qkv, ones, ones, inv, torch.tensor([0], device=dev), kc, vc, torch.zeros(H * HD, device=dev))
+
+
+def test_long_cache_many_splits():
+    """8192 positions over 128 splits, bf16 cache, against the float64
+    reference at a few positions."""
+    from ai_amd.attn import RopeAttn
+    dev = "cuda"
+    H, KV, HD, maxt = 32, 8, 128, 8192
+    g = torch.Generator(device=dev).manual_seed(11)
+    inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+    qn = 1 + 0.1 * torch.randn(HD, device=dev, generator=g)
+    kn = 1 + 0.1 * torch.randn(HD, device=dev, generator=g)
+    att = RopeAttn(H, KV, HD, maxt, torch.bfloat16, 1e-6, dev)
+    assert att.a.splits == 128
+    for pos in (5, 4100, maxt - 1):
+        print("pos", pos, flush=True)
+        qkv = torch.randn((H + 2 * KV) * HD, device=dev, generator=g) * 3
+        kc = torch.randn(KV, maxt, HD, device=dev, generator=g).bfloat16()
+        vc = torch.randn(KV, maxt, HD, device=dev, generator=g).bfloat16()
+        kc0, vc0 = kc.clone(), vc.clone()
+        out = torch.zeros(H * HD, device=dev)
+        att(qkv, qn, kn, inv, torch.tensor([pos], device=dev), kc, vc, out)
+        torch.cuda.synchronize()
+        ref, _, _ = _torch_ref(qkv, qn, kn, inv, pos, kc0, vc0, H, KV, HD, 1e-6, k_at_pos=kc[:, pos].clone())
+        assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), float((out - ref).abs().max())
+
+
+def test_graph_replays_advance_the_position():
+    """The call captured in a HIP graph with the position advanced on the
+    device: every replay (eager work and a synchronisation between them)
+    matches the reference at its own position."""
+    from ai_amd.attn import RopeAttn
+    dev = "cuda"
+    H, KV, HD, maxt = 32, 8, 128, 256
+    g = torch.Generator(device=dev).manual_seed(12)
+    inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+    ones = torch.ones(HD, device=dev)
+    att = RopeAttn(H, KV, HD, maxt, torch.bfloat16, 1e-6, dev)
+    qkv = torch.randn((H + 2 * KV) * HD, device=dev, generator=g)
+    kc = torch.randn(KV, maxt, HD, device=dev, generator=g).bfloat16()
+    vc = torch.randn(KV, maxt, HD, device=dev, generator=g).bfloat16()
+    pos = torch.tensor([100], device=dev)
+    out = torch.zeros(H * HD, device=dev)
+
+    def step():
+        att(qkv, ones, ones, inv, pos, kc, vc, out)
+        pos.add_(1)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()  # eager warm call at position 100
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    pos.fill_(120)
+    for r in range(5):
+        kc0, vc0 = kc.clone(), vc.clone()
+        graph.replay()
+        torch.cuda.synchronize()
+        p = 120 + r
+        assert int(pos) == p + 1
+        ref, _, _ = _torch_ref(qkv, ones, ones, inv, p, kc0, vc0, H, KV, HD, 1e-6, k_at_pos=kc[:, p].clone())
+        assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), (r, float((out - ref).abs().max()))
+        qkv.mul_(0.9)  # eager work between the replays
