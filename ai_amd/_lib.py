@@ -22,7 +22,7 @@ RV12_E_LAUNCH = -20
 EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_pack_plan", "rv12_pack",
            "rv12_codec_to_bf16", "rv12_encode_stats", "rv12_encode", "rv12_encode_exc", "rv12_workspace_bytes",
            "rv12_gemv", "rv12_gemm", "rv12_decode_rows", "rv12_attn_workspace_bytes", "rv12_rope_attn")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class Codec(ctypes.Structure):

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define RV12_ABI_VERSION 3
+#define RV12_ABI_VERSION 4
 
 enum rv12_status {
     RV12_OK = 0,
