@@ -31,7 +31,7 @@ def test_library_exports_every_symbol():
 def test_abi_version_and_strerror():
     from ai_amd import _lib
     L = _lib.lib()
-    assert L.rv12_abi_version() == 3
+    assert L.rv12_abi_version() == 4
     for s in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -20):
         assert _lib.strerror(s) and _lib.strerror(s) != "unknown rv12 status"
     assert _lib.strerror(-99) == "unknown rv12 status"
@@ -132,3 +132,33 @@ def test_python_mirror_rejects_cpu_tensors():
     from ai_amd import wcomp
     with pytest.raises(ValueError):
         wcomp.compress(torch.zeros(4, 256, dtype=torch.bfloat16))
+
+
+def test_attention_argument_errors():
+    """Every attention argument fault is a status before any device work; the
+    workspace size follows the partial layout [n_kv][splits][G][HD + 2]."""
+    from ai_amd import _lib
+    L = _lib.lib()
+    A = lambda **kw: _lib.Attn(*[kw.get(k, d) for k, d in (("n_heads", 32), ("n_kv", 8), ("head_dim", 128),
+                                                              ("maxt", 2304), ("kv_bf16", 1), ("splits", 36),
+                                                              ("eps", 1e-6), ("scale", 128 ** -0.5))])
+    assert L.rv12_attn_workspace_bytes(ctypes.byref(A())) == 4 * 8 * 36 * 4 * 130
+    assert L.rv12_attn_workspace_bytes(ctypes.byref(A(maxt=64, splits=1))) == 0
+    p = ctypes.c_void_p(0x1000)
+
+    def call(a, ws=0x100000, ws_bytes=1 << 30, **null):
+        args = {k: (None if k in null else p) for k in ("qkv", "qn", "kn", "inv", "pos", "kc", "vc", "out")}
+        return L.rv12_rope_attn(ctypes.byref(a), *args.values(), ctypes.c_void_p(ws), ctypes.c_size_t(ws_bytes), None)
+
+    assert call(A(head_dim=96)) == _lib.RV12_E_SHAPE
+    assert call(A(n_heads=24)) == _lib.RV12_E_SHAPE          # 3 q heads per kv head
+    assert call(A(n_heads=4)) == _lib.RV12_E_SHAPE           # fewer q heads than kv heads
+    assert call(A(maxt=0)) == _lib.RV12_E_SHAPE
+    assert call(A(splits=0)) == _lib.RV12_E_CONFIG
+    assert call(A(splits=129, maxt=8192)) == _lib.RV12_E_CONFIG
+    assert call(A(splits=35)) == _lib.RV12_E_CONFIG          # 66 positions per split
+    assert call(A(maxt=8193, splits=128)) == _lib.RV12_E_CONFIG
+    assert call(A(), out=None) == _lib.RV12_E_NULL
+    assert call(A(), pos=None) == _lib.RV12_E_NULL
+    assert call(A(), ws=0) == _lib.RV12_E_WORKSPACE
+    assert call(A(), ws_bytes=1000) == _lib.RV12_E_WORKSPACE
