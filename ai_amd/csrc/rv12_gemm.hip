@@ -23,10 +23,13 @@
 //      wave's row blocks is unpacked once and meets the three parts in three
 //      MFMAs into three independent accumulators;
 //   5. epilogue per wave: the exceptions of the wave's rows whose column is
-//      inside the split are summed per (row, token) by a segmented scan over
-//      the row-major exception list, x' taken from the LDS parts; the sum of
+//      inside the split are added per (row, token) in list order (the entries
+//      found by a ballot, one at a time), x' taken from the LDS parts; the sum of
 //      the three accumulators is rescaled by 2^sc, the exception sums added,
 //      and stored (one split) or written as a partial for k_splitk_reduce.
+//      The exception range and first 64 entries, the row windows and the old
+//      y are loaded right after the weight prefetch, so the epilogue waits for
+//      no memory in the common case.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -130,6 +133,33 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
 #pragma unroll
     for (int u = 0; u < kDepth; ++u) issue_rows<RBW>(buf[u], rv, rnull, voff, s_lo + u, s_hi);
 
+    // what the epilogue reads, loaded now so that it arrives during the main
+    // loop: the wave's exception range and first 64 entries (a descriptor over
+    // the list reads zeros past its end), and per output the row window and,
+    // for an accumulating single split, the old y (rows and tokens clamped
+    // into range: no branch)
+    const int q = lane >> 4;
+    const int32_t e_lo = p.rp[min(nw, p.N)], e_hi = p.rp[min(nw + RBW * 16, p.N)];
+    const uint32_t exc_bytes = (uint32_t)min(p.n_exc, (int64_t)(1 << 28)) * 4u;
+    const __amdgpu_buffer_rsrc_t r_er = make_rsrc(p.er, exc_bytes), r_ec = make_rsrc(p.ec, exc_bytes),
+                                 r_ev = make_rsrc(p.ev, exc_bytes);
+    const uint32_t e_off = e_lo + lane < e_hi ? (uint32_t)(e_lo + lane) * 4u : 0xFFFFFFF0u;
+    const int er0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_er, (int)e_off, 0, 0);
+    const int ec0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_ec, (int)e_off, 0, 0);
+    const float ev0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_ev, (int)e_off, 0, 0));
+    int obase[RBW][4];
+    float oy[RBW][4];
+    constexpr bool kPreY = RBW <= 2;  // four row blocks per wave: y is read in the epilogue (registers)
+    const bool acc_y = kPreY && S == 1 && p.mode != 0;
+#pragma unroll
+    for (int b = 0; b < RBW; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = min(nw + b * 16 + q * 4 + i, p.N - 1);
+            obase[b][i] = p.rbase[n];
+            oy[b][i] = acc_y ? p.y[(int64_t)min(jj, T - 1) * p.N + n] : 0.0f;
+        }
+
     // ---- 3. x' split into bf16 parts, in B-operand order
     float sq = 0.0f;
 #pragma unroll
@@ -211,54 +241,47 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
 
     // ---- 5. exceptions of this wave's rows, columns inside the split
     const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(xb);
-    if (p.n_exc > 0 && nvalid > 0) {
-        const int32_t e_lo = p.rp[nw], e_hi = p.rp[min(nw + RBW * 16, p.N)];
+    if (nvalid > 0) {
         for (int32_t j0 = e_lo; j0 < e_hi; j0 += 64) {
             const int32_t j = j0 + lane;
             const bool valid = j < e_hi;
             int r = 0x7FFFFFFF, c = -1;
             float v = 0.0f;
-            if (valid) {
+            if (j0 == e_lo) {  // the first 64 entries were loaded at the start
+                if (valid) {
+                    r = er0 - nw;
+                    c = ec0 - k_lo;
+                    v = ev0;
+                }
+            } else if (valid) {  // rare: more than 64 exceptions in the wave's rows
                 r = p.er[j] - nw;
                 c = p.ec[j] - k_lo;
                 v = p.ev[j];
             }
             const bool in = valid && c >= 0 && c < krange;
-            // byte offset of x'(token 0, c) in part 0: step c/32, lane 16 * ((c%32)/8), element c%8
-            const int cb = in ? ((c >> 5) * 192 + ((c & 31) >> 3) * 16) * 16 + (c & 7) * 2 : 0;
-            float pv[16];
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                pv[t] = 0.0f;
-                if (in && t < T) {
-                    const int o = cb + t * 16;
+            // the entries inside the split, in list order (so each output adds
+            // its products in a fixed order): row, column and value made
+            // wave-uniform, lanes t < T add ev * x'(t, c) for their token
+            uint64_t m = __ballot(in);
+            while (m) {
+                const int src = __builtin_ctzll(m);
+                m &= m - 1;
+                const int rr = __builtin_amdgcn_readlane(r, src), cc = __builtin_amdgcn_readlane(c, src);
+                const float vv = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), src));
+                if (lane < T) {
+                    // byte offset of x'(token lane, cc) in part 0: step cc/32,
+                    // B lane 16 * ((cc%32)/8) + token, element cc%8
+                    const int o = (((cc >> 5) * 192 + ((cc & 31) >> 3) * 16 + lane) * 16) + (cc & 7) * 2;
                     const float xv = bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o)) +
                                      bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o + 1024)) +
                                      bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o + 2048));
-                    pv[t] = v * xv;
+                    excw[rr * 16 + lane] += vv * xv;
                 }
-            }
-            for (int d = 1; d < 64; d <<= 1) {
-                const int rn = __shfl_up(r, d);
-#pragma unroll
-                for (int t = 0; t < 16; ++t) {
-                    if (t < T) {
-                        const float o = __shfl_up(pv[t], d);
-                        if (lane >= d && rn == r) pv[t] += o;
-                    }
-                }
-            }
-            const int rnext = __shfl_down(r, 1);
-            if (valid && (lane == 63 || rnext != r)) {
-#pragma unroll
-                for (int t = 0; t < 16; ++t)
-                    if (t < T) excw[r * 16 + t] += pv[t];
             }
         }
     }
 
     // ---- 6. outputs: lane l holds token l%16, rows 4(l/16) + 0..3 of each row block
-    const int q = lane >> 4;
     float rs = 1.0f;
     if (p.lnw && S == 1 && tok) {
         float v = 0.0f;
@@ -275,11 +298,11 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
             const int rloc = b * 16 + q * 4 + i;
             const int n = nw + rloc;
             if (tok && n < p.N) {
-                float v = ldexpf(av[i], scale_exp(p.rbase[n])) + excw[rloc * 16 + jj];
+                float v = ldexpf(av[i], scale_exp(obase[b][i])) + excw[rloc * 16 + jj];
                 if (S == 1) {
-                    float* y = p.y + (int64_t)jj * p.N + n;
                     if (p.lnw) v *= rs;
-                    *y = p.mode == 0 ? v : *y + v;
+                    float* y = p.y + (int64_t)jj * p.N + n;
+                    *y = p.mode == 0 ? v : (kPreY ? oy[b][i] : *y) + v;
                 } else {
                     p.part[((int64_t)sp * T + jj) * p.npad + n] = v;
                 }

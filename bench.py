@@ -38,6 +38,11 @@ D, FF, L, V = 4096, 12288, 36, 151936
 QKV = (32 + 2 * 8) * 128
 LAYER = [("qkv", QKV, D, 0, True), ("o", D, 32 * 128, 1, False), ("gu", 2 * FF, D, 0, True),
          ("down", D, FF, 2, False)]
+# Qwen3-14B skinny-GEMM shapes (N, K): fused as the engine runs them, and unfused
+SWEEP_14B = {"qkv": (7168, 5120), "o": (5120, 5120), "gu": (34816, 5120), "down": (5120, 17408),
+             "q": (5120, 5120), "k_v": (1024, 5120), "gate_up": (17408, 5120)}
+SWEEP_M = (1, 2, 4, 8, 16)
+PEAK_BF16 = 2500.0  # TFLOP/s, MI355X dense bf16 MFMA
 SWEEP = {"q_o": (4096, 4096, 0), "k_v": (1024, 4096, 0), "gate_up": (12288, 4096, 0),
          "down": (4096, 12288, 0), "lm_head": (151936, 4096, 0), "qkv": (6144, 4096, 0),
          "gu": (24576, 4096, 0)}
@@ -225,6 +230,47 @@ def run_shape(name, reps, dev, min_bytes=1.2e9):
             "alg_GBs": ab / ms / 1e6, "frac_peak": cb / ms / 1e6 / PEAK_HBM}
 
 
+def run_skinny(name, reps, dev, min_bytes=1.2e9):
+    """Config-4 entry: one Qwen3-14B shape at every M of SWEEP_M, weights
+    N(0, 0.02) bf16 with 0.1% of output rows x20, distinct copies totalling
+    > 1 GB replayed round-robin; M <= 4 runs the vector kernel, M > 4 the bf16
+    MFMA kernel (3 MFMAs per tile: the hi/mid/lo split of x)."""
+    from ai_amd import wcomp
+    N, K = SWEEP_14B[name]
+    gen = torch.Generator().manual_seed(200 + sorted(SWEEP_14B).index(name))
+    ncopy = max(1, int(np.ceil(min_bytes / (1.5 * N * K))))
+    cs = []
+    for _ in range(ncopy):
+        w = torch.randn(N, K, device=dev, generator=torch.Generator(device=dev).manual_seed(
+            int(torch.randint(0, 2**31 - 1, (1,), generator=gen)))).mul_(0.02)
+        w[torch.randperm(N, generator=gen)[: max(1, N // 1000)].to(dev)] *= 20
+        cs.append(wcomp.compact(wcomp.compress(w.bfloat16())))
+        del w
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(16, K, device=dev, generator=g).bfloat16().float()
+    y = torch.zeros(16, N, device=dev)
+    out = []
+    for M in SWEEP_M:
+        def fn():
+            for c in cs:
+                wcomp.gemvc_tc(x, c, y, 0, M)
+
+        graph = Graph(fn)
+        ms = time_graph(graph, reps) / ncopy
+        del graph
+        cb = sum(comp_bytes(c) for c in cs) / ncopy
+        r = {"shape": name, "N": N, "K": K, "M": M, "copies": ncopy, "kernel": "k_gemv" if M <= 4 else "k_gemm",
+             "us": round(ms * 1e3, 3), "comp_GBs": round(cb / ms / 1e6, 1), "frac_peak": round(cb / ms / 1e6 / PEAK_HBM, 4),
+             "alg_TFLOPs": round(2 * M * N * K / ms / 1e9, 3)}
+        if M > 4:  # issued: 3 MFMAs over 16 token columns per tile
+            r["mfma_TFLOPs"] = round(3 * 2 * 16 * N * K / ms / 1e9, 2)
+            r["mfma_frac"] = round(r["mfma_TFLOPs"] / PEAK_BF16, 4)
+        out.append(r)
+    del cs
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(seconds=12.0):
     """The reference CPU path's linear (matmat16: bf16 weights, fp32 sums,
     ramvi/engine/ramvi_engine/cpu/cpu_layer.py:35-48) restated in C, on one
@@ -276,6 +322,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the Qwen3-8B end-to-end decode")
+    ap.add_argument("--no-14b", action="store_true", help="skip the Qwen3-14B skinny-GEMM sweep")
+    ap.add_argument("--only-14b", action="store_true", help="run only the Qwen3-14B skinny-GEMM sweep (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (scale factor of the HBM byte counters)")
     args = ap.parse_args()
@@ -295,6 +343,9 @@ def main():
         r = run_shape(args.only, args.reps, dev)
         print(json.dumps(r), flush=True)
         return
+    if args.only_14b:
+        print(json.dumps([r for name in SWEEP_14B for r in run_skinny(name, args.reps, dev)]), flush=True)
+        return
 
     tok = run_token_bench(args, dev)
     ms = tok["ms"]
@@ -313,6 +364,14 @@ def main():
             print(f"# {name}: {r['us']:.1f} us/launch, {r['comp_GBs']:.0f} GB/s ({r['frac_peak']:.1%})",
                   file=sys.stderr, flush=True)
             sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
+
+    sweep14 = []
+    if not args.no_14b:
+        for name in SWEEP_14B:
+            rs = run_skinny(name, args.reps, dev)
+            print("# 14b " + name + ": " + ", ".join(f"M{r['M']} {r['us']:.1f} us {r['frac_peak']:.1%}" for r in rs),
+                  file=sys.stderr, flush=True)
+            sweep14 += rs
 
     e2e = None
     if not args.no_e2e:
@@ -347,6 +406,7 @@ def main():
         "e2e_decode": e2e,
         "cpu_baseline": cpu,
         "sweep_m1": sweep,
+        "sweep_14b": sweep14,
     }
     print(json.dumps(line), flush=True)
 
