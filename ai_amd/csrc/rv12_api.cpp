@@ -29,30 +29,41 @@ bool shape_fits(int K, int T, const Shape& c) {
     return split_steps(K, c.splits) <= 4 * c.waves && gemm_fits(K, c.rb, c.waves, c.splits);
 }
 
-// Built-in launch shape for (N, K, T), from launch-shape sweeps of the
-// Qwen3-8B / 14B linear shapes on MI355X.
-//   vector kernel (T <= 4): one row block per workgroup and 8 waves (16 for
+// Built-in launch shapes, from launch-shape sweeps of the Qwen3-8B / 14B
+// linear shapes on MI355X.
+//   vector kernel: one row block per workgroup and 8 waves (16 for
 //     K >= 8192, 4 with two row blocks beyond 4096 row blocks); K is split
 //     only when there are fewer than 128 row blocks, so the grid still
 //     covers the 256 CUs;
-//   MFMA kernel (T > 4): 8 waves of one row block each, K split so a
-//     workgroup stages at most 1024 columns of x'.
-Shape default_shape(int N, int K, int T) {
+//   MFMA kernel: two row blocks per wave (one x' staging serves 32 rows per
+//     wave), 8 waves from 384 row blocks or K >= 8192 on, else 4; K split so
+//     a workgroup stages at most 1024 columns of x'.
+// The MFMA kernel is the built-in choice from 3 tokens on (at 3-4 tokens the
+// vector kernel's 8 FMAs per weight and token make it ALU-bound).
+Shape vector_shape(int N, int K) {
     const int64_t nblk = nblocks(N);
-    const int nsteps = K / 32;
     Shape c;
-    if (T <= kMaxVectorTokens) {
-        c.kernel = 1;
-        c.rb = nblk >= 4096 ? 2 : 1;
-        c.waves = nblk >= 4096 ? 4 : (K >= 8192 ? 16 : 8);
-        c.splits = 1;
-        if (nblk < 128) c.splits = (int)std::min<int64_t>(4, (256 + nblk - 1) / nblk);
-    } else {
-        c.kernel = 2;
-        c.rb = 1;
-        c.waves = 8;
-        c.splits = (nsteps + 31) / 32;
-    }
+    c.kernel = 1;
+    c.rb = nblk >= 4096 ? 2 : 1;
+    c.waves = nblk >= 4096 ? 4 : (K >= 8192 ? 16 : 8);
+    c.splits = 1;
+    if (nblk < 128) c.splits = (int)std::min<int64_t>(4, (256 + nblk - 1) / nblk);
+    return c;
+}
+
+Shape mfma_shape(int N, int K) {
+    const int64_t nblk = nblocks(N);
+    Shape c;
+    c.kernel = 2;
+    c.rb = 2;
+    c.waves = (nblk >= 384 || K >= 8192) ? 8 : 4;
+    c.splits = (K / 32 + 31) / 32;
+    return c;
+}
+
+Shape default_shape(int N, int K, int T) {
+    const int nsteps = K / 32;
+    Shape c = T <= kVectorDefaultTokens ? vector_shape(N, K) : mfma_shape(N, K);
     while (c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
     while (c.splits < kMaxSplits && c.splits < nsteps && !shape_fits(K, T, c)) ++c.splits;
     // the vector kernel streams best with all activations loaded before the weights
@@ -64,13 +75,9 @@ Shape default_shape(int N, int K, int T) {
 int resolve_launch(int N, int K, int T, const rv12_launch* cfg, Shape* out) {
     Shape c = default_shape(N, K, T);
     if (cfg) {
-        if (cfg->kernel) c.kernel = cfg->kernel;
-        if (cfg->kernel && cfg->kernel != default_shape(N, K, T).kernel) {
-            // another kernel than the built-in one: its own defaults first
-            c.rb = 1;
-            c.waves = 8;
-            c.splits = c.kernel == 2 ? (K / 32 + 31) / 32 : 1;
-        }
+        if (cfg->kernel && cfg->kernel != c.kernel)
+            c = cfg->kernel == 2 ? mfma_shape(N, K) : vector_shape(N, K);  // that kernel's own defaults first
+        if (cfg->kernel) c.kernel = cfg->kernel;                            // an unknown kernel is rejected below
         if (cfg->rb) c.rb = cfg->rb;
         if (cfg->waves) c.waves = cfg->waves;
         if (cfg->splits) {

@@ -37,7 +37,8 @@ constexpr size_t kMaxLds = 163840;  // LDS bytes of one gfx950 workgroup (160 KB
 constexpr size_t kDefaultLds = 65536;  // above this a kernel needs hipFuncAttributeMaxDynamicSharedMemorySize
 constexpr int kMaxK = 1 << 20;             // keeps every 32-bit buffer offset of a workgroup in range
 constexpr int64_t kMaxExc = (int64_t)1 << 28;  // exception entries of one matrix (read through 32-bit buffer ranges)
-constexpr int kMaxVectorTokens = 4;  // k_gemv (vector FMA) serves 1..4 tokens
+constexpr int kMaxVectorTokens = 4;      // k_gemv (vector FMA) serves 1..4 tokens
+constexpr int kVectorDefaultTokens = 2;  // the built-in shape runs k_gemm from 3 tokens on
 
 // --- vector-FMA linear (k_gemv), 1..4 tokens
 // K steps of the largest split

@@ -87,20 +87,23 @@ class Engine:
         self.ar = torch.arange(maxt, device=dev)
         self.attn = RopeAttn(H, KV, HD, maxt, kv_dtype, self.eps, dev)
         self.graph = None
+        self.pgraph = None  # a full prefill chunk of BATCH tokens
 
     # ---------------------------------------------------------------- layers
-    def _rope_attn(self, l, T):
+    def _rope_attn(self, l, T, p0=None):
         """Rows 0..T-1 of qkv at positions pos..pos+T-1: q/k head RMSNorm,
         RoPE, K/V into the cache (rounded to its dtype), causal attention over
         the cache (tkernels.py:82-150, 164-213).  One token: the HIP kernel;
-        a batch (prefill): torch."""
+        a batch (prefill, first position p0 known on the host): torch."""
         if T == 1:
             s = self.small[l]
             self.attn(self.qkvb[0], s["qn"], s["kn"], self.inv, self.pos, self.Kc[l], self.Vc[l], self.attb[0])
             return
-        self._rope_attn_torch(l, T)
+        self._rope_attn_torch(l, T, p0)
 
-    def _rope_attn_torch(self, l, T):
+    def _rope_attn_torch(self, l, T, p0=None):
+        """Batched prefill attention in torch; with p0 given only the cache
+        positions [0, p0 + T) take part (the rest are masked anyway)."""
         H, KV, HD = self.H, self.KV, self.HD
         G = H // KV
         qkv = self.qkvb[:T]
@@ -116,19 +119,20 @@ class Engine:
         Kc, Vc = self.Kc[l], self.Vc[l]
         Kc.index_copy_(1, p, k.to(self.kv_dtype).transpose(0, 1))
         Vc.index_copy_(1, p, v.to(self.kv_dtype).transpose(0, 1))
-        Kf, Vf = Kc.float(), Vc.float()
+        n = self.maxt if p0 is None else min(self.maxt, p0 + T)
+        Kf, Vf = Kc[:, :n].float(), Vc[:, :n].float()
         qg = q.view(T, KV, G, HD).permute(1, 2, 0, 3).reshape(KV, G * T, HD)
-        sc = torch.bmm(Kf, qg.transpose(1, 2).contiguous()).transpose(1, 2)  # [KV, G*T, maxt]
-        sc = sc.reshape(KV, G, T, self.maxt) * HD ** -0.5
-        sc = sc.masked_fill(self.ar[None, None, None, :] > p[None, None, :, None], float("-inf"))
-        a = torch.softmax(sc, -1).reshape(KV, G * T, self.maxt)
+        sc = torch.bmm(Kf, qg.transpose(1, 2).contiguous()).transpose(1, 2)  # [KV, G*T, n]
+        sc = sc.reshape(KV, G, T, n) * HD ** -0.5
+        sc = sc.masked_fill(self.ar[None, None, None, :n] > p[None, None, :, None], float("-inf"))
+        a = torch.softmax(sc, -1).reshape(KV, G * T, n)
         o = torch.bmm(a, Vf).view(KV, G, T, HD).permute(2, 0, 1, 3).reshape(T, H * HD)
         self.attb[:T].copy_(o)
 
-    def _gpu_layer(self, l, x, T):
+    def _gpu_layer(self, l, x, T, p0=None):
         """engine.py:329-341: one token with the RMS prologues fused, else the batched layer."""
         if T > 1:
-            return self._batch_layer(l, x, T)
+            return self._batch_layer(l, x, T, p0)
         W, s = self.W[l], self.small[l]
         wcomp.gemvc1(x, W["qkv"], self.qkvb[:1], 0, lnw=s["ln1"], eps=self.eps)
         self._rope_attn(l, 1)
@@ -136,21 +140,21 @@ class Engine:
         wcomp.gemvc1(x, W["gu"], self.gub[:1], 0, lnw=s["ln2"], eps=self.eps)
         wcomp.gemvc1(self.gub[:1], W["down"], x, 2)
 
-    def _batch_layer(self, l, x, T):
-        """engine.py:344-356: T <= 16 tokens of one sequence."""
+    def _batch_layer(self, l, x, T, p0=None):
+        """engine.py:344-356: T <= 16 tokens of one sequence (first position p0)."""
         W, s = self.W[l], self.small[l]
         h = self.hb[:T]
         h.copy_(_rms(x, s["ln1"].float(), self.eps))
         wcomp.gemvc_tc(h, W["qkv"], self.qkvb[:T], 0, T)
-        self._rope_attn(l, T)
+        self._rope_attn(l, T, p0)
         wcomp.gemvc_tc(self.attb[:T], W["o"], x, 1, T)
         h.copy_(_rms(x, s["ln2"].float(), self.eps))
         wcomp.gemvc_tc(h, W["gu"], self.gub[:T], 0, T)
         wcomp.gemvc_tc(self.gub[:T], W["down"], x, 2, T)
 
-    def _layers(self, x, T):
+    def _layers(self, x, T, p0=None):
         for l in range(self.L):
-            self._gpu_layer(l, x, T)
+            self._gpu_layer(l, x, T, p0)
 
     def _head_row(self, x1):
         """Greedy id of one row: the final norm fused into the 12-bit lm_head,
@@ -179,21 +183,35 @@ class Engine:
         self.steps.zero_()
         self.out.zero_()
 
-    def capture(self):
-        """Record the decode step as a HIP graph: two eager warm passes on a
-        side stream (workspaces get allocated, engine.py:432-444), then the
-        capture; the state they touched is reset."""
+    def _chunk(self):
+        """One full prefill chunk (BATCH tokens at positions pos.., tokens in
+        self.tok) through all layers: the body of the prefill graph."""
+        self._embed(BATCH)
+        self._layers(self.xb[:BATCH], BATCH)
+
+    def _record(self, fn):
+        """fn as a HIP graph: two eager warm passes on a side stream
+        (workspaces get allocated, engine.py:432-444), then the capture."""
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             for _ in range(2):
-                self._step()
+                fn()
         torch.cuda.current_stream().wait_stream(s)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self._step()
+            fn()
         torch.cuda.synchronize()
-        self.graph = g
+        return g
+
+    def capture(self):
+        """Record the decode step and a full prefill chunk as HIP graphs (the
+        reference captures one graph per batch bucket, engine.py:31, 432-444);
+        the state the warm passes touched is reset."""
+        self.graph = self._record(self._step)
+        if self.maxt > BATCH:
+            self.pos.zero_()
+            self.pgraph = self._record(self._chunk)
         self.reset()
 
     def prefill(self, tokens):
@@ -208,8 +226,11 @@ class Engine:
             T = min(BATCH, P - c0)
             self.pos.fill_(c0)
             self.tok[:T].copy_(t[c0:c0 + T])
-            self._embed(T)
-            self._layers(self.xb[:T], T)
+            if T == BATCH and self.pgraph is not None:
+                self.pgraph.replay()
+            else:
+                self._embed(T)
+                self._layers(self.xb[:T], T, c0)
         last = (P - 1) % BATCH
         self._head_row(self.xb[last:last + 1])
         self.pos.fill_(P)

@@ -31,6 +31,7 @@ from ._lib import Codec, Launch, Matrix, check, lib
 
 CFG1 = {}  # (N, K, MODE) -> (BN, waves) or (BN, waves, S); filled by ai_amd.tune
 CFGT = {}  # (N, K, MODE) -> (BN, waves, S); filled by ai_amd.tune
+VECTOR_TOKENS = 2  # the library's built-in kernel: vector FMA up to 2 tokens, bf16 MFMA above
 _SK = {}   # (N, device) -> workspace tensor (split-K partial sums)
 
 
@@ -185,11 +186,12 @@ def decompress(c):
 
 def _launch(BN, w, S, T):
     """Launch struct for the reference's tuning triple.  BN = rows per
-    workgroup: row blocks of 16 per workgroup in the vector kernel (T <= 4),
-    row blocks per wave times waves in the MFMA kernel (T > 4)."""
+    workgroup: row blocks of 16 per workgroup in the vector kernel (the
+    built-in choice for T <= 2), row blocks per wave times waves in the MFMA
+    kernel (T > 2)."""
     rb = 0
     if BN:
-        per = BN // 16 if T <= 4 else BN // (16 * int(w or 8))
+        per = BN // 16 if T <= VECTOR_TOKENS else BN // (16 * int(w or 8))
         rb = 1 if per <= 1 else (2 if per <= 2 else 4)
     return Launch(0, rb, int(w or 0), int(S or 0))
 
@@ -255,7 +257,7 @@ def gemvc1(x, c, y, mode, BN=None, w=None, lnw=None, eps=1e-6):
 def gemvc_tc(x, c, y, mode, T, BN=None, w=None, S=None):
     """1 <= T <= 16 token rows: y[t] (=|+=) W x'[t] (wcomp.py:155-242)."""
     N, K = int(c["N"]), int(c["K"])
-    if BN is None:
+    if BN is None and int(T) > VECTOR_TOKENS:  # CFGT is tuned at 16 tokens, for the MFMA kernel
         cfg = CFGT.get((N, K, mode))
         if cfg:
             BN, w, S = cfg

@@ -105,13 +105,21 @@ def test_shapes_and_launch_shapes(N, K):
     cnp = codec.compress(bits)
     cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
     nsteps = K // 32
+    # vector kernel (the built-in choice up to 2 tokens): BN rows per workgroup
     for BN, w, S in ((16, 1, 1), (16, 4, 1), (32, 2, 2), (64, 4, 1), (16, 3, min(5, nsteps)), (16, 4, nsteps)):
         if N % BN:
             BN = None  # the reference's N % BN rule; the default row tiling handles any N
         print("  launch", BN, w, S, flush=True)
         for mode in (0, 2):
             _check(cnp, cg, 1, mode, mode == 0, 7, BN=BN, w=w)
-            _check(cnp, cg, 4, mode, False, 8, BN=BN, w=w, S=S, use_tc=True)
+            _check(cnp, cg, 2, mode, False, 8, BN=BN, w=w, S=S, use_tc=True)
+    # MFMA kernel (the built-in choice from 3 tokens): BN = row blocks per wave x waves x 16
+    for BN, w, S in ((16, 1, None), (64, 2, None), (128, 4, None), (64, 4, nsteps), (256, 8, None)):
+        if N % BN:
+            BN = None
+        print("  mfma launch", BN, w, S, flush=True)
+        for mode in (0, 2):
+            _check(cnp, cg, 3, mode, False, 9, BN=BN, w=w, S=S, use_tc=True)
 
 
 def test_bn_must_divide_rows():
