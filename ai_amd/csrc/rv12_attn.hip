@@ -298,42 +298,64 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
     }
 }
 
-// combine the splits of each head in split order: M = max m_s,
-// out = sum acc_s e^(m_s - M) / sum l_s e^(m_s - M).  One workgroup per head,
-// one thread per dim; 16 partials in flight at a time (a descriptor over the
-// group's partials reads zeros past the last split)
+// combine the splits of each head: M = max m_s, w_s = e^(m_s - M),
+// out = sum acc_s w_s / sum l_s w_s, the numerator in split order.  One
+// workgroup per head, one thread per dim; every load (the split statistics,
+// one split per thread, and the thread's value of every split, 64 at a time)
+// is issued before anything waits, so the combine costs one memory round trip.
+// Descriptors over the head's partials read zeros past the last split.
+constexpr int kCombineBatch = 64;
 __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out, int S,
                                                       int G, int HD) {
-    const int h = blockIdx.x, d = threadIdx.x;
+    __shared__ float wts[kAttnMaxSplits];
+    __shared__ float red[2][2];
+    const int h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6, nw = HD >> 6;
     const int g = h / G, i = h % G;
     const int stride = G * (HD + 2) * 4;  // bytes from one split's partial of head h to the next
     const __amdgpu_buffer_rsrc_t r =
         attn_rsrc(part + ((int64_t)g * S * G + i) * (HD + 2), (uint32_t)((S - 1) * stride + (HD + 2) * 4));
-    float M = -INFINITY;
-    for (int s0 = 0; s0 < S; s0 += 16) {
-        float m[16];
+    // statistics of splits d, d + HD (HD >= 64 threads, S <= 128)
+    float m[2], l[2];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) m[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (s0 + u) * stride + HD * 4, 0, 0));
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-            if (s0 + u < S) M = fmaxf(M, m[u]);
+    for (int u = 0; u < 2; ++u) {
+        const int s2 = d + u * HD;
+        const auto ml = __builtin_amdgcn_raw_buffer_load_b64(r, s2 * stride + HD * 4, 0, 0);
+        m[u] = s2 < S ? __uint_as_float(ml[0]) : -INFINITY;
+        l[u] = s2 < S ? __uint_as_float(ml[1]) : 0.0f;
     }
-    float num = 0.0f, den = 0.0f;
-    for (int s0 = 0; s0 < S; s0 += 16) {
-        float a[16], m[16], l[16];
+    float a[kCombineBatch];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+    for (int u = 0; u < kCombineBatch; ++u)
+        a[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, u * stride + d * 4, 0, 0));
+    // M over the splits, then the weights and the denominator
+    float mx = wave_max(fmaxf(m[0], m[1]));
+    if (lane == 0) red[0][wave] = mx;
+    __syncthreads();
+    mx = red[0][0];
+    for (int w = 1; w < nw; ++w) mx = fmaxf(mx, red[0][w]);
+    float dn = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int s2 = d + u * HD;
+        const float w8 = l[u] > 0.0f ? expf(m[u] - mx) : 0.0f;
+        if (s2 < kAttnMaxSplits) wts[s2] = w8;
+        dn = fmaf(l[u], w8, dn);
+    }
+    dn = wave_sum(dn);
+    if (lane == 0) red[1][wave] = dn;
+    __syncthreads();
+    float den = red[1][0];
+    for (int w = 1; w < nw; ++w) den += red[1][w];
+    float num = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) num = fmaf(a[u], u < S ? wts[u] : 0.0f, num);
+    for (int s0 = kCombineBatch; s0 < S; s0 += kCombineBatch) {  // contexts above 4096 positions
+#pragma unroll
+        for (int u = 0; u < kCombineBatch; ++u)
             a[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (s0 + u) * stride + d * 4, 0, 0));
-            const auto ml = __builtin_amdgcn_raw_buffer_load_b64(r, (s0 + u) * stride + HD * 4, 0, 0);
-            m[u] = __uint_as_float(ml[0]);
-            l[u] = __uint_as_float(ml[1]);
-        }
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const float w = (s0 + u < S && l[u] > 0.0f) ? expf(m[u] - M) : 0.0f;
-            num = fmaf(a[u], w, num);
-            den = fmaf(l[u], w, den);
-        }
+        for (int u = 0; u < kCombineBatch; ++u)
+            num = fmaf(a[u], s0 + u < S ? wts[min(s0 + u, kAttnMaxSplits - 1)] : 0.0f, num);
     }
     out[(int64_t)h * HD + d] = num / den;
 }
