@@ -236,6 +236,27 @@ class Engine:
         self.pos.fill_(P)
         return self.nxt[:1]
 
+    def batch_pass_ms(self, T, p0, reps=10):
+        """ms of one pass of T tokens of one sequence through every layer (the
+        reference's _batch_layer, engine.py:344-356) at positions p0..p0+T-1,
+        replayed from a HIP graph (each replay rewrites those cache slots)."""
+        if not 1 < T <= BATCH or p0 + T > self.maxt:
+            raise ValueError("T must be in 2..16 and the pass must fit the context")
+
+        def body():
+            self._embed(T)
+            self._layers(self.xb[:T], T)
+
+        self.pos.fill_(p0)
+        g = self._record(body)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
     def generate(self, prompt, max_new, timing=False):
         """Greedy ids of `max_new` tokens after `prompt`.  With timing=True also
         (prefill ms, decode ms for the max_new - 1 graph replays)."""

@@ -181,15 +181,18 @@ def copy_calibration(dev, reps=20):
     print(json.dumps({"copy_bytes": 4 * n, "launches": reps}), flush=True)
 
 
-def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0):
+def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None):
     """Greedy decode of a random-init Qwen3 (BASELINE config 3 for 8b: a
-    2048-token random-id prompt, 256 new tokens, bf16 KV cache): decode-only
-    tok/s from the graph replays after the prefill."""
+    2048-token random-id prompt, 256 new tokens; config 5 for 32b: 4096 and
+    128; bf16 KV cache): decode-only tok/s from the graph replays after the
+    prefill.  batch=T adds the reference's "batch": one pass of T tokens of the
+    same sequence through every layer (_batch_layer), replayed from a graph
+    at the position after the prompt; tok/s = T / pass time."""
     from ai_amd.engine import Engine
     from ai_amd.model import QWEN3, RandomCkpt
     ck = RandomCkpt(QWEN3[size], seed=seed)
     t0 = time.time()
-    eng = Engine(ck, maxt=prompt_len + new, kv_dtype=torch.bfloat16)
+    eng = Engine(ck, maxt=prompt_len + new + (batch or 0), kv_dtype=torch.bfloat16)
     load_s = time.time() - t0
     prompt = [int(t) for t in np.random.default_rng(seed).integers(0, ck.V, prompt_len)]
     eng.generate(prompt[:64], 8)  # capture + warm
@@ -198,6 +201,11 @@ def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0):
     out = {"model": f"qwen3-{size} random init", "prompt": prompt_len, "new_tokens": new, "kv_cache": "bf16",
            "tok_s": round(1e3 / per_tok, 2), "ms_per_token": round(per_tok, 4), "prefill_ms": round(prefill_ms, 1),
            "load_s": round(load_s, 1), "first_ids": ids[:8]}
+    if batch:
+        ms = eng.batch_pass_ms(batch, prompt_len)
+        out["batch_pass"] = {"tokens_per_pass": batch, "ms_per_pass": round(ms, 3), "tok_s": round(batch * 1e3 / ms, 2),
+                             "semantics": "T tokens of one sequence per pass (the reference's _batch_layer), "
+                                          "not independent sequences"}
     del eng
     torch.cuda.empty_cache()
     return out
@@ -323,6 +331,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the Qwen3-8B end-to-end decode")
     ap.add_argument("--no-14b", action="store_true", help="skip the Qwen3-14B skinny-GEMM sweep")
+    ap.add_argument("--no-32b", action="store_true", help="skip the Qwen3-32B end-to-end decode")
     ap.add_argument("--only-14b", action="store_true", help="run only the Qwen3-14B skinny-GEMM sweep (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (scale factor of the HBM byte counters)")
@@ -379,6 +388,13 @@ def main():
         print(f"# qwen3-8b decode: {e2e['tok_s']} tok/s ({e2e['ms_per_token']} ms/token), prefill "
               f"{e2e['prefill_ms']} ms for {e2e['prompt']} tokens", file=sys.stderr, flush=True)
 
+    e2e32 = None
+    if not args.no_e2e and not args.no_32b:
+        e2e32 = run_e2e(dev, "32b", prompt_len=4096, new=128, batch=8)
+        print(f"# qwen3-32b decode: {e2e32['tok_s']} tok/s ({e2e32['ms_per_token']} ms/token), prefill "
+              f"{e2e32['prefill_ms']} ms for {e2e32['prompt']} tokens; 8-token passes "
+              f"{e2e32['batch_pass']['tok_s']} tok/s", file=sys.stderr, flush=True)
+
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": "Qwen3-8B bs1 decode tok/s; fused GEMV effective HBM GB/s vs peak",
@@ -404,6 +420,7 @@ def main():
                      "avg_launch_us": round(us_launch, 3),
                      "alg_bytes_per_launch": round(tok["alg_bytes_layers"] / tok["launches_layers"])},
         "e2e_decode": e2e,
+        "e2e_decode_32b": e2e32,
         "cpu_baseline": cpu,
         "sweep_m1": sweep,
         "sweep_14b": sweep14,
