@@ -25,9 +25,18 @@ output counter advance) run on the device, so the host only replays the graph.
 The step's attention (head norms, RoPE, KV write, grouped-query attention)
 is one HIP kernel per layer (ai_amd.attn); the batched prefill passes use the
 same math in torch.
+
+A prompt goes through passes of up to 16 tokens (the reference's legacy
+prefill, engine.py:471-480), or, in the reference's opt-in blocked mode
+(RAMVI_PREFILL=blocked from RAMVI_PREFILL_MIN_TOKENS tokens on,
+ramvi/engine/ramvi_engine/kernels/prefill.py), all prompt tokens at once with
+each matrix decoded once and multiplied in one GEMM (ai_amd.prefill).
 """
+import os
+
 import torch
 
+from . import prefill as blocked_prefill
 from . import wcomp
 from .attn import RopeAttn
 
@@ -51,9 +60,24 @@ class Engine:
     maxt      context length of the KV cache
     kv_dtype  dtype of the KV cache (the reference keeps float32,
               engine.py:234-235; bfloat16 halves its traffic)
+    prefill   "legacy" (passes of 16 tokens) or "blocked" (ai_amd.prefill);
+              None reads RAMVI_PREFILL as the reference does
+    prefill_min  fewest prompt tokens for the blocked prefill (None:
+              RAMVI_PREFILL_MIN_TOKENS, 256)
     """
 
-    def __init__(self, ck, maxt=2048, kv_dtype=torch.float32, device="cuda", log=None):
+    def __init__(self, ck, maxt=2048, kv_dtype=torch.float32, device="cuda", log=None, prefill=None,
+                 prefill_min=None):
+        if prefill is None:
+            blocked_prefill.enabled()  # validates RAMVI_PREFILL
+            prefill = os.environ.get("RAMVI_PREFILL", "legacy")
+        if prefill not in ("legacy", "blocked"):
+            raise ValueError("prefill must be legacy or blocked")
+        if prefill_min is None:
+            prefill_min = int(os.environ.get("RAMVI_PREFILL_MIN_TOKENS", "256"))
+        if prefill_min < 0:
+            raise ValueError("prefill_min must not be negative")
+        self.prefill_mode, self.prefill_min = prefill, int(prefill_min)
         self.ck = ck
         self.L, self.D, self.H, self.KV, self.HD, self.FF, self.eps = ck.L, ck.D, ck.H, ck.KV, ck.HD, ck.FF, ck.eps
         self.V, self.maxt, self.kv_dtype = ck.V, maxt, kv_dtype
@@ -222,6 +246,8 @@ class Engine:
         if not 1 <= P < self.maxt:
             raise ValueError("prompt must fit the context")
         t = torch.tensor(tokens, dtype=torch.long, device=self.dev)
+        if self.prefill_mode == "blocked" and P >= self.prefill_min:
+            return self._prefill_blocked(t)
         for c0 in range(0, P, BATCH):
             T = min(BATCH, P - c0)
             self.pos.fill_(c0)
@@ -233,6 +259,17 @@ class Engine:
                 self._layers(self.xb[:T], T, c0)
         last = (P - 1) % BATCH
         self._head_row(self.xb[last:last + 1])
+        self.pos.fill_(P)
+        return self.nxt[:1]
+
+    def _prefill_blocked(self, t):
+        """All prompt tokens t at positions 0.. through every layer at once
+        (ai_amd.prefill.layer), then the greedy id after the last one."""
+        P = t.numel()
+        x = self.emb.index_select(0, t).float()
+        for l in range(self.L):
+            blocked_prefill.layer(self, l, x, 0)
+        self._head_row(x[P - 1:P].contiguous())
         self.pos.fill_(P)
         return self.nxt[:1]
 

@@ -181,25 +181,29 @@ def copy_calibration(dev, reps=20):
     print(json.dumps({"copy_bytes": 4 * n, "launches": reps}), flush=True)
 
 
-def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None):
-    """Greedy decode of a random-init Qwen3 (BASELINE config 3 for 8b: a
-    2048-token random-id prompt, 256 new tokens; config 5 for 32b: 4096 and
+def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefill="blocked"):
+    """Greedy decode of a random-init Qwen3 (8b: a 2048-token random-id
+    prompt, 256 new tokens; 32b: 4096 and
     128; bf16 KV cache): decode-only tok/s from the graph replays after the
-    prefill.  batch=T adds the reference's "batch": one pass of T tokens of the
+    prefill (the reference's blocked prefill: each matrix decoded once for the
+    whole prompt).  batch=T adds the reference's "batch": one pass of T tokens of the
     same sequence through every layer (_batch_layer), replayed from a graph
     at the position after the prompt; tok/s = T / pass time."""
     from ai_amd.engine import Engine
     from ai_amd.model import QWEN3, RandomCkpt
     ck = RandomCkpt(QWEN3[size], seed=seed)
     t0 = time.time()
-    eng = Engine(ck, maxt=prompt_len + new + (batch or 0), kv_dtype=torch.bfloat16)
+    eng = Engine(ck, maxt=prompt_len + new + (batch or 0), kv_dtype=torch.bfloat16, prefill=prefill)
     load_s = time.time() - t0
     prompt = [int(t) for t in np.random.default_rng(seed).integers(0, ck.V, prompt_len)]
     eng.generate(prompt[:64], 8)  # capture + warm
+    if prefill == "blocked":
+        eng.generate(prompt[:eng.prefill_min + 8], 2)  # the blocked prefill's GEMM shapes
     ids, prefill_ms, decode_ms = eng.generate(prompt, new, timing=True)
     per_tok = decode_ms / (new - 1)
     out = {"model": f"qwen3-{size} random init", "prompt": prompt_len, "new_tokens": new, "kv_cache": "bf16",
            "tok_s": round(1e3 / per_tok, 2), "ms_per_token": round(per_tok, 4), "prefill_ms": round(prefill_ms, 1),
+           "prefill": prefill,
            "load_s": round(load_s, 1), "first_ids": ids[:8]}
     if batch:
         ms = eng.batch_pass_ms(batch, prompt_len)
@@ -212,7 +216,7 @@ def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None):
 
 
 def run_shape(name, reps, dev, min_bytes=1.2e9):
-    """Config-2 sweep entry: one shape, distinct copies totalling > 1 GB
+    """Qwen3-8B linear-shape sweep entry: one shape, distinct copies totalling > 1 GB
     replayed round-robin from a graph; ms per launch."""
     from ai_amd import wcomp
     N, K, mode = SWEEP[name]
@@ -239,7 +243,7 @@ def run_shape(name, reps, dev, min_bytes=1.2e9):
 
 
 def run_skinny(name, reps, dev, min_bytes=1.2e9):
-    """Config-4 entry: one Qwen3-14B shape at every M of SWEEP_M, weights
+    """Qwen3-14B skinny-GEMM entry: one shape at every M of SWEEP_M, weights
     N(0, 0.02) bf16 with 0.1% of output rows x20, distinct copies totalling
     > 1 GB replayed round-robin; M <= 2 runs the vector kernel, M > 2 the bf16
     MFMA kernel (3 MFMAs per tile: the hi/mid/lo split of x)."""
@@ -325,7 +329,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=sorted(SWEEP), help="time one config-2 shape only (for profiling)")
+    ap.add_argument("--only", choices=sorted(SWEEP), help="time one Qwen3-8B linear shape only (for profiling)")
     ap.add_argument("--reps", type=int, default=20, help="graph replays per sweep shape")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")

@@ -12,7 +12,7 @@ GOLDEN = os.path.join(ROOT, "tests", "golden", "codec_golden.npz")
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X (runs on the GPU box)")
+    config.addinivalue_line("markers", "gpu: needs an MI355X")
 
 
 @pytest.fixture(scope="session")

@@ -8,10 +8,10 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def _check(ck, prompt, new, kv_dtype=torch.float32, maxt=None):
+def _check(ck, prompt, new, kv_dtype=torch.float32, maxt=None, prefill="legacy"):
     from ai_amd.engine import Engine
     from oracle import qwen3
-    eng = Engine(ck, maxt=maxt or len(prompt) + new + 8, kv_dtype=kv_dtype)
+    eng = Engine(ck, maxt=maxt or len(prompt) + new + 8, kv_dtype=kv_dtype, prefill=prefill, prefill_min=1)
     ids = eng.generate(prompt, new)
     again = eng.generate(prompt, new)  # graph replays are repeatable
     assert ids == again
@@ -31,6 +31,16 @@ def test_tiny_model_greedy_matches_oracle():
     ck = RandomCkpt(tiny_config(layers=2, vocab=4096), seed=11)
     prompt = [int(t) for t in np.random.default_rng(1).integers(0, ck.V, 37)]
     _check(ck, prompt, 24)
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16])
+def test_tiny_model_blocked_prefill(kv_dtype):
+    """The reference's blocked prefill (RAMVI_PREFILL=blocked): the whole
+    prompt in one pass per layer, each matrix decoded once."""
+    from ai_amd.model import RandomCkpt, tiny_config
+    ck = RandomCkpt(tiny_config(layers=2, vocab=4096), seed=14)
+    prompt = [int(t) for t in np.random.default_rng(4).integers(0, ck.V, 300)]
+    _check(ck, prompt, 16, kv_dtype=kv_dtype, prefill="blocked")
 
 
 def test_tiny_model_bf16_cache():
@@ -54,7 +64,7 @@ def test_checkpoint_folder_round_trip(tmp_path):
 
 def test_qwen3_0_6b_64_tokens():
     """Qwen3-0.6B architecture, random init: 128-token random prompt, 64
-    greedy tokens, all equal to the fp32 oracle's (BASELINE config 1)."""
+    greedy tokens, all equal to the fp32 oracle's."""
     from ai_amd.model import QWEN3, RandomCkpt
     ck = RandomCkpt(QWEN3["0.6b"], seed=0)
     prompt = [int(t) for t in np.random.default_rng(0).integers(0, ck.V, 128)]

@@ -1,7 +1,7 @@
 """GPU parity of the fused decode-linear (gemvc1 / gemvc_tc through librv12.so)
 against the oracle's closed form.
 
-Bar (north star): |y - y_ref| <= 1e-3 + 1e-2 |y_ref| in every output.  Each
+Bar: |y - y_ref| <= 1e-3 + 1e-2 |y_ref| in every output.  Each
 case is also held to the fp32 forward-error bound of the oracle
 (oracle.linear.error_bound: (K + 8) 2^-24 sum_k |w_k x'_k|), which a dropped
 exception, a wrong exponent or a transposed operand would break."""
@@ -143,7 +143,7 @@ QWEN3_8B = [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288), (6144, 409
 
 @pytest.mark.parametrize("N,K", QWEN3_8B)
 def test_qwen3_8b_shapes_full_size(N, K):
-    """Config-2 matrices (sigma ~ U(0.01, 0.05), 0.1% outlier rows x20) at full
+    """Qwen3-8B sweep matrices (sigma ~ U(0.01, 0.05), 0.1% outlier rows x20) at full
     size against the C oracle, modes 0/1/2 and RMS, T = 1 and 8."""
     from ai_amd import wcomp
     print("shape", N, K, flush=True)
