@@ -31,13 +31,21 @@ prefill, engine.py:471-480), or, in the reference's opt-in blocked mode
 (RAMVI_PREFILL=blocked from RAMVI_PREFILL_MIN_TOKENS tokens on,
 ramvi/engine/ramvi_engine/kernels/prefill.py), all prompt tokens at once with
 each matrix decoded once and multiplied in one GEMM (ai_amd.prefill).
+
+Layers past `resident` stay in host memory as packed byte images and are
+streamed into two device slots for each pass (the reference's "stream"
+placement, engine.py:34-187, 271-326: ai_amd.stream); such an engine runs its
+decode step eagerly instead of as one graph, and its prompt layer by layer.
 """
+import collections
+import itertools
 import os
+import threading
 
 import torch
 
 from . import prefill as blocked_prefill
-from . import wcomp
+from . import stream, wcomp
 from .attn import RopeAttn
 
 MATS = ("qkv", "o", "gu", "down")
@@ -64,10 +72,13 @@ class Engine:
               None reads RAMVI_PREFILL as the reference does
     prefill_min  fewest prompt tokens for the blocked prefill (None:
               RAMVI_PREFILL_MIN_TOKENS, 256)
+    resident  layers kept in HBM (the first ones); the others are streamed
+              from host memory (None: all resident)
+    pin_budget  bytes of pinned host memory for the streamed images (None: all)
     """
 
     def __init__(self, ck, maxt=2048, kv_dtype=torch.float32, device="cuda", log=None, prefill=None,
-                 prefill_min=None):
+                 prefill_min=None, resident=None, pin_budget=None):
         if prefill is None:
             blocked_prefill.enabled()  # validates RAMVI_PREFILL
             prefill = os.environ.get("RAMVI_PREFILL", "legacy")
@@ -85,11 +96,20 @@ class Engine:
         H, KV, HD = self.H, self.KV, self.HD
         self.inv = (1.0 / (ck.theta ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)  # engine.py:204
         self.emb = ck.t("model.embed_tokens.weight", dev)
+        if resident is None:
+            resident = self.L
+        if resident < 0:
+            raise ValueError("resident must not be negative")
+        self.place = ["gpu" if i < resident else "stream" for i in range(self.L)]
+        self.arena = stream.Arena(float("inf") if pin_budget is None else pin_budget)
         self.W, self.small, self.Kc, self.Vc = [], [], [], []
         for i in range(self.L):
             w = ck.layer(i, dev)
             self.small.append({k: w[k] for k in ("ln1", "ln2")} | {k: w[k].float() for k in ("qn", "kn")})
-            self.W.append({n: wcomp.compact(wcomp.compress(w[n])) for n in MATS})
+            c = {n: wcomp.compact(wcomp.compress(w[n])) for n in MATS}
+            if self.place[i] == "stream":  # engine.py:226-231: the packed image in pinned host memory
+                c = {n: self._stream_image(c[n]) for n in MATS}
+            self.W.append(c)
             self.Kc.append(torch.zeros(KV, maxt, HD, dtype=kv_dtype, device=dev))
             self.Vc.append(torch.zeros_like(self.Kc[-1]))
             del w
@@ -112,6 +132,87 @@ class Engine:
         self.attn = RopeAttn(H, KV, HD, maxt, kv_dtype, self.eps, dev)
         self.graph = None
         self.pgraph = None  # a full prefill chunk of BATCH tokens
+        self.stream_ids = [i for i in range(self.L) if self.place[i] == "stream"]
+        self.all_gpu = not self.stream_ids
+        self.loader = None
+        if not self.all_gpu:  # engine.py:241-247: two device slots per matrix
+            self.loader = stream.Loader(dev)
+            self.pending, self.last_rel, self.cslot = collections.deque(), {}, 0
+            self.order, self.phase, self.cur = None, None, None
+            mx = {n: max(self.W[l][n][0].numel() for l in self.stream_ids) for n in MATS}
+            self.cbuf = [{n: torch.empty(mx[n], dtype=torch.uint8, device=dev) for n in MATS} for _ in range(2)]
+
+    def _stream_image(self, c):
+        """(pinned host image, layout) of one packed matrix (only what the
+        kernels read: the packed form and the shape)."""
+        img, lay = stream.pack({"q16": c["q16"], "N": c["N"], "K": c["K"]})
+        return self.arena.put(img.cpu()), lay
+
+    def close(self):
+        """Stop the loader thread (engine.py:258-261)."""
+        if self.loader is not None:
+            self.loader.close()
+            self.loader = None
+
+    # ------------------------------------------------------------- streaming
+    def _request(self, l):
+        """Queue the copy of layer l's images into the next device slot; it
+        waits until that slot's previous user has released it (engine.py:264-284)."""
+        if l is None:
+            return
+        s = self.cslot
+        self.cslot ^= 1
+        pairs = [(self.W[l][n][0], self.cbuf[s][n]) for n in MATS]
+        rel = {"done": threading.Event(), "ev": None}
+        job = {"l": l, "s": s, "pairs": pairs, "wait": self.last_rel.get(s), "done": threading.Event(), "ev": None,
+               "rel": rel}
+        self.last_rel[s] = rel
+        self.pending.append(job)
+        self.loader.q.put(job)
+
+    def _acquire(self, l):
+        """Wait for layer l's images; views of them in the device slot (engine.py:286-295)."""
+        job = self.pending.popleft()
+        if job["l"] != l:
+            raise RuntimeError(f"streamed layer {job['l']} arrived where layer {l} was expected")
+        self.loader.wait(job)
+        torch.cuda.current_stream(self.dev).wait_event(job["ev"])
+        self.cur = job
+        return {n: stream.unpack(self.cbuf[job["s"]][n], self.W[l][n][1]) for n in MATS}
+
+    def _release(self, job=None):
+        """The current layer's kernels are queued: its slot may be refilled
+        once they end; request the next layer (engine.py:297-302)."""
+        job = job or self.cur
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.dev))
+        job["rel"]["ev"] = ev
+        job["rel"]["done"].set()
+        self._request(next(self.order, None))
+
+    def _set_phase(self, phase):
+        """Streaming order of a pass: every streamed layer once (prefill) or
+        round and round (decode), two requests ahead (engine.py:304-320)."""
+        if self.all_gpu or (self.phase == phase and phase != "prefill"):
+            return
+        while self.pending:
+            job = self.pending.popleft()
+            self.loader.wait(job)
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.dev))
+            job["rel"]["ev"] = ev
+            job["rel"]["done"].set()
+        self.order = iter(self.stream_ids) if phase == "prefill" else itertools.cycle(self.stream_ids)
+        self.phase = phase
+        self._request(next(self.order, None))
+        self._request(next(self.order, None))
+
+    def _weights(self, l):
+        return self.W[l] if self.place[l] == "gpu" else self._acquire(l)
+
+    def _done(self, l):
+        if self.place[l] != "gpu":
+            self._release()
 
     # ---------------------------------------------------------------- layers
     def _rope_attn(self, l, T, p0=None):
@@ -153,20 +254,22 @@ class Engine:
         o = torch.bmm(a, Vf).view(KV, G, T, HD).permute(2, 0, 1, 3).reshape(T, H * HD)
         self.attb[:T].copy_(o)
 
-    def _gpu_layer(self, l, x, T, p0=None):
+    def _gpu_layer(self, l, x, T, p0=None, W=None):
         """engine.py:329-341: one token with the RMS prologues fused, else the batched layer."""
+        W = self.W[l] if W is None else W
         if T > 1:
-            return self._batch_layer(l, x, T, p0)
-        W, s = self.W[l], self.small[l]
+            return self._batch_layer(l, x, T, p0, W)
+        s = self.small[l]
         wcomp.gemvc1(x, W["qkv"], self.qkvb[:1], 0, lnw=s["ln1"], eps=self.eps)
         self._rope_attn(l, 1)
         wcomp.gemvc1(self.attb[:1], W["o"], x, 1)
         wcomp.gemvc1(x, W["gu"], self.gub[:1], 0, lnw=s["ln2"], eps=self.eps)
         wcomp.gemvc1(self.gub[:1], W["down"], x, 2)
 
-    def _batch_layer(self, l, x, T, p0=None):
+    def _batch_layer(self, l, x, T, p0=None, W=None):
         """engine.py:344-356: T <= 16 tokens of one sequence (first position p0)."""
-        W, s = self.W[l], self.small[l]
+        W = self.W[l] if W is None else W
+        s = self.small[l]
         h = self.hb[:T]
         h.copy_(_rms(x, s["ln1"].float(), self.eps))
         wcomp.gemvc_tc(h, W["qkv"], self.qkvb[:T], 0, T)
@@ -178,7 +281,9 @@ class Engine:
 
     def _layers(self, x, T, p0=None):
         for l in range(self.L):
-            self._gpu_layer(l, x, T, p0)
+            W = self._weights(l)
+            self._gpu_layer(l, x, T, p0, W)
+            self._done(l)
 
     def _head_row(self, x1):
         """Greedy id of one row: the final norm fused into the 12-bit lm_head,
@@ -246,8 +351,11 @@ class Engine:
         if not 1 <= P < self.maxt:
             raise ValueError("prompt must fit the context")
         t = torch.tensor(tokens, dtype=torch.long, device=self.dev)
+        self._set_phase("prefill")
         if self.prefill_mode == "blocked" and P >= self.prefill_min:
             return self._prefill_blocked(t)
+        if not self.all_gpu:
+            return self._prefill_layers(t)
         for c0 in range(0, P, BATCH):
             T = min(BATCH, P - c0)
             self.pos.fill_(c0)
@@ -268,7 +376,25 @@ class Engine:
         P = t.numel()
         x = self.emb.index_select(0, t).float()
         for l in range(self.L):
-            blocked_prefill.layer(self, l, x, 0)
+            W = self._weights(l)
+            blocked_prefill.layer(self, l, x, 0, W)
+            self._done(l)
+        self._head_row(x[P - 1:P].contiguous())
+        self.pos.fill_(P)
+        return self.nxt[:1]
+
+    def _prefill_layers(self, t):
+        """Passes of up to 16 tokens, layer by layer over the whole prompt,
+        so each streamed layer crosses the bus once (engine.py:446-487)."""
+        P = t.numel()
+        x = self.emb.index_select(0, t).float()
+        for l in range(self.L):
+            W = self._weights(l)
+            for c0 in range(0, P, BATCH):
+                T = min(BATCH, P - c0)
+                self.pos.fill_(c0)
+                self._gpu_layer(l, x[c0:c0 + T], T, c0, W)
+            self._done(l)
         self._head_row(x[P - 1:P].contiguous())
         self.pos.fill_(P)
         return self.nxt[:1]
@@ -279,6 +405,8 @@ class Engine:
         replayed from a HIP graph (each replay rewrites those cache slots)."""
         if not 1 < T <= BATCH or p0 + T > self.maxt:
             raise ValueError("T must be in 2..16 and the pass must fit the context")
+        if not self.all_gpu:
+            raise ValueError("a pass replayed from a graph needs every layer resident")
 
         def body():
             self._embed(T)
@@ -299,7 +427,7 @@ class Engine:
         (prefill ms, decode ms for the max_new - 1 graph replays)."""
         if len(prompt) + max_new > self.maxt:
             raise ValueError("prompt + max_new exceed the context")
-        if self.graph is None:
+        if self.graph is None and self.all_gpu:
             self.capture()
         self.reset()
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
@@ -309,8 +437,13 @@ class Engine:
         self.tok[:1].copy_(first)
         self.steps.fill_(1)
         e[1].record()
-        for _ in range(max_new - 1):
-            self.graph.replay()
+        if self.all_gpu:
+            for _ in range(max_new - 1):
+                self.graph.replay()
+        else:  # streamed layers: the step runs eagerly, the loader two layers ahead
+            self._set_phase("decode")
+            for _ in range(max_new - 1):
+                self._step()
         e[2].record()
         torch.cuda.synchronize()
         ids = self.out[:max_new].tolist()

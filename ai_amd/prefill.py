@@ -107,14 +107,16 @@ def attention(eng, l, q, start):
     return out
 
 
-def layer(eng, l, x, start):
+def layer(eng, l, x, start, W=None):
     """One layer over all prompt rows x (fp32 [T, D], updated in place) at
     positions start.. (prefill.py:81-121): RMSNorm, qkv, q/k head norms,
     RoPE, K/V into the cache (rounded to its dtype), causal attention, o
-    (residual add), RMSNorm, gate/up, silu(g) * u, down (residual add)."""
+    (residual add), RMSNorm, gate/up, silu(g) * u, down (residual add).
+    W: the layer's matrices (a streamed layer's views), default eng.W[l]."""
     T = x.shape[0]
     H, KV, HD, FF, eps = eng.H, eng.KV, eng.HD, eng.FF, eng.eps
-    W, s = eng.W[l], eng.small[l]
+    W = eng.W[l] if W is None else W
+    s = eng.small[l]
     norm = _rms(x, s["ln1"].float(), eps)
     qkv = torch.empty(T, (H + 2 * KV) * HD, device=x.device)
     matrix(norm, W["qkv"], qkv)
