@@ -66,13 +66,38 @@ __device__ __forceinline__ float pair_val(const uint32_t (&u)[2], int e) {
     else return __uint_as_float(u[e]);
 }
 
+// Lane exchanges on the VALU, no LDS round trip: DPP within rows of 16 lanes,
+// the gfx950 lane swaps across rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within 16
+// the two 16-lane rows of each 32-lane half, then the two halves, combined
+// with op into every lane
+template <typename Op>
+__device__ __forceinline__ float rows_and_halves(float v, Op op) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppMirror>(v);
+    return rows_and_halves(v, [](float x, float y) { return x + y; });
 }
 __device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppMirror>(v));
+    return rows_and_halves(v, [](float x, float y) { return fmaxf(x, y); });
 }
 
 // RMSNorm (weight pair wa, wb) and rotate-half RoPE (cos c, sin sn) of one
@@ -110,8 +135,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
     float* kn = qs + G * HD;        // [HD] step key (normed, roped, rounded)
     float* vn = kn + HD;            // [HD] step value (rounded)
     float* wt = vn + HD;            // [P][G] weights exp(s - m)
-    float* red = wt + P * G;        // [NW][G] per-wave maxima / sums
-    float* stat = red + NW * G;     // [2 G] m, l
+    float* red = wt + P * G;        // [2][NW][G] per-wave maxima, sums
+    float* stat = red + 2 * NW * G; // [2 G] m, l
     float* wacc = stat + 2 * G;     // [PG][G][HD] value sums of the position groups
     if (pos < 0 || pos >= p.maxt) {  // a position outside the cache: zeros out, no cache access
         if (S == 1) {
@@ -221,41 +246,43 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < G; ++i) {
         float s = sc[i];
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
+        s += dpp<kDppXor1>(s);
+        s += dpp<kDppXor2>(s);
         sc[i] = valid ? s * p.scale : -INFINITY;
     }
 
-    // ---- 3. per-head max, then the weights exp(s - m) and their sum
+    // ---- 3. softmax statistics in one pass: each wave's max m_w of a head's
+    // scores and sum l_w of exp(s - m_w); after one barrier the split's max
+    // M = max_w m_w, the weights exp(s - M) and L = sum_w l_w exp(m_w - M)
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-        const float m = wave_max(sc[i]);
-        if (lane == 0) red[wave * G + i] = m;
+        const float mw = wave_max(sc[i]);
+        const float e = valid ? expf(sc[i] - mw) : 0.0f;
+        const float lw = wave_sum(qq == 0 ? e : 0.0f);
+        if (lane == 0) {
+            red[wave * G + i] = mw;
+            red[(NW + wave) * G + i] = lw;
+        }
     }
     __syncthreads();
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        float m = red[i];
+        for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w * G + i]);
+        if (qq == 0) wt[pl * G + i] = valid ? expf(sc[i] - m) : 0.0f;
+    }
     if (t < G) {
         float m = red[t];
         for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w * G + t]);
-        stat[t] = m;
-    }
-    __syncthreads();
-    float lsum[G];
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-        const float e = valid ? expf(sc[i] - stat[i]) : 0.0f;
-        if (qq == 0) wt[pl * G + i] = e;
-        lsum[i] = wave_sum(qq == 0 ? e : 0.0f);
-    }
-    __syncthreads();  // every thread has read stat[] and red[] of the max step
-    if (lane == 0)
-#pragma unroll
-        for (int i = 0; i < G; ++i) red[wave * G + i] = lsum[i];
-    __syncthreads();
-    if (t < G) {
         float l = 0.0f;
-        for (int w = 0; w < NW; ++w) l += red[w * G + t];
+        for (int w = 0; w < NW; ++w) {
+            const float lw = red[(NW + w) * G + t];
+            l += lw > 0.0f ? lw * expf(red[w * G + t] - m) : 0.0f;
+        }
+        stat[t] = m;
         stat[G + t] = l;
     }
+    __syncthreads();  // the weights of every position
 
     // ---- 4. weighted values: thread (dp, pg) over its PPG positions
     float acc[G][2];

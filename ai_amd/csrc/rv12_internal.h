@@ -96,7 +96,7 @@ constexpr int kAttnSpan = 64;         // positions one attention workgroup cover
 constexpr int kAttnMaxSplits = 128;   // so the context is at most 8192 positions
 inline size_t attn_lds_bytes(int hd, int g) {
     const size_t pg = kAttnThreads / (hd / 2);  // position groups of the value sums
-    return 4 * ((size_t)g * hd + 2 * (size_t)hd + (size_t)kAttnSpan * g + 4 * (size_t)g + 2 * (size_t)g +
+    return 4 * ((size_t)g * hd + 2 * (size_t)hd + (size_t)kAttnSpan * g + 8 * (size_t)g + 2 * (size_t)g +
                 pg * g * hd);
 }
 inline size_t attn_part_floats(int n_kv, int g, int hd, int splits) {
