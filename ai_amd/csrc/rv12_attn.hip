@@ -26,6 +26,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "rv12_device.h"
 #include "rv12_internal.h"
 
 namespace rv12 {
@@ -66,25 +67,6 @@ __device__ __forceinline__ float pair_val(const uint32_t (&u)[2], int e) {
     else return __uint_as_float(u[e]);
 }
 
-// Lane exchanges on the VALU, no LDS round trip: DPP within rows of 16 lanes,
-// the gfx950 lane swaps across rows.
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
-constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
-constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8
-constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within 16
-// the two 16-lane rows of each 32-lane half, then the two halves, combined
-// with op into every lane
-template <typename Op>
-__device__ __forceinline__ float rows_and_halves(float v, Op op) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp<kDppXor1>(v);
     v += dpp<kDppXor2>(v);

@@ -16,7 +16,8 @@
 // W * RBW row blocks; wave w owns row blocks w*RBW .. w*RBW + RBW - 1.
 //   1. every thread loads the activations of its B-operand groups (one group
 //      = one step x one lane: token l%16, k = 8(l/16) + 0..7);
-//   2. each wave issues the loads of its first kDepth weight steps;
+//   2. each wave issues the loads of its first D weight steps (D = kDepth, half
+//      that with four row blocks per wave: the same bytes in flight);
 //   3. x' is formed (MODE / RMS transform), split into hi/mid/lo and written
 //      to LDS in B-operand lane order (tokens >= T are zeros); barrier;
 //   4. main loop: per step three ds_read_b128 fetch the B parts, each of the
@@ -27,9 +28,9 @@
 //      found by a ballot, one at a time), x' taken from the LDS parts; the sum of
 //      the three accumulators is rescaled by 2^sc, the exception sums added,
 //      and stored (one split) or written as a partial for k_splitk_reduce.
-//      The exception range and first 64 entries, the row windows and the old
-//      y are loaded right after the weight prefetch, so the epilogue waits for
-//      no memory in the common case.
+//      The exception range, the row windows and the old y are loaded right
+//      after the weight prefetch, the first 64 exception entries right after
+//      the x' staging, so the epilogue waits for no memory in the common case.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -77,7 +78,10 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                    0, 0, 0);
 }
 
-template <int RBW>
+// M2: silu(g) * u prologue (MODE 2); LN: RMSNorm weight.  Template arguments,
+// so that the activation loads of step 1 are straight-line code that waits for
+// no kernel argument test.
+template <int RBW, bool M2, bool LN>
 __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int T) {
     extern __shared__ u32x4 lds4[];
     const int W = blockDim.x >> 6;
@@ -86,7 +90,9 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     const int wu = __builtin_amdgcn_readfirstlane(wave);
     const int S = gridDim.y, sp = blockIdx.y;
     const int nsteps = p.K >> 5;
-    const int s_lo = (int)((int64_t)sp * nsteps / S), s_hi = (int)((int64_t)(sp + 1) * nsteps / S);
+    // split bounds in 32 bits: nsteps <= 2^15 and S <= 64
+    const int s_lo = (int)((uint32_t)(sp * nsteps) / (uint32_t)S);
+    const int s_hi = (int)((uint32_t)((sp + 1) * nsteps) / (uint32_t)S);
     const int nst = s_hi - s_lo, k_lo = s_lo * 32, krange = nst * 32;
     const int64_t nblk = (p.N + 15) / 16;
     const int64_t blk0 = (int64_t)blockIdx.x * W * RBW;
@@ -99,29 +105,36 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     float* exc = reinterpret_cast<float*>(xb + (size_t)nst * 192);  // [W*RBW*16 rows][16 tokens]
     float* ssq = exc + W * RBW * 256;                               // [W][16]
 
-    // ---- 1. activations of this thread's B groups
+    // ---- 1. activations of this thread's B groups, as straight-line loads:
+    // a group past the split's steps reads column k_lo again and a token
+    // past T reads token T - 1 (both unused), so no load waits for a branch
     f32x4 xa[kGroupsPerThread][2], ua[kGroupsPerThread][2];
     u32x4 la[kGroupsPerThread];
     const int jj = lane & 15;  // token of every group of this thread
     const bool tok = jj < T;
+    const float* xrow = p.x + (int64_t)min(jj, T - 1) * p.xs;
 #pragma unroll
     for (int i = 0; i < kGroupsPerThread; ++i) {
         const int g = threadIdx.x + i * nthr;
         const int s = g >> 6;
-        if (s < nst && tok) {
-            const int k = k_lo + s * 32 + ((g & 63) >> 4) * 8;
-            const float* xt = p.x + (int64_t)jj * p.xs + k;
-            xa[i][0] = *reinterpret_cast<const f32x4*>(xt);
-            xa[i][1] = *reinterpret_cast<const f32x4*>(xt + 4);
-            if (p.mode == 2) {
-                ua[i][0] = *reinterpret_cast<const f32x4*>(xt + p.K);
-                ua[i][1] = *reinterpret_cast<const f32x4*>(xt + p.K + 4);
-            }
-            if (p.lnw) la[i] = *reinterpret_cast<const u32x4*>(p.lnw + k);
+        const int k = k_lo + (s < nst ? s * 32 + ((g & 63) >> 4) * 8 : 0);
+        xa[i][0] = *reinterpret_cast<const f32x4*>(xrow + k);
+        xa[i][1] = *reinterpret_cast<const f32x4*>(xrow + k + 4);
+        if constexpr (M2) {
+            ua[i][0] = *reinterpret_cast<const f32x4*>(xrow + p.K + k);
+            ua[i][1] = *reinterpret_cast<const f32x4*>(xrow + p.K + k + 4);
         }
+        if constexpr (LN) la[i] = *reinterpret_cast<const u32x4*>(p.lnw + k);
     }
+#if RV12_GEMM_XWAIT
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's activations are in
+#endif
+    // every wave's activation loads enter the memory pipeline before any
+    // weight load (a bare barrier: it orders the issue, it waits for no data)
+    __builtin_amdgcn_s_barrier();
 
-    // ---- 2. first kDepth weight steps of this wave's row blocks
+    // ---- 2. first D weight steps of this wave's row blocks
+    constexpr int D = RBW >= 4 ? kDepth / 2 : kDepth;
     const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
     const char* wbase = reinterpret_cast<const char*>(p.tiles) + wblk * (int64_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, (uint32_t)nvalid * blk_bytes);
@@ -129,36 +142,39 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     int voff[RBW];
 #pragma unroll
     for (int b = 0; b < RBW; ++b) voff[b] = (int)(b * blk_bytes) + lane * 12;
-    u32x3 buf[kDepth][RBW];
+    u32x3 buf[D][RBW];
 #pragma unroll
-    for (int u = 0; u < kDepth; ++u) issue_rows<RBW>(buf[u], rv, rnull, voff, s_lo + u, s_hi);
+    for (int u = 0; u < D; ++u) issue_rows<RBW>(buf[u], rv, rnull, voff, s_lo + u, s_hi);
 
     // what the epilogue reads, loaded now so that it arrives during the main
-    // loop: the wave's exception range and first 64 entries (a descriptor over
-    // the list reads zeros past its end), and per output the row window and,
-    // for an accumulating single split, the old y (rows and tokens clamped
-    // into range: no branch)
+    // loop: the wave's exception range (its first 64 entries are loaded after
+    // the x' staging below, so that the wait for these row pointers does not
+    // hold up the staging), and per output the row window and, for an
+    // accumulating single split, the old y (rows and tokens clamped into
+    // range: no branch)
     const int q = lane >> 4;
     const int32_t e_lo = p.rp[min(nw, p.N)], e_hi = p.rp[min(nw + RBW * 16, p.N)];
-    const uint32_t exc_bytes = (uint32_t)min(p.n_exc, (int64_t)(1 << 28)) * 4u;
-    const __amdgpu_buffer_rsrc_t r_er = make_rsrc(p.er, exc_bytes), r_ec = make_rsrc(p.ec, exc_bytes),
-                                 r_ev = make_rsrc(p.ev, exc_bytes);
-    const uint32_t e_off = e_lo + lane < e_hi ? (uint32_t)(e_lo + lane) * 4u : 0xFFFFFFF0u;
-    const int er0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_er, (int)e_off, 0, 0);
-    const int ec0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_ec, (int)e_off, 0, 0);
-    const float ev0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_ev, (int)e_off, 0, 0));
-    int obase[RBW][4];
-    float oy[RBW][4];
-    constexpr bool kPreY = RBW <= 2;  // four row blocks per wave: y is read in the epilogue (registers)
-    const bool acc_y = kPreY && S == 1 && p.mode != 0;
+    // Per row block, lane l's four rows 4(l/16) + 0..3 are consecutive: one
+    // 16-byte load of their windows and (one split, accumulating) of their
+    // old y.  With N % 4 == 0 each such group lies wholly inside or wholly
+    // past the rows, and the descriptors (over rbase and y) read zeros past
+    // the end; with N % 4 != 0 the epilogue reads them one by one instead.
+    // y is loaded whatever the mode, so every load here is straight-line and
+    // the waits of the staging below count exactly; with four row blocks per
+    // wave y is read in the epilogue (registers).
+    constexpr bool kPreY = RBW <= 2;
+    const bool vec = (p.N & 3) == 0;
+    const __amdgpu_buffer_rsrc_t r_rb = make_rsrc(p.rbase, (uint32_t)p.N * 4u);
+    const __amdgpu_buffer_rsrc_t r_y = make_rsrc(p.y, (uint32_t)((int64_t)T * p.N * 4));
+    u32x4 obase[RBW];
+    f32x4 oy[RBW];
 #pragma unroll
-    for (int b = 0; b < RBW; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int n = min(nw + b * 16 + q * 4 + i, p.N - 1);
-            obase[b][i] = p.rbase[n];
-            oy[b][i] = acc_y ? p.y[(int64_t)min(jj, T - 1) * p.N + n] : 0.0f;
-        }
+    for (int b = 0; b < RBW; ++b) {
+        const int nb = nw + b * 16 + q * 4;
+        obase[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_rb, nb * 4, 0, 0));
+        if constexpr (kPreY)
+            oy[b] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r_y, (min(jj, T - 1) * p.N + nb) * 4, 0, 0));
+    }
 
     // ---- 3. x' split into bf16 parts, in B-operand order
     float sq = 0.0f;
@@ -171,17 +187,17 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
             if (tok) {
                 float v[8] = {xa[i][0].x, xa[i][0].y, xa[i][0].z, xa[i][0].w,
                               xa[i][1].x, xa[i][1].y, xa[i][1].z, xa[i][1].w};
-                if (p.lnw) {
+                if constexpr (LN) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) sq += v[e] * v[e];
                 }
-                if (p.mode == 2) {
+                if constexpr (M2) {
                     const float u[8] = {ua[i][0].x, ua[i][0].y, ua[i][0].z, ua[i][0].w,
                                         ua[i][1].x, ua[i][1].y, ua[i][1].z, ua[i][1].w};
 #pragma unroll
                     for (int e = 0; e < 8; ++e) v[e] = silu_mul(v[e], u[e]);
                 }
-                if (p.lnw) {
+                if constexpr (LN) {
                     const uint32_t lw[4] = {la[i].x, la[i].y, la[i].z, la[i].w};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
@@ -197,7 +213,7 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
             d[128] = lo;
         }
     }
-    if (p.lnw) {
+    if constexpr (LN) {
         sq += __shfl_xor(sq, 16);
         sq += __shfl_xor(sq, 32);
         if (lane < 16) ssq[wave * 16 + lane] = sq;
@@ -206,6 +222,15 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     float* excw = exc + wu * RBW * 256;
 #pragma unroll
     for (int i = 0; i < RBW * 4; ++i) excw[i * 64 + lane] = 0.0f;
+    // the wave's first 64 exception entries (a descriptor over the list reads
+    // zeros past its end)
+    const uint32_t exc_bytes = (uint32_t)min(p.n_exc, (int64_t)(1 << 28)) * 4u;
+    const __amdgpu_buffer_rsrc_t r_er = make_rsrc(p.er, exc_bytes), r_ec = make_rsrc(p.ec, exc_bytes),
+                                 r_ev = make_rsrc(p.ev, exc_bytes);
+    const uint32_t e_off = e_lo + lane < e_hi ? (uint32_t)(e_lo + lane) * 4u : 0xFFFFFFF0u;
+    const int er0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_er, (int)e_off, 0, 0);
+    const int ec0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_ec, (int)e_off, 0, 0);
+    const float ev0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_ev, (int)e_off, 0, 0));
     __syncthreads();
 
     // ---- 4. main loop
@@ -214,15 +239,15 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     for (int b = 0; b < RBW; ++b)
 #pragma unroll
         for (int c = 0; c < 3; ++c) acc[b][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int rounds = (nst + kDepth - 1) / kDepth;
+    const int rounds = (nst + D - 1) / D;
     for (int r = 0; r < rounds; ++r) {
 #pragma unroll
-        for (int u = 0; u < kDepth; ++u) {
-            const int sr = r * kDepth + u;  // step within the split
+        for (int u = 0; u < D; ++u) {
+            const int sr = r * D + u;  // step within the split
             u32x3 cur[RBW];
 #pragma unroll
             for (int b = 0; b < RBW; ++b) cur[b] = buf[u][b];
-            issue_rows<RBW>(buf[u], rv, rnull, voff, s_lo + sr + kDepth, s_hi);
+            issue_rows<RBW>(buf[u], rv, rnull, voff, s_lo + sr + D, s_hi);
             if (sr < nst) {
                 const u32x4* bsrc = xb + (size_t)sr * 192 + lane;
                 const u32x4 b0 = bsrc[0], b1 = bsrc[64], b2 = bsrc[128];
@@ -281,9 +306,11 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
         }
     }
 
-    // ---- 6. outputs: lane l holds token l%16, rows 4(l/16) + 0..3 of each row block
+    // ---- 6. outputs: lane l holds token l%16 and rows 4(l/16) + 0..3 of each
+    // row block, four consecutive outputs of one token: one 16-byte store
+    // where all four rows exist and the token rows of y are 16-byte aligned
     float rs = 1.0f;
-    if (p.lnw && S == 1 && tok) {
+    if (LN && S == 1 && tok) {
         float v = 0.0f;
         for (int w = 0; w < W; ++w) v += ssq[w * 16 + jj];
         rs = 1.0f / sqrtf(v / (float)p.K + p.eps);
@@ -293,23 +320,36 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
         if (b >= nvalid) break;
         const f32x4 a = acc[b][0] + acc[b][1] + acc[b][2];
         const float av[4] = {a.x, a.y, a.z, a.w};
+        const int nb = nw + b * 16 + q * 4;
+        int ob[4] = {(int)obase[b].x, (int)obase[b].y, (int)obase[b].z, (int)obase[b].w};
+        if (!vec) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int rloc = b * 16 + q * 4 + i;
-            const int n = nw + rloc;
-            if (tok && n < p.N) {
-                float v = ldexpf(av[i], scale_exp(obase[b][i])) + excw[rloc * 16 + jj];
-                if (S == 1) {
-                    if (p.lnw) v *= rs;
-                    float* y = p.y + (int64_t)jj * p.N + n;
-                    *y = p.mode == 0 ? v : (kPreY ? oy[b][i] : *y) + v;
-                } else {
-                    p.part[((int64_t)sp * T + jj) * p.npad + n] = v;
-                }
+            for (int i = 0; i < 4; ++i) ob[i] = p.rbase[min(nb + i, p.N - 1)];
+        }
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = ldexpf(av[i], scale_exp(ob[i])) + excw[(b * 16 + q * 4 + i) * 16 + jj];
+        if (!tok) continue;
+        if (S == 1) {
+            if constexpr (LN) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] *= rs;
             }
+            float* yp = p.y + (int64_t)jj * p.N + nb;
+            if (vec && nb < p.N) {
+                f32x4 o = {v[0], v[1], v[2], v[3]};
+                if (p.mode != 0) o = (kPreY ? oy[b] : *reinterpret_cast<const f32x4*>(yp)) + o;
+                *reinterpret_cast<f32x4*>(yp) = o;
+            } else if (!vec) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (nb + i < p.N) yp[i] = p.mode == 0 ? v[i] : yp[i] + v[i];
+            }
+        } else {  // partial rows run to npad, a multiple of 16: always four
+            *reinterpret_cast<f32x4*>(p.part + ((int64_t)sp * T + jj) * p.npad + nb) = f32x4{v[0], v[1], v[2], v[3]};
         }
     }
-    if (S > 1 && p.lnw && blockIdx.x == 0 && threadIdx.x < T) {
+    if (LN && S > 1 && blockIdx.x == 0 && threadIdx.x < T) {
         float v = 0.0f;
         for (int w = 0; w < W; ++w) v += ssq[w * 16 + threadIdx.x];
         p.ssq[sp * T + threadIdx.x] = v;
@@ -317,12 +357,21 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     (void)n0;
 }
 
+template <int RBW, bool M2, bool LN>
+static void launch_t(const LinearParams& p, int T, dim3 grid, int threads, size_t lds, hipStream_t st) {
+    if (lds > kDefaultLds)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<RBW, M2, LN>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL((k_gemm<RBW, M2, LN>), grid, dim3(threads), lds, st, p, T);
+}
+
 template <int RBW>
 static void launch_r(const LinearParams& p, int T, dim3 grid, int threads, size_t lds, hipStream_t st) {
-    if (lds > kDefaultLds)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<RBW>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((k_gemm<RBW>), grid, dim3(threads), lds, st, p, T);
+    const bool m2 = p.mode == 2, ln = p.lnw != nullptr;
+    if (m2 && ln) launch_t<RBW, true, true>(p, T, grid, threads, lds, st);
+    else if (m2) launch_t<RBW, true, false>(p, T, grid, threads, lds, st);
+    else if (ln) launch_t<RBW, false, true>(p, T, grid, threads, lds, st);
+    else launch_t<RBW, false, false>(p, T, grid, threads, lds, st);
 }
 
 int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st) {

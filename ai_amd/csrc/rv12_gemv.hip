@@ -127,17 +127,11 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
 #pragma unroll
     for (int u = 0; u < D; ++u) issue_step<RB>(buf[u], rv, rnull, voff, s0 + u * W, s_hi);
 
-    // the workgroup's first round of exceptions, one entry per thread (after
-    // the weight loads: these wait for a scalar load of the row pointers); a
-    // descriptor over the n_exc entries reads zeros past the list's end
+    // the workgroup's exception range (scalar loads of the row pointers; its
+    // first round of entries is loaded after the x' staging, so that the wait
+    // for these pointers does not hold up the staging)
     const int32_t e_lo = p.rp[n0];
     const int32_t e_hi = p.rp[min(n0 + RB * 16, p.N)];
-    const uint32_t exc_bytes = (uint32_t)min(p.n_exc, (int64_t)(1 << 28)) * 4u;
-    const __amdgpu_buffer_rsrc_t r_ec = make_rsrc(p.ec, exc_bytes), r_ev = make_rsrc(p.ev, exc_bytes);
-    const int32_t j_exc = e_lo + (int32_t)threadIdx.x;
-    const uint32_t exc_off = j_exc < e_hi ? (uint32_t)j_exc * 4u : 0xFFFFFFF0u;
-    const int ec0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_ec, (int)exc_off, 0, 0);
-    const float ev0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_ev, (int)exc_off, 0, 0));
 
     // ---- 3. x' into LDS
     float sq[T];
@@ -195,6 +189,14 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
             if (lane == 0) ssq[wave * T + t] = v;
         }
     }
+    // the workgroup's first round of exceptions, one entry per thread; a
+    // descriptor over the n_exc entries reads zeros past the list's end
+    const uint32_t exc_bytes = (uint32_t)min(p.n_exc, (int64_t)(1 << 28)) * 4u;
+    const __amdgpu_buffer_rsrc_t r_ec = make_rsrc(p.ec, exc_bytes), r_ev = make_rsrc(p.ev, exc_bytes);
+    const int32_t j_exc = e_lo + (int32_t)threadIdx.x;
+    const uint32_t exc_off = j_exc < e_hi ? (uint32_t)j_exc * 4u : 0xFFFFFFF0u;
+    const int ec0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_ec, (int)exc_off, 0, 0);
+    const float ev0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_ev, (int)exc_off, 0, 0));
     __syncthreads();
 
     // ---- 4. main loop
@@ -246,9 +248,8 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     for (int b = 0; b < RB; ++b)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            float v = acc[b][t];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
+            // (q0 + q1) + (q2 + q3) of the four lane quarters, on the VALU
+            const float v = rows_and_halves(acc[b][t], [](float x, float y) { return x + y; });
             if (lane < 16) red[((wave * RB + b) * T + t) * 16 + lane] = v;
         }
 

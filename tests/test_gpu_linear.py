@@ -54,8 +54,9 @@ def _run(c_gpu, X, Y0, mode, T, lnw=None, BN=None, w=None, S=None, eps=1e-6, use
     ln = None if lnw is None else torch.from_numpy(lnw.view(np.int16).copy()).view(torch.bfloat16).cuda()
     if T == 1 and not use_tc:
         wcomp.gemvc1(x, c_gpu, y, mode, BN=BN, w=w, lnw=ln, eps=eps)
+    elif ln is not None:  # the C-ABI's RMS prologue at T > 1 (no reference operator has it)
+        wcomp._linear(x, c_gpu, y, mode, T, BN, w, S, ln, eps, "rv12_gemm")
     else:
-        assert ln is None
         wcomp.gemvc_tc(x, c_gpu, y, mode, T, BN=BN, w=w, S=S)
     torch.cuda.synchronize()
     return y.cpu().numpy()
@@ -83,6 +84,21 @@ def test_golden_matrices_all_modes(golden, case):
             _check(cnp, cg, 1, mode, rms, 3)
         for T in (2, 5, 16):
             _check(cnp, cg, T, mode, False, 4 + T, use_tc=True)
+
+
+@pytest.mark.parametrize("case", ["prefill_seed7", "outliers_rows_cols", "subnormal_heavy"])
+def test_rms_prologue_batched(golden, case):
+    """rv12_gemm with an RMSNorm weight at 2..16 tokens: the vector kernel at
+    2 tokens, the MFMA kernel from 3 on, one split and several."""
+    from ai_amd import wcomp
+    print("case", case, flush=True)
+    cnp = ref_dict(golden[case])
+    cg = wcomp.prepare(ref_dict(golden[case]))
+    nsteps = cnp["K"] // 32
+    for T in (2, 3, 8, 16):
+        for mode in (0, 1, 2):
+            _check(cnp, cg, T, mode, True, 20 + T + mode, use_tc=True)
+            _check(cnp, cg, T, mode, True, 30 + T + mode, use_tc=True, S=min(3, nsteps))
 
 
 def _random_matrix(N, K, seed, sigma=0.02, out_rows=0.0, out_cols=0.0):
