@@ -35,9 +35,9 @@ bool shape_fits(int K, int T, const Shape& c) {
 //     K >= 8192, 4 with two row blocks beyond 4096 row blocks); K is split
 //     only when there are fewer than 128 row blocks, so the grid still
 //     covers the 256 CUs;
-//   MFMA kernel: two row blocks per wave (one x' staging serves 32 rows per
-//     wave), 8 waves from 384 row blocks or K >= 8192 on, else 4; K split so
-//     a workgroup stages at most 1024 columns of x'.
+//   MFMA kernel: 8 waves; two row blocks per wave (one x' staging serves 32
+//     rows per wave), four from K >= 8192 on, one (and 4 waves) below 128
+//     row blocks; K split so a workgroup stages at most 1024 columns of x'.
 // The MFMA kernel is the built-in choice from 3 tokens on (at 3-4 tokens the
 // vector kernel's 8 FMAs per weight and token make it ALU-bound).
 Shape vector_shape(int N, int K) {
@@ -55,8 +55,8 @@ Shape mfma_shape(int N, int K) {
     const int64_t nblk = nblocks(N);
     Shape c;
     c.kernel = 2;
-    c.rb = 2;
-    c.waves = (nblk >= 384 || K >= 8192) ? 8 : 4;
+    c.rb = K >= 8192 ? 4 : (nblk < 128 ? 1 : 2);
+    c.waves = nblk < 128 ? 4 : 8;
     c.splits = (K / 32 + 31) / 32;
     return c;
 }
