@@ -39,7 +39,9 @@ bool shape_fits(int K, int T, const Shape& c) {
 //     rows per wave), four from K >= 8192 on, one (and 4 waves) below 128
 //     row blocks; K split so a workgroup stages at most 1024 columns of x'.
 // The MFMA kernel is the built-in choice from 3 tokens on (at 3-4 tokens the
-// vector kernel's 8 FMAs per weight and token make it ALU-bound).
+// vector kernel's 8 FMAs per weight and token make it ALU-bound), and at 2
+// tokens where the vector kernel would have to split K to hold its activations
+// in registers (Qwen3-14B down: 35 vs 37.5 us).
 Shape vector_shape(int N, int K) {
     const int64_t nblk = nblocks(N);
     Shape c;
@@ -63,7 +65,9 @@ Shape mfma_shape(int N, int K) {
 
 Shape default_shape(int N, int K, int T) {
     const int nsteps = K / 32;
-    Shape c = T <= kVectorDefaultTokens ? vector_shape(N, K) : mfma_shape(N, K);
+    bool vec = T <= kVectorDefaultTokens;
+    if (T == 2 && !gemv_prefetch_all(K, T, vector_shape(N, K).waves, 1)) vec = false;
+    Shape c = vec ? vector_shape(N, K) : mfma_shape(N, K);
     while (c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
     while (c.splits < kMaxSplits && c.splits < nsteps && !shape_fits(K, T, c)) ++c.splits;
     // the vector kernel streams best with all activations loaded before the weights
@@ -196,6 +200,18 @@ int rv12_encode_exc(const uint16_t* w, int n, int k, int base, const int32_t* rp
     if (base < 0 || base > 241) return RV12_E_BASE;
     launch_encode_exc(w, n, k, base, rp, er, ec, ev, (hipStream_t)stream);
     return launch_status();
+}
+
+int rv12_default_launch(int n, int k, int t, rv12_launch* out) {
+    if (!out) return RV12_E_NULL;
+    if (n < 1 || k < 32 || k % 32 || k > kMaxK) return RV12_E_SHAPE;
+    if (t < 1 || t > 16) return RV12_E_TOKENS;
+    const Shape c = default_shape(n, k, t);
+    out->kernel = c.kernel;
+    out->rb = c.rb;
+    out->waves = c.waves;
+    out->splits = c.splits;
+    return RV12_OK;
 }
 
 size_t rv12_workspace_bytes(int n, int k, int t, int splits) {

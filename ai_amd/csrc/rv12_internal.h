@@ -45,7 +45,7 @@ constexpr int kVectorDefaultTokens = 2;  // the built-in shape runs k_gemm from 
 inline int split_steps(int K, int splits) { return (K / 32 + splits - 1) / splits; }
 
 // float4 activation chunks per thread the kernel keeps in registers
-__host__ __device__ constexpr int gemv_chunks(int T) { return T == 1 ? 6 : (T == 2 ? 2 : 1); }
+__host__ __device__ constexpr int gemv_chunks(int T) { return T == 1 ? 6 : (T == 2 ? 3 : 1); }
 
 inline size_t gemv_lds_bytes(int K, int T, int rb, int waves, int splits) {
     const size_t krange = (size_t)split_steps(K, splits) * 32;

@@ -27,7 +27,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import Codec, Launch, Matrix, check, lib
+from ._lib import KERNEL_MFMA, KERNEL_VECTOR, Codec, Launch, Matrix, check, lib
 
 CFG1 = {}  # (N, K, MODE) -> (BN, waves) or (BN, waves, S); filled by ai_amd.tune
 CFGT = {}  # (N, K, MODE) -> (BN, waves, S); filled by ai_amd.tune
@@ -186,14 +186,25 @@ def decompress(c):
 
 def _launch(BN, w, S, T):
     """Launch struct for the reference's tuning triple.  BN = rows per
-    workgroup: row blocks of 16 per workgroup in the vector kernel (the
-    built-in choice for T <= 2), row blocks per wave times waves in the MFMA
-    kernel (T > 2)."""
-    rb = 0
+    workgroup: row blocks of 16 per workgroup in the vector kernel (T <= 2),
+    row blocks per wave times waves in the MFMA kernel (T > 2).  A given BN
+    names its kernel; without one the library picks (the vector kernel up to
+    2 tokens, except where it would have to split K at 2 tokens)."""
+    rb = kernel = 0
     if BN:
-        per = BN // 16 if T <= VECTOR_TOKENS else BN // (16 * int(w or 8))
+        vec = T <= VECTOR_TOKENS
+        per = BN // 16 if vec else BN // (16 * int(w or 8))
         rb = 1 if per <= 1 else (2 if per <= 2 else 4)
-    return Launch(0, rb, int(w or 0), int(S or 0))
+        kernel = KERNEL_VECTOR if vec else KERNEL_MFMA
+    return Launch(kernel, rb, int(w or 0), int(S or 0))
+
+
+def default_launch(N, K, T):
+    """The library's built-in (kernel, rb, waves, splits) for N x K at T
+    tokens: kernel 1 = vector FMA, 2 = bf16 MFMA (rv12_default_launch)."""
+    c = Launch()
+    check(lib().rv12_default_launch(int(N), int(K), int(T), ctypes.byref(c)), "default_launch")
+    return c.kernel, c.rb, c.waves, c.splits
 
 
 _SK_RETIRED = []  # workspaces replaced by larger ones: kept alive for graphs that captured them

@@ -274,8 +274,9 @@ def run_shape(name, reps, dev, min_bytes=1.2e9):
 def run_skinny(name, reps, dev, min_bytes=1.2e9):
     """Qwen3-14B skinny-GEMM entry: one shape at every M of SWEEP_M, weights
     N(0, 0.02) bf16 with 0.1% of output rows x20, distinct copies totalling
-    > 1 GB replayed round-robin; M <= 2 runs the vector kernel, M > 2 the bf16
-    MFMA kernel (3 MFMAs per tile: the hi/mid/lo split of x)."""
+    > 1 GB replayed round-robin, with the library's built-in kernel choice:
+    the vector kernel up to 2 tokens where its activations fit unsplit, else
+    the bf16 MFMA kernel (3 MFMAs per tile: the hi/mid/lo split of x)."""
     from ai_amd import wcomp
     N, K = SWEEP_14B[name]
     gen = torch.Generator().manual_seed(200 + sorted(SWEEP_14B).index(name))
@@ -300,10 +301,11 @@ def run_skinny(name, reps, dev, min_bytes=1.2e9):
         ms = time_graph(graph, reps) / ncopy
         del graph
         cb = sum(comp_bytes(c) for c in cs) / ncopy
-        r = {"shape": name, "N": N, "K": K, "M": M, "copies": ncopy, "kernel": "k_gemv" if M <= 2 else "k_gemm",
+        mfma = wcomp.default_launch(N, K, M)[0] == 2
+        r = {"shape": name, "N": N, "K": K, "M": M, "copies": ncopy, "kernel": "k_gemm" if mfma else "k_gemv",
              "us": round(ms * 1e3, 3), "comp_GBs": round(cb / ms / 1e6, 1), "frac_peak": round(cb / ms / 1e6 / PEAK_HBM, 4),
              "alg_TFLOPs": round(2 * M * N * K / ms / 1e9, 3)}
-        if M > 2:  # issued: 3 MFMAs over 16 token columns per tile
+        if mfma:  # issued: 3 MFMAs over 16 token columns per tile
             r["mfma_TFLOPs"] = round(3 * 2 * 16 * N * K / ms / 1e9, 2)
             r["mfma_frac"] = round(r["mfma_TFLOPs"] / PEAK_BF16, 4)
         out.append(r)

@@ -79,11 +79,20 @@ typedef struct rv12_matrix {
  *   waves   waves per workgroup (1..16)
  *   splits  K splits across workgroups (1..64); more than one adds a second,
  *           atomic-free pass that sums the partials in split order
- * A zero field (or a NULL pointer) selects the built-in choice for the shape:
- * the vector kernel for T <= 4, the MFMA kernel above. */
+ * A zero field (or a NULL pointer) selects the built-in choice for the shape
+ * (rv12_default_launch). */
 typedef struct rv12_launch {
     int32_t kernel, rb, waves, splits;
 } rv12_launch;
+
+/* The built-in launch shape for n rows, k columns and t tokens: the vector
+ * kernel up to 2 tokens (at 2 only while its activations fit in registers
+ * without splitting K), the MFMA kernel above; waves, row blocks and splits
+ * from launch-shape sweeps on MI355X.  Fills *out and returns RV12_OK, or
+ * RV12_E_NULL / RV12_E_SHAPE / RV12_E_TOKENS for what the linears reject.
+ * The default the reference's tuning tables fall back to, CFG1 / CFGT in
+ * ramvi/engine/ramvi_engine/kernels/wcomp.py:115, 222. */
+int rv12_default_launch(int n, int k, int t, rv12_launch* out);
 
 /* ABI version of the library (RV12_ABI_VERSION).  Mirrors the reference's
  * native ABI check, ramvi/engine/ramvi_engine/native/qmm.cpp:24. */

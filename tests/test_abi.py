@@ -48,6 +48,31 @@ def test_sizes():
     assert L.rv12_workspace_bytes(4096, 4096, 17, 1) == 0
 
 
+def test_default_launch_shapes():
+    """The built-in launch table (host code only): the vector kernel up to 2
+    tokens while its activations fit unsplit, the MFMA kernel beyond."""
+    from ai_amd import _lib
+    L = _lib.lib()
+
+    def shape(n, k, t):
+        c = _lib.Launch()
+        assert L.rv12_default_launch(n, k, t, ctypes.byref(c)) == _lib.RV12_OK
+        return (c.kernel, c.rb, c.waves, c.splits)
+
+    assert shape(6144, 4096, 1) == (1, 1, 8, 1)           # Qwen3-8B qkv, one token
+    assert shape(4096, 12288, 1) == (1, 1, 16, 1)         # down: 16 waves for K >= 8192
+    assert shape(151936, 4096, 1) == (1, 2, 4, 1)         # lm_head: two row blocks per workgroup
+    assert shape(5120, 17408, 2)[0] == 2                  # Qwen3-14B down at 2 tokens: MFMA
+    assert shape(7168, 5120, 2) == (1, 1, 8, 1)           # 14B qkv at 2 tokens: vector, unsplit
+    assert shape(5120, 17408, 16)[:3] == (2, 4, 8)        # MFMA, four row blocks per wave
+    assert shape(1024, 5120, 16)[:3] == (2, 1, 4)         # fewer than 128 row blocks
+    assert shape(5120, 5120, 8) == (2, 2, 8, 5)
+    c = _lib.Launch()
+    assert L.rv12_default_launch(64, 100, 1, ctypes.byref(c)) == _lib.RV12_E_SHAPE
+    assert L.rv12_default_launch(64, 256, 17, ctypes.byref(c)) == _lib.RV12_E_TOKENS
+    assert L.rv12_default_launch(64, 256, 1, None) == _lib.RV12_E_NULL
+
+
 def _mat(n=64, k=256, tiles=0x1000, n_exc=0, rbase=0x1800):
     from ai_amd import _lib
     return _lib.Matrix(tiles, rbase, 0x2000, 0x3000 if n_exc else 0, 0x4000 if n_exc else 0,

@@ -215,3 +215,20 @@ def test_tuned_launch_shapes_keep_parity(tmp_path):
     finally:
         wcomp.CFG1.clear()
         wcomp.CFGT.clear()
+
+
+def test_two_tokens_with_k_beyond_the_vector_staging():
+    """At 2 tokens the library runs the vector kernel while its activations fit
+    in registers unsplit and the MFMA kernel beyond (K > 12288 here); both
+    sides of the switch, every mode, with and without the RMS prologue."""
+    from ai_amd import wcomp
+    for N, K in ((100, 12288), (100, 16384)):
+        print("shape", N, K, flush=True)
+        bits = _random_matrix(N, K, 31 + K, out_rows=0.01, out_cols=0.001)
+        cnp = codec.compress(bits)
+        cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+        for mode in (0, 1, 2):
+            _check(cnp, cg, 2, mode, False, 40 + mode, use_tc=True)
+            _check(cnp, cg, 2, mode, True, 50 + mode, use_tc=True)
+        del cg
+        torch.cuda.empty_cache()
