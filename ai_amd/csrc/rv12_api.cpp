@@ -35,9 +35,8 @@ bool shape_fits(int K, int T, const Shape& c) {
 //     K >= 8192, 4 with two row blocks beyond 4096 row blocks); K is split
 //     only when there are fewer than 128 row blocks, so the grid still
 //     covers the 256 CUs;
-//   MFMA kernel: 8 waves; two row blocks per wave (one x' staging serves 32
-//     rows per wave), four from K >= 8192 on, one (and 4 waves) below 128
-//     row blocks; K split so a workgroup stages at most 1024 columns of x'.
+//   MFMA kernel: the shape with the least time in a model of its rounds of
+//     workgroups (mfma_model_us);
 // The MFMA kernel is the built-in choice from 3 tokens on (at 3-4 tokens the
 // vector kernel's 8 FMAs per weight and token make it ALU-bound), and at 2
 // tokens where the vector kernel would have to split K to hold its activations
@@ -53,21 +52,78 @@ Shape vector_shape(int N, int K) {
     return c;
 }
 
-Shape mfma_shape(int N, int K) {
+// Time model of the MFMA kernel, in us (constants from register timestamps
+// and launch-shape sweeps on MI355X).  A workgroup stages x' for its K split
+// in LDS before streaming, so the launch runs in rounds: one workgroup per CU
+// at 8 waves (registers allow two waves per SIMD), two at 4 waves where the
+// LDS holds both.  Each round costs a fixed prologue (kernel arguments, x'
+// staging, barrier: ~5 us at 16 tokens) plus its weight bytes at the smaller
+// of the HBM rate and 45 GB/s per active CU (the bytes one CU keeps in
+// flight over the memory latency); a K split adds the reduce pass.  The model
+// ranks the measured 8B/14B/32B shapes at 8-16 tokens as the sweeps do (e.g.
+// 32B o 5120x8192: 2 row blocks per wave, 160 workgroups, 20 us; 4 row blocks,
+// 90 workgroups, 30 us).
+constexpr double kModelPrologueUs = 5.0;
+constexpr double kModelHbmGBs = 6500.0;
+constexpr double kModelCuGBs = 45.0;
+constexpr double kModelLaunchUs = 1.6;
+constexpr int kModelCUs = 256;
+constexpr double kModelStepBytes = 768.0;  // one (row block, step) tile
+
+double mfma_model_us(int64_t nblk, int N, int K, int T, int rb, int waves, int splits) {
+    const int64_t per_wg = (int64_t)rb * waves;
+    const int64_t wgs = (nblk + per_wg - 1) / per_wg * splits;
+    const int per_cu = (waves <= 4 && 2 * gemm_lds_bytes(K, rb, waves, splits) <= kMaxLds) ? 2 : 1;
+    const double wg_bytes = (double)per_wg * split_steps(K, splits) * kModelStepBytes;
+    double t = 0.0;
+    for (int64_t left = wgs; left > 0;) {
+        const int64_t n = std::min<int64_t>(left, (int64_t)kModelCUs * per_cu);
+        const double active = (double)std::min<int64_t>(n, kModelCUs);
+        t += kModelPrologueUs + (double)n * wg_bytes / (std::min(kModelHbmGBs, active * kModelCuGBs) * 1e3);
+        left -= n;
+    }
+    if (splits > 1) t += kModelLaunchUs + (double)(splits + 1) * T * N * 4 / (kModelHbmGBs * 1e3);
+    return t;
+}
+
+// candidates: 1, 2 or 4 row blocks per wave, 4 or 8 waves, the fewest K
+// splits whose staging fits and up to 8 more
+Shape mfma_shape(int N, int K, int T) {
     const int64_t nblk = nblocks(N);
-    Shape c;
-    c.kernel = 2;
-    c.rb = K >= 8192 ? 4 : (nblk < 128 ? 1 : 2);
-    c.waves = nblk < 128 ? 4 : 8;
-    c.splits = (K / 32 + 31) / 32;
-    return c;
+    const int nsteps = K / 32;
+    Shape best;
+    best.kernel = 2;
+    best.rb = 1;
+    best.waves = 1;
+    best.splits = nsteps;
+    double best_t = 1e300;
+    for (int rb : {1, 2, 4}) {
+        for (int w : {4, 8}) {
+            const int wv = std::min(w, nsteps);  // no more waves than K steps
+            auto fits = [&](int s) { return split_steps(K, s) <= 4 * wv && gemm_fits(K, rb, wv, s); };
+            int s0 = 1;
+            while (s0 < std::min(kMaxSplits, nsteps) && !fits(s0)) ++s0;
+            if (!fits(s0)) continue;
+            for (int s = s0; s <= std::min({s0 + 8, kMaxSplits, nsteps}); ++s) {
+                if (!fits(s)) continue;
+                const double t = mfma_model_us(nblk, N, K, T, rb, wv, s);
+                if (t < best_t) {
+                    best_t = t;
+                    best.rb = rb;
+                    best.waves = wv;
+                    best.splits = s;
+                }
+            }
+        }
+    }
+    return best;
 }
 
 Shape default_shape(int N, int K, int T) {
     const int nsteps = K / 32;
     bool vec = T <= kVectorDefaultTokens;
     if (T == 2 && !gemv_prefetch_all(K, T, vector_shape(N, K).waves, 1)) vec = false;
-    Shape c = vec ? vector_shape(N, K) : mfma_shape(N, K);
+    Shape c = vec ? vector_shape(N, K) : mfma_shape(N, K, T);
     while (c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
     while (c.splits < kMaxSplits && c.splits < nsteps && !shape_fits(K, T, c)) ++c.splits;
     // the vector kernel streams best with all activations loaded before the weights
@@ -80,7 +136,7 @@ int resolve_launch(int N, int K, int T, const rv12_launch* cfg, Shape* out) {
     Shape c = default_shape(N, K, T);
     if (cfg) {
         if (cfg->kernel && cfg->kernel != c.kernel)
-            c = cfg->kernel == 2 ? mfma_shape(N, K) : vector_shape(N, K);  // that kernel's own defaults first
+            c = cfg->kernel == 2 ? mfma_shape(N, K, T) : vector_shape(N, K);  // that kernel's own defaults first
         if (cfg->kernel) c.kernel = cfg->kernel;                            // an unknown kernel is rejected below
         if (cfg->rb) c.rb = cfg->rb;
         if (cfg->waves) c.waves = cfg->waves;
@@ -202,11 +258,13 @@ int rv12_encode_exc(const uint16_t* w, int n, int k, int base, const int32_t* rp
     return launch_status();
 }
 
-int rv12_default_launch(int n, int k, int t, rv12_launch* out) {
+int rv12_launch_shape(int n, int k, int t, const rv12_launch* cfg, rv12_launch* out) {
     if (!out) return RV12_E_NULL;
     if (n < 1 || k < 32 || k % 32 || k > kMaxK) return RV12_E_SHAPE;
     if (t < 1 || t > 16) return RV12_E_TOKENS;
-    const Shape c = default_shape(n, k, t);
+    Shape c;
+    const int rc = resolve_launch(n, k, t, cfg, &c);
+    if (rc) return rc;
     out->kernel = c.kernel;
     out->rb = c.rb;
     out->waves = c.waves;

@@ -199,11 +199,13 @@ def _launch(BN, w, S, T):
     return Launch(kernel, rb, int(w or 0), int(S or 0))
 
 
-def default_launch(N, K, T):
-    """The library's built-in (kernel, rb, waves, splits) for N x K at T
-    tokens: kernel 1 = vector FMA, 2 = bf16 MFMA (rv12_default_launch)."""
+def launch_shape(N, K, T, cfg=None):
+    """(kernel, rb, waves, splits) a linear of N x K at T tokens runs with for
+    the Launch cfg (None: the built-in choice); kernel 1 = vector FMA, 2 =
+    bf16 MFMA (rv12_launch_shape)."""
     c = Launch()
-    check(lib().rv12_default_launch(int(N), int(K), int(T), ctypes.byref(c)), "default_launch")
+    check(lib().rv12_launch_shape(int(N), int(K), int(T), None if cfg is None else ctypes.byref(cfg),
+                                  ctypes.byref(c)), "launch_shape")
     return c.kernel, c.rb, c.waves, c.splits
 
 
@@ -246,7 +248,7 @@ def _linear(x, c, y, mode, T, BN, w, S, lnw, eps, where):
             raise ValueError(f"{where}: lnw must be a contiguous bf16 vector of K entries")
     m = _matrix(c)
     cfg = _launch(BN, w, S, T)
-    splits = int(S or 0)
+    splits = launch_shape(N, K, T, cfg)[3]  # the split count the launch resolves to
     ws = _sk_buf(N, splits, x.device, K, T)
     rc = lib().rv12_gemm(ctypes.byref(m), _ptr(x), _ptr(y), int(T), _ptr(lnw), float(eps), int(mode),
                          ctypes.byref(cfg), _ptr(ws), ws.numel(), _stream(x.device))

@@ -301,7 +301,7 @@ def run_skinny(name, reps, dev, min_bytes=1.2e9):
         ms = time_graph(graph, reps) / ncopy
         del graph
         cb = sum(comp_bytes(c) for c in cs) / ncopy
-        mfma = wcomp.default_launch(N, K, M)[0] == 2
+        mfma = wcomp.launch_shape(N, K, M)[0] == 2
         r = {"shape": name, "N": N, "K": K, "M": M, "copies": ncopy, "kernel": "k_gemm" if mfma else "k_gemv",
              "us": round(ms * 1e3, 3), "comp_GBs": round(cb / ms / 1e6, 1), "frac_peak": round(cb / ms / 1e6 / PEAK_HBM, 4),
              "alg_TFLOPs": round(2 * M * N * K / ms / 1e9, 3)}

@@ -80,19 +80,22 @@ typedef struct rv12_matrix {
  *   splits  K splits across workgroups (1..64); more than one adds a second,
  *           atomic-free pass that sums the partials in split order
  * A zero field (or a NULL pointer) selects the built-in choice for the shape
- * (rv12_default_launch). */
+ * (rv12_launch_shape). */
 typedef struct rv12_launch {
     int32_t kernel, rb, waves, splits;
 } rv12_launch;
 
-/* The built-in launch shape for n rows, k columns and t tokens: the vector
- * kernel up to 2 tokens (at 2 only while its activations fit in registers
- * without splitting K), the MFMA kernel above; waves, row blocks and splits
- * from launch-shape sweeps on MI355X.  Fills *out and returns RV12_OK, or
- * RV12_E_NULL / RV12_E_SHAPE / RV12_E_TOKENS for what the linears reject.
- * The default the reference's tuning tables fall back to, CFG1 / CFGT in
- * ramvi/engine/ramvi_engine/kernels/wcomp.py:115, 222. */
-int rv12_default_launch(int n, int k, int t, rv12_launch* out);
+/* The launch shape a linear of n rows, k columns and t tokens runs with for
+ * cfg (NULL or all-zero: the built-in choice — the vector kernel up to 2
+ * tokens, at 2 only while its activations fit in registers without splitting
+ * K, the MFMA kernel above, with waves, row blocks and splits from
+ * launch-shape sweeps on MI355X; zero fields of a partial cfg are filled in,
+ * with K split further where the given fields need it).  Fills *out and
+ * returns RV12_OK, or the status rv12_gemm would return for the shape and
+ * cfg (RV12_E_NULL, RV12_E_SHAPE, RV12_E_TOKENS, RV12_E_CONFIG).  Size the
+ * workspace with out->splits.  The reference's launch defaults and tuning
+ * tables, CFG1 / CFGT in ramvi/engine/ramvi_engine/kernels/wcomp.py:115, 222. */
+int rv12_launch_shape(int n, int k, int t, const rv12_launch* cfg, rv12_launch* out);
 
 /* ABI version of the library (RV12_ABI_VERSION).  Mirrors the reference's
  * native ABI check, ramvi/engine/ramvi_engine/native/qmm.cpp:24. */

@@ -48,15 +48,17 @@ def test_sizes():
     assert L.rv12_workspace_bytes(4096, 4096, 17, 1) == 0
 
 
-def test_default_launch_shapes():
+def test_launch_shapes():
     """The built-in launch table (host code only): the vector kernel up to 2
-    tokens while its activations fit unsplit, the MFMA kernel beyond."""
+    tokens while its activations fit unsplit, the MFMA kernel beyond; a
+    partial configuration is completed, with K split further where it needs
+    it."""
     from ai_amd import _lib
     L = _lib.lib()
 
-    def shape(n, k, t):
+    def shape(n, k, t, cfg=None):
         c = _lib.Launch()
-        assert L.rv12_default_launch(n, k, t, ctypes.byref(c)) == _lib.RV12_OK
+        assert L.rv12_launch_shape(n, k, t, None if cfg is None else ctypes.byref(cfg), ctypes.byref(c)) == _lib.RV12_OK
         return (c.kernel, c.rb, c.waves, c.splits)
 
     assert shape(6144, 4096, 1) == (1, 1, 8, 1)           # Qwen3-8B qkv, one token
@@ -64,13 +66,20 @@ def test_default_launch_shapes():
     assert shape(151936, 4096, 1) == (1, 2, 4, 1)         # lm_head: two row blocks per workgroup
     assert shape(5120, 17408, 2)[0] == 2                  # Qwen3-14B down at 2 tokens: MFMA
     assert shape(7168, 5120, 2) == (1, 1, 8, 1)           # 14B qkv at 2 tokens: vector, unsplit
-    assert shape(5120, 17408, 16)[:3] == (2, 4, 8)        # MFMA, four row blocks per wave
-    assert shape(1024, 5120, 16)[:3] == (2, 1, 4)         # fewer than 128 row blocks
-    assert shape(5120, 5120, 8) == (2, 2, 8, 5)
+    # the MFMA kernel's time model picks the shapes the MI355X sweeps found best
+    assert shape(5120, 17408, 16)[:3] == (2, 4, 8)        # 14B down: four row blocks per wave
+    assert shape(1024, 5120, 16)[:3] == (2, 1, 4)         # 14B k/v: 64 row blocks
+    assert shape(5120, 5120, 8) == (2, 1, 8, 5)           # 14B o: one row block per wave, 200 workgroups
+    assert shape(5120, 8192, 16)[:3] == (2, 2, 8)         # 32B o: two (four would leave 90 workgroups)
+    assert shape(5120, 25600, 8)[:3] == (2, 2, 8)         # 32B down
+    # 4 waves of the MFMA kernel stage at most 16 steps: K = 5120 is split 10 ways
+    assert shape(5120, 5120, 16, _lib.Launch(2, 2, 4, 0)) == (2, 2, 4, 10)
+    assert shape(5120, 5120, 1, _lib.Launch(1, 1, 4, 3)) == (1, 1, 4, 3)
     c = _lib.Launch()
-    assert L.rv12_default_launch(64, 100, 1, ctypes.byref(c)) == _lib.RV12_E_SHAPE
-    assert L.rv12_default_launch(64, 256, 17, ctypes.byref(c)) == _lib.RV12_E_TOKENS
-    assert L.rv12_default_launch(64, 256, 1, None) == _lib.RV12_E_NULL
+    assert L.rv12_launch_shape(64, 100, 1, None, ctypes.byref(c)) == _lib.RV12_E_SHAPE
+    assert L.rv12_launch_shape(64, 256, 17, None, ctypes.byref(c)) == _lib.RV12_E_TOKENS
+    assert L.rv12_launch_shape(64, 256, 1, None, None) == _lib.RV12_E_NULL
+    assert L.rv12_launch_shape(64, 256, 1, ctypes.byref(_lib.Launch(3, 1, 4, 1)), ctypes.byref(c)) == _lib.RV12_E_CONFIG
 
 
 def _mat(n=64, k=256, tiles=0x1000, n_exc=0, rbase=0x1800):

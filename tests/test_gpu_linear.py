@@ -232,3 +232,19 @@ def test_two_tokens_with_k_beyond_the_vector_staging():
             _check(cnp, cg, 2, mode, True, 50 + mode, use_tc=True)
         del cg
         torch.cuda.empty_cache()
+
+
+def test_partial_launch_shape_sizes_its_workspace():
+    """BN and w given, S left to the library: with 2 waves the MFMA kernel
+    stages at most 8 steps of K, so K = 5120 is split at least 20 ways, more
+    than the built-in shape's split, and the workspace is sized for the split
+    the launch resolves to."""
+    from ai_amd import wcomp
+    N, K = 2048, 5120
+    bits = _random_matrix(N, K, 77, out_rows=0.01)
+    cnp = codec.compress(bits)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    shape = wcomp.launch_shape(N, K, 16, wcomp._launch(32, 2, None, 16))
+    assert shape[:3] == (2, 1, 2) and shape[3] >= 20 > wcomp.launch_shape(N, K, 16)[3]
+    for mode in (0, 2):
+        _check(cnp, cg, 16, mode, False, 60 + mode, BN=32, w=2, use_tc=True)
