@@ -290,6 +290,9 @@ int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint1
     rc = resolve_launch(w->n, w->k, t, cfg, &c);
     if (rc) return rc;
     const int splits = c.splits;
+    // the reduce pass addresses the partials with 32-bit byte offsets
+    if (splits > 1 && (int64_t)(splits + kReduceBatchMax) * t * nblocks(w->n) * 16 * 4 >= ((int64_t)1 << 31))
+        return RV12_E_CONFIG;
     const size_t need = ws_bytes_for(w->n, t, splits);
     if (need && (!ws || ws_bytes < need)) return RV12_E_WORKSPACE;
     if (need && !aligned16(ws)) return RV12_E_ALIGN;

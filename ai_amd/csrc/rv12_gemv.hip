@@ -312,22 +312,42 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     }
 }
 
-// second pass of a split linear: sum the partials of each output in split order
+// second pass of a split linear: sum the partials of each output in split
+// order.  Every split's partial (and sum of squares) is loaded before any is
+// added, kReduceBatch at a time through a descriptor over the partials (one
+// memory round trip for up to 16 splits, where a load-add loop paid one per
+// split); the sum runs in split order, as before.
+constexpr int kReduceBatch = kReduceBatchMax;
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, const float* __restrict__ ssq,
                                                        float* __restrict__ y, int N, int npad, int T, int S,
                                                        int mode, int rms, float eps, int K) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (int64_t)T * N) return;
     const int t = (int)(idx / N), n = (int)(idx % N);
-    float v = 0.0f;
-    for (int s = 0; s < S; ++s) v += part[((int64_t)s * T + t) * npad + n];
-    if (rms) {
-        float q = 0.0f;
-        for (int s = 0; s < S; ++s) q += ssq[s * T + t];
-        v *= 1.0f / sqrtf(q / (float)K + eps);
-    }
     float* o = y + (int64_t)t * N + n;
-    *o = mode == 0 ? v : *o + v;
+    const float old = mode == 0 ? 0.0f : *o;
+    // byte offsets in 32 bits: the host rejects (S + 16) T npad 4 >= 2^31
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, (uint32_t)((int64_t)S * T * npad * 4));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(ssq, rms ? (uint32_t)(S * T * 4) : 0u);
+    float v = 0.0f, q = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += kReduceBatch) {
+        float a[kReduceBatch], b[kReduceBatch];
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u) {
+            const int sp = s0 + u;  // past S: out of the descriptor's range, reads 0 (not added)
+            a[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, ((sp * T + t) * npad + n) * 4, 0, 0));
+            b[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, (sp * T + t) * 4, 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u) {
+            if (s0 + u < S) {
+                v += a[u];
+                q += b[u];
+            }
+        }
+    }
+    if (rms) v *= 1.0f / sqrtf(q / (float)K + eps);
+    *o = mode == 0 ? v : old + v;
 }
 
 // ------------------------------------------------------------------ launch

@@ -32,6 +32,7 @@ __host__ __device__ inline int scale_exp(int base) { return base > 0 ? base - 1 
 constexpr int kDepth = 8;          // weight steps in flight per wave
 constexpr int kMaxThreads = 1024;  // 16 waves
 constexpr int kMaxSplits = 64;
+constexpr int kReduceBatchMax = 16;  // splits the reduce pass loads at once
 constexpr int kMaxWaves = 16;
 constexpr size_t kMaxLds = 163840;  // LDS bytes of one gfx950 workgroup (160 KB)
 constexpr size_t kDefaultLds = 65536;  // above this a kernel needs hipFuncAttributeMaxDynamicSharedMemorySize
