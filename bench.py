@@ -244,6 +244,35 @@ def run_e2e_stream(dev, size="8b", streamed=4, prompt_len=512, new=32, seed=0):
     return out
 
 
+def run_attn(dev, reps=20, layers=36, positions=(100, 1000, 2100)):
+    """Decode-step attention of the Qwen3-8B shape alone (32 q / 8 kv heads,
+    head dim 128, 2304-position bf16 caches, one per layer, 340 MB in all, so
+    the caches stream from HBM as in the decode): k_rope_attn + k_attn_combine
+    for `layers` layers replayed from a HIP graph, us per layer at each
+    position (HIP events)."""
+    from ai_amd.attn import RopeAttn
+    H, KV, HD, maxt = 32, 8, 128, 2304
+    att = RopeAttn(H, KV, HD, maxt, torch.bfloat16, 1e-6, dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    qkv = torch.randn((H + 2 * KV) * HD, device=dev, generator=g)
+    qn, kn = torch.ones(HD, device=dev), torch.ones(HD, device=dev)
+    inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+    kcs = [torch.randn(KV, maxt, HD, device=dev, generator=g).bfloat16() for _ in range(layers)]
+    vcs = [torch.randn(KV, maxt, HD, device=dev, generator=g).bfloat16() for _ in range(layers)]
+    out = torch.zeros(H * HD, device=dev)
+    res = {}
+    for pos in positions:
+        p = torch.tensor([pos], device=dev)
+
+        def fn():
+            for l in range(layers):
+                att(qkv, qn, kn, inv, p, kcs[l], vcs[l], out)
+
+        res[pos] = round(time_graph(Graph(fn), reps) / layers * 1e3, 2)
+    return {"heads": H, "kv_heads": KV, "head_dim": HD, "maxt": maxt, "splits": att.a.splits,
+            "kv_bytes_per_layer_at_2100": 2 * KV * 2101 * HD * 2, "us_per_layer": res}
+
+
 def run_shape(name, reps, dev, min_bytes=1.2e9):
     """Qwen3-8B linear-shape sweep entry: one shape, distinct copies totalling > 1 GB
     replayed round-robin from a graph; ms per launch."""
@@ -369,6 +398,7 @@ def main():
     ap.add_argument("--no-32b", action="store_true", help="skip the Qwen3-32B end-to-end decode")
     ap.add_argument("--no-stream", action="store_true", help="skip the streamed-layers decode")
     ap.add_argument("--only-14b", action="store_true", help="run only the Qwen3-14B skinny-GEMM sweep (for profiling)")
+    ap.add_argument("--only-attn", action="store_true", help="run only the Qwen3-8B decode attention (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (scale factor of the HBM byte counters)")
     args = ap.parse_args()
@@ -390,6 +420,9 @@ def main():
         return
     if args.only_14b:
         print(json.dumps([r for name in SWEEP_14B for r in run_skinny(name, args.reps, dev)]), flush=True)
+        return
+    if args.only_attn:
+        print(json.dumps(run_attn(dev, args.reps)), flush=True)
         return
 
     tok = run_token_bench(args, dev)
