@@ -72,8 +72,9 @@ typedef struct rv12_matrix {
 } rv12_matrix;
 
 /* Launch shape of a linear.
- *   kernel  0 = built-in (vector for T <= 2, MFMA above), 1 = vector-FMA
- *           kernel (T <= 4), 2 = bf16-MFMA kernel (T <= 16)
+ *   kernel  0 = built-in (rv12_launch_shape: vector up to T = 2, MFMA
+ *           above), 1 = vector-FMA kernel (T <= 4), 2 = bf16-MFMA kernel
+ *           (T <= 16)
  *   rb      vector kernel: row blocks of 16 rows per workgroup (1, 2, 4);
  *           MFMA kernel: row blocks per wave (1, 2, 4)
  *   waves   waves per workgroup (1..16)
