@@ -32,7 +32,8 @@ bool shape_fits(int K, int T, const Shape& c) {
 // Built-in launch shapes, from launch-shape sweeps of the Qwen3-8B / 14B
 // linear shapes on MI355X.
 //   vector kernel: one row block per workgroup and 8 waves (16 for
-//     K >= 8192, 4 with two row blocks beyond 4096 row blocks); K is split
+//     K >= 8192, 4 with two row blocks beyond 4096 row blocks, 8 with two
+//     row blocks for 257-512 row blocks at one token); K is split
 //     only when there are fewer than 128 row blocks, so the grid still
 //     covers the 256 CUs;
 //   MFMA kernel: the shape with the least time in a model of its rounds of
@@ -41,12 +42,22 @@ bool shape_fits(int K, int T, const Shape& c) {
 // vector kernel's 8 FMAs per weight and token make it ALU-bound), and at 2
 // tokens where the vector kernel would have to split K to hold its activations
 // in registers (Qwen3-14B down: 35 vs 37.5 us).
-Shape vector_shape(int N, int K) {
+Shape vector_shape(int N, int K, int T) {
     const int64_t nblk = nblocks(N);
     Shape c;
     c.kernel = 1;
-    c.rb = nblk >= 4096 ? 2 : 1;
-    c.waves = nblk >= 4096 ? 4 : (K >= 8192 ? 16 : 8);
+    c.rb = 1;
+    c.waves = K >= 8192 ? 16 : 8;
+    if (nblk >= 4096) {
+        c.rb = 2;
+        c.waves = 4;
+    } else if (T == 1 && nblk > 256 && nblk <= 512) {
+        // 257-512 row blocks: two row blocks of 8 waves per workgroup
+        // (Qwen3-8B qkv 11.0 -> 10.4 us, 14B o 12.3 -> 11.6, 32B o
+        // 17.5 -> 15.6, 14B down 33.1 -> 27.7 with 3 splits)
+        c.rb = 2;
+        c.waves = 8;
+    }
     c.splits = 1;
     if (nblk < 128) c.splits = (int)std::min<int64_t>(4, (256 + nblk - 1) / nblk);
     return c;
@@ -122,13 +133,29 @@ Shape mfma_shape(int N, int K, int T) {
 Shape default_shape(int N, int K, int T) {
     const int nsteps = K / 32;
     bool vec = T <= kVectorDefaultTokens;
-    if (T == 2 && !gemv_prefetch_all(K, T, vector_shape(N, K).waves, 1)) vec = false;
-    Shape c = vec ? vector_shape(N, K) : mfma_shape(N, K, T);
+    if (T == 2 && !gemv_prefetch_all(K, T, vector_shape(N, K, T).waves, 1)) vec = false;
+    Shape c = vec ? vector_shape(N, K, T) : mfma_shape(N, K, T);
     while (c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
     while (c.splits < kMaxSplits && c.splits < nsteps && !shape_fits(K, T, c)) ++c.splits;
     // the vector kernel streams best with all activations loaded before the weights
+    const int s_fit = c.splits;
     while (c.kernel == 1 && c.splits < kMaxSplits && c.splits < nsteps && !gemv_prefetch_all(K, T, c.waves, c.splits))
         ++c.splits;
+    if (c.splits > s_fit) {
+        // once K is split anyway, up to two more splits may fill the last
+        // round of workgroups better (Qwen3-14B down at one token: 480
+        // workgroups in 27.7 us against 320 in 33.8)
+        const int s0 = c.splits;
+        double best = 0.0;
+        for (int s = s0; s <= std::min(s0 + 2, std::min(kMaxSplits, nsteps)); ++s) {
+            const int64_t wg = (nblocks(N) + c.rb - 1) / c.rb * s;
+            const double fill = (double)wg / (double)(kModelCUs * ((wg + kModelCUs - 1) / kModelCUs));
+            if (fill > best + 1e-9 && gemv_prefetch_all(K, T, c.waves, s)) {
+                best = fill;
+                c.splits = s;
+            }
+        }
+    }
     return c;
 }
 
@@ -136,7 +163,7 @@ int resolve_launch(int N, int K, int T, const rv12_launch* cfg, Shape* out) {
     Shape c = default_shape(N, K, T);
     if (cfg) {
         if (cfg->kernel && cfg->kernel != c.kernel)
-            c = cfg->kernel == 2 ? mfma_shape(N, K, T) : vector_shape(N, K);  // that kernel's own defaults first
+            c = cfg->kernel == 2 ? mfma_shape(N, K, T) : vector_shape(N, K, T);  // that kernel's own defaults first
         if (cfg->kernel) c.kernel = cfg->kernel;                            // an unknown kernel is rejected below
         if (cfg->rb) c.rb = cfg->rb;
         if (cfg->waves) c.waves = cfg->waves;

@@ -33,7 +33,7 @@ PEAK_HBM = 8000.0  # GB/s, MI355X HBM3E
 # layer matrices of a Qwen3-8B token, mean per launch) from the rocprofv3
 # FETCH_SIZE and WRITE_SIZE counters, each scaled by what it reads for a 1 GiB
 # device copy (--copy-calibration): profiles/k_gemv_qwen3-8b_token.md
-TRAFFIC_BYTES_PER_LAUNCH = 73317161
+TRAFFIC_BYTES_PER_LAUNCH = 73296386
 D, FF, L, V = 4096, 12288, 36, 151936
 QKV = (32 + 2 * 8) * 128
 LAYER = [("qkv", QKV, D, 0, True), ("o", D, 32 * 128, 1, False), ("gu", 2 * FF, D, 0, True),
@@ -138,7 +138,8 @@ def token_linears(layers, head, bufs, with_head=True):
 def run_token_bench(args, dev):
     """Two graphs over the same resident weights: the whole token (145
     launches: value, tok/s) and the 144 layer launches alone, which are all
-    the dominant kernel (vector-FMA linear, one row block per workgroup): the
+    the dominant kernel (vector-FMA linear, one token; two row blocks per
+    workgroup for qkv, one for the others): the
     roofline figure is its algorithmic bytes over its measured time."""
     layers, head = build_model(dev)
     g = torch.Generator(device=dev).manual_seed(1)
@@ -491,7 +492,7 @@ def main():
         "linear_only_tok_s": round(1e3 / ms, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved_alg, 2), "peak": PEAK_HBM, "unit": "GB/s",
                      "frac": round(achieved_alg / PEAK_HBM, 4), "traffic": TRAFFIC_BYTES_PER_LAUNCH,
-                     "kernel": "k_gemv<T=1, RB=1> (vector-FMA linear, 1 token, RMS / silu prologue variants): the 144 layer launches of one token",
+                     "kernel": "k_gemv<T=1> (vector-FMA linear, 1 token, RMS / silu prologue variants; RB=2 for qkv, RB=1 otherwise): the 144 layer launches of one token",
                      "avg_launch_us": round(us_launch, 3),
                      "alg_bytes_per_launch": round(tok["alg_bytes_layers"] / tok["launches_layers"])},
         "e2e_decode": e2e,

@@ -61,7 +61,11 @@ def test_launch_shapes():
         assert L.rv12_launch_shape(n, k, t, None if cfg is None else ctypes.byref(cfg), ctypes.byref(c)) == _lib.RV12_OK
         return (c.kernel, c.rb, c.waves, c.splits)
 
-    assert shape(6144, 4096, 1) == (1, 1, 8, 1)           # Qwen3-8B qkv, one token
+    assert shape(6144, 4096, 1) == (1, 2, 8, 1)           # Qwen3-8B qkv, one token: 384 row blocks, two per workgroup
+    assert shape(4096, 4096, 1) == (1, 1, 8, 1)           # o: 256 row blocks, one per workgroup
+    assert shape(5120, 8192, 1) == (1, 2, 8, 1)           # 32B o: 320 row blocks of K 8192, two per workgroup
+    assert shape(5120, 17408, 1) == (1, 2, 8, 3)          # 14B down: 3 splits fill the last round (480 workgroups)
+    assert shape(5120, 25600, 1) == (1, 2, 8, 3)          # 32B down
     assert shape(4096, 12288, 1) == (1, 1, 16, 1)         # down: 16 waves for K >= 8192
     assert shape(151936, 4096, 1) == (1, 2, 4, 1)         # lm_head: two row blocks per workgroup
     assert shape(5120, 17408, 2)[0] == 2                  # Qwen3-14B down at 2 tokens: MFMA
