@@ -182,6 +182,43 @@ def copy_calibration(dev, reps=20):
     print(json.dumps({"copy_bytes": 4 * n, "launches": reps}), flush=True)
 
 
+def measure_hbm(dev, reps=10):
+    """HBM rates torch's own kernels reach on this device, next to the
+    published 8 TB/s: a 2 GiB device-to-device copy (bytes read + written per
+    second), a read-only reduction of the same 2 GiB, and a plain bf16
+    matrix-vector product over a 2 GiB matrix (65536 x 16384, the library
+    GEMV of uncompressed weights; bytes read per second), HIP events over
+    `reps` launches after one warm launch."""
+    n = 1 << 29
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    acc = torch.empty((), dtype=torch.float32, device=dev)
+    a = torch.full((1 << 16, 1 << 14), 0.5, dtype=torch.bfloat16, device=dev)
+    xv = torch.ones(1 << 14, dtype=torch.bfloat16, device=dev)
+    yv = torch.empty(1 << 16, dtype=torch.bfloat16, device=dev)
+
+    def rate(fn, nbytes):
+        fn()
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(reps):
+            fn()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+    copy = rate(lambda: dst.copy_(src), 8 * n)
+    read = rate(lambda: torch.sum(src, 0, out=acc), 4 * n)
+    mv = rate(lambda: torch.mv(a, xv, out=yv), 2 * a.numel())
+    del src, dst, a
+    torch.cuda.empty_cache()
+    return {"copy_GBs": round(copy, 1), "sum_read_GBs": round(read, 1), "bf16_gemv_read_GBs": round(mv, 1),
+            "read_GBs": round(max(read, mv), 1),
+            "method": "torch copy_, sum and bf16 mv over 2 GiB; read_GBs = the faster read; HIP events, 10 launches"}
+
+
 def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefill="blocked"):
     """Greedy decode of a random-init Qwen3 (8b: a 2048-token random-id
     prompt, 256 new tokens; 32b: 4096 and
@@ -471,6 +508,9 @@ def main():
               f"{e2e32['prefill_ms']} ms for {e2e32['prompt']} tokens; 8-token passes "
               f"{e2e32['batch_pass']['tok_s']} tok/s", file=sys.stderr, flush=True)
 
+    hbm = measure_hbm(dev)
+    print(f"# measured HBM: copy {hbm['copy_GBs']:.0f} GB/s, sum {hbm['sum_read_GBs']:.0f} GB/s read, bf16 mv "
+          f"{hbm['bf16_gemv_read_GBs']:.0f} GB/s read", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": "Qwen3-8B bs1 decode tok/s; fused GEMV effective HBM GB/s vs peak",
@@ -494,7 +534,9 @@ def main():
                      "frac": round(achieved_alg / PEAK_HBM, 4), "traffic": TRAFFIC_BYTES_PER_LAUNCH,
                      "kernel": "k_gemv<T=1> (vector-FMA linear, 1 token, RMS / silu prologue variants; RB=2 for qkv, RB=1 otherwise): the 144 layer launches of one token",
                      "avg_launch_us": round(us_launch, 3),
-                     "alg_bytes_per_launch": round(tok["alg_bytes_layers"] / tok["launches_layers"])},
+                     "alg_bytes_per_launch": round(tok["alg_bytes_layers"] / tok["launches_layers"]),
+                     "frac_of_measured_read": round(achieved_alg / hbm["read_GBs"], 4)},
+        "hbm_measured": hbm,
         "e2e_decode": e2e,
         "e2e_decode_32b": e2e32,
         "e2e_decode_streamed": e2e_stream,

@@ -78,10 +78,16 @@ def test_position_outside_cache_gives_zeros():
     out = torch.full((H * HD,), 7.0, device=dev)
     inv = torch.ones(HD // 2, device=dev)
     ones = torch.ones(HD, device=dev)
-    att(torch.randn((H + 2 * KV) * HD, device=dev), ones, ones, inv, torch.tensor([maxt], device=dev), kc, vc, out)
+    qkv = torch.randn((H + 2 * KV) * HD, device=dev)
+    att(qkv, ones, ones, inv, torch.tensor([maxt], device=dev), kc, vc, out)
     torch.cuda.synchronize()
     assert torch.equal(out, torch.zeros_like(out))
     assert torch.equal(kc, kc0) and torch.equal(vc, vc0)
+    # the same workspace then serves a position inside the cache
+    att(qkv, ones, ones, inv, torch.tensor([maxt - 1], device=dev), kc, vc, out)
+    torch.cuda.synchronize()
+    ref, _, _ = _torch_ref(qkv, ones, ones, inv, maxt - 1, kc0, vc0, H, KV, HD, 1e-6, k_at_pos=kc[:, maxt - 1].clone())
+    assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), float((out - ref).abs().max())
 
 
 def test_single_split_and_split_limits():
