@@ -48,13 +48,19 @@ SWEEP = {"q_o": (4096, 4096, 0), "k_v": (1024, 4096, 0), "gate_up": (12288, 4096
          "gu": (24576, 4096, 0)}
 
 
-def make_matrix(N, K, gen, dev):
+def make_matrix(N, K, gen, dev, outliers="rows"):
+    """N(0, sigma) bf16 weights, sigma ~ U(0.01, 0.05), with 0.1 % of the
+    output rows (or of the input columns) x20."""
     sigma = float(torch.empty(1).uniform_(0.01, 0.05, generator=gen))
     seed = int(torch.randint(0, 2**31 - 1, (1,), generator=gen))
     w = torch.randn(N, K, device=dev, generator=torch.Generator(device=dev).manual_seed(seed))
     w.mul_(sigma)
-    rows = torch.randperm(N, generator=gen)[: max(1, N // 1000)].to(dev)
-    w[rows] *= 20
+    if outliers == "rows":
+        rows = torch.randperm(N, generator=gen)[: max(1, N // 1000)].to(dev)
+        w[rows] *= 20
+    else:
+        cols = torch.randperm(K, generator=gen)[: max(1, K // 1000)].to(dev)
+        w[:, cols] *= 20
     return w.bfloat16()
 
 
@@ -311,15 +317,16 @@ def run_attn(dev, reps=20, layers=36, positions=(100, 1000, 2100)):
             "kv_bytes_per_layer_at_2100": 2 * KV * 2101 * HD * 2, "us_per_layer": res}
 
 
-def run_shape(name, reps, dev, min_bytes=1.2e9):
+def run_shape(name, reps, dev, min_bytes=1.2e9, outliers="rows"):
     """Qwen3-8B linear-shape sweep entry: one shape, distinct copies totalling > 1 GB
-    replayed round-robin from a graph; ms per launch."""
+    replayed round-robin from a graph; ms per launch.  outliers: the x20
+    outliers on 0.1 % of the output rows or of the input columns."""
     from ai_amd import wcomp
     N, K, mode = SWEEP[name]
     gen = torch.Generator().manual_seed(100 + sorted(SWEEP).index(name))
     per = 1.5 * N * K
     ncopy = max(1, int(np.ceil(min_bytes / per)))
-    cs = [wcomp.compact(wcomp.compress(make_matrix(N, K, gen, dev))) for _ in range(ncopy)]
+    cs = [wcomp.compact(wcomp.compress(make_matrix(N, K, gen, dev, outliers))) for _ in range(ncopy)]
     g = torch.Generator(device=dev).manual_seed(2)
     x = torch.randn(K * (2 if mode == 2 else 1), device=dev, generator=g).bfloat16().float()
     y = torch.zeros(N, device=dev)
@@ -332,10 +339,11 @@ def run_shape(name, reps, dev, min_bytes=1.2e9):
     ms = time_graph(graph, reps) / ncopy
     cb = sum(comp_bytes(c) for c in cs) / ncopy
     ab = sum(alg_bytes(c, mode, False) for c in cs) / ncopy
+    exc = sum(int(c["er"].numel()) for c in cs) / ncopy / (N * K)
     del cs, graph
     torch.cuda.empty_cache()
     return {"shape": name, "N": N, "K": K, "copies": ncopy, "us": ms * 1e3, "comp_GBs": cb / ms / 1e6,
-            "alg_GBs": ab / ms / 1e6, "frac_peak": cb / ms / 1e6 / PEAK_HBM}
+            "alg_GBs": ab / ms / 1e6, "frac_peak": cb / ms / 1e6 / PEAK_HBM, "exception_frac": exc}
 
 
 def run_skinny(name, reps, dev, min_bytes=1.2e9):
@@ -473,13 +481,18 @@ def main():
     del tok["layers"], tok["head"]
     torch.cuda.empty_cache()
 
-    sweep = []
+    sweep, sweep_cols = [], []
     if not args.no_sweep:
         for name in ("q_o", "k_v", "gate_up", "down", "lm_head", "qkv", "gu"):
             r = run_shape(name, args.reps, dev)
             print(f"# {name}: {r['us']:.1f} us/launch, {r['comp_GBs']:.0f} GB/s ({r['frac_peak']:.1%})",
                   file=sys.stderr, flush=True)
-            sweep.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
+            sweep.append({k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()})
+        for name in ("q_o", "k_v", "gate_up", "down", "lm_head", "qkv", "gu"):
+            r = run_shape(name, args.reps, dev, outliers="columns")
+            print(f"# {name} (outlier input columns): {r['us']:.1f} us/launch, {r['comp_GBs']:.0f} GB/s "
+                  f"({r['frac_peak']:.1%})", file=sys.stderr, flush=True)
+            sweep_cols.append({k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()})
 
     sweep14 = []
     if not args.no_14b:
@@ -542,6 +555,7 @@ def main():
         "e2e_decode_streamed": e2e_stream,
         "cpu_baseline": cpu,
         "sweep_m1": sweep,
+        "sweep_m1_input_column_outliers": sweep_cols,
         "sweep_14b": sweep14,
     }
     print(json.dumps(line), flush=True)
