@@ -241,13 +241,13 @@ def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefil
     load_s = time.time() - t0
     prompt = [int(t) for t in np.random.default_rng(seed).integers(0, ck.V, prompt_len)]
     eng.generate(prompt[:64], 8)  # capture + warm
-    if prefill == "blocked":
+    if prefill == "blocked" and prompt_len >= eng.prefill_min:
         eng.generate(prompt[:eng.prefill_min + 8], 2)  # the blocked prefill's GEMM shapes
     ids, prefill_ms, decode_ms = eng.generate(prompt, new, timing=True)
     per_tok = decode_ms / (new - 1)
     out = {"model": f"qwen3-{size} random init", "prompt": prompt_len, "new_tokens": new, "kv_cache": "bf16",
            "tok_s": round(1e3 / per_tok, 2), "ms_per_token": round(per_tok, 4), "prefill_ms": round(prefill_ms, 1),
-           "prefill": prefill,
+           "prefill": prefill if prefill != "blocked" or prompt_len >= eng.prefill_min else "legacy (below the blocked minimum)",
            "load_s": round(load_s, 1), "first_ids": ids[:8]}
     if batch:
         ms = eng.batch_pass_ms(batch, prompt_len)
@@ -508,6 +508,14 @@ def main():
         print(f"# qwen3-8b decode: {e2e['tok_s']} tok/s ({e2e['ms_per_token']} ms/token), prefill "
               f"{e2e['prefill_ms']} ms for {e2e['prompt']} tokens", file=sys.stderr, flush=True)
 
+    e2e06 = None
+    if not args.no_e2e:
+        e2e06 = run_e2e(dev, "0.6b", prompt_len=128, new=64)
+        e2e06["reference_published"] = {"tok_s": 290, "hardware": "RTX 5060 Laptop 8 GB (other hardware)",
+                                        "source": "ramvi/docs/architecture/COMPATIBILITY.md:72"}
+        print(f"# qwen3-0.6b decode: {e2e06['tok_s']} tok/s ({e2e06['ms_per_token']} ms/token), prefill "
+              f"{e2e06['prefill_ms']} ms for {e2e06['prompt']} tokens", file=sys.stderr, flush=True)
+
     e2e_stream = None
     if not args.no_e2e and not args.no_stream:
         e2e_stream = run_e2e_stream(dev)
@@ -551,6 +559,7 @@ def main():
                      "frac_of_measured_read": round(achieved_alg / hbm["read_GBs"], 4)},
         "hbm_measured": hbm,
         "e2e_decode": e2e,
+        "e2e_decode_0_6b": e2e06,
         "e2e_decode_32b": e2e32,
         "e2e_decode_streamed": e2e_stream,
         "cpu_baseline": cpu,
