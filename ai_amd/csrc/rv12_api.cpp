@@ -33,9 +33,10 @@ bool shape_fits(int K, int T, const Shape& c) {
 // linear shapes on MI355X.
 //   vector kernel: one row block per workgroup and 8 waves (16 for
 //     K >= 8192, 4 with two row blocks beyond 4096 row blocks, 8 with two
-//     row blocks for 257-512 row blocks at one token); K is split
-//     only when there are fewer than 128 row blocks, so the grid still
-//     covers the 256 CUs;
+//     row blocks for 257-512 row blocks at one token, and there at most
+//     one wave per 8 K steps); K is split at 2 tokens when there are fewer than 128
+//     row blocks, so the grid still covers the 256 CUs, and wherever the
+//     activations would not fit in registers;
 //   MFMA kernel: the shape with the least time in a model of its rounds of
 //     workgroups (mfma_model_us);
 // The MFMA kernel is the built-in choice from 3 tokens on (at 3-4 tokens the
@@ -59,7 +60,10 @@ Shape vector_shape(int N, int K, int T) {
         c.waves = 8;
     }
     c.splits = 1;
-    if (nblk < 128) c.splits = (int)std::min<int64_t>(4, (256 + nblk - 1) / nblk);
+    // below 128 row blocks a K split fills more CUs but costs a reduce
+    // launch: at one token the unsplit launch is faster (Qwen3-8B k/v
+    // 1024x4096 6.0 vs 7.2 us with 4 splits, 0.6B o 1024x2048 4.6 vs 6.7)
+    if (nblk < 128 && T > 1) c.splits = (int)std::min<int64_t>(4, (256 + nblk - 1) / nblk);
     return c;
 }
 
@@ -136,6 +140,9 @@ Shape default_shape(int N, int K, int T) {
     if (T == 2 && !gemv_prefetch_all(K, T, vector_shape(N, K, T).waves, 1)) vec = false;
     Shape c = vec ? vector_shape(N, K, T) : mfma_shape(N, K, T);
     while (c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
+    // at one token the vector kernel's waves want at least 8 K steps each
+    // (Qwen3-0.6B qkv 4096x1024: 4.6 us at 4 waves, 5.1 at 8)
+    while (c.kernel == 1 && T == 1 && c.waves > 2 && split_steps(K, c.splits) < 8 * c.waves) c.waves >>= 1;
     while (c.splits < kMaxSplits && c.splits < nsteps && !shape_fits(K, T, c)) ++c.splits;
     // the vector kernel streams best with all activations loaded before the weights
     const int s_fit = c.splits;
