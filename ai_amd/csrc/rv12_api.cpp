@@ -33,8 +33,9 @@ bool shape_fits(int K, int T, const Shape& c) {
 // linear shapes on MI355X.
 //   vector kernel: one row block per workgroup and 8 waves (16 for
 //     K >= 8192, 4 with two row blocks beyond 4096 row blocks, 8 with two
-//     row blocks for 257-512 row blocks at one token, and there at most
-//     one wave per 8 K steps); K is split at 2 tokens when there are fewer than 128
+//     row blocks for 257-512 row blocks at one token, 4 above that for
+//     K <= 6144, and there at most one wave per 8 K steps); K is split at 2
+//     tokens when there are fewer than 128
 //     row blocks, so the grid still covers the 256 CUs, and wherever the
 //     activations would not fit in registers;
 //   MFMA kernel: the shape with the least time in a model of its rounds of
@@ -58,6 +59,11 @@ Shape vector_shape(int N, int K, int T) {
         // 17.5 -> 15.6, 14B down 33.1 -> 27.7 with 3 splits)
         c.rb = 2;
         c.waves = 8;
+    } else if (T == 1 && nblk > 512 && K <= 6144) {
+        // more row blocks: 4 waves, twice the workgroups resident per CU, so
+        // one's prologue overlaps another's stream (with the RMS prologue
+        // Qwen3-32B gu 51200x5120 67.6 -> 63.5 us, 8B gu 28.0 -> 26.7)
+        c.waves = 4;
     }
     c.splits = 1;
     // below 128 row blocks a K split fills more CUs but costs a reduce
