@@ -32,12 +32,12 @@ bool shape_fits(int K, int T, const Shape& c) {
 // Built-in launch shapes, from launch-shape sweeps of the Qwen3-8B / 14B
 // linear shapes on MI355X.
 //   vector kernel: one row block per workgroup and 8 waves (16 for
-//     K >= 8192, 4 with two row blocks beyond 4096 row blocks, 8 with two
-//     row blocks for 257-512 row blocks at one token, 4 above that for
-//     K <= 6144, and there at most one wave per 8 K steps); K is split at 2
-//     tokens when there are fewer than 128
-//     row blocks, so the grid still covers the 256 CUs, and wherever the
-//     activations would not fit in registers;
+//     K >= 8192); two row blocks and 4 waves beyond 4096 row blocks; two
+//     row blocks and 8 waves for 257-512 row blocks (at 2 tokens only for
+//     K <= 6144); at one token 4 waves above 512 row blocks for K <= 6144
+//     and at most one wave per 8 K steps.  K is split at 2 tokens when
+//     there are fewer than 128 row blocks, so the grid still covers the 256
+//     CUs, and wherever the activations would not fit in registers;
 //   MFMA kernel: the shape with the least time in a model of its rounds of
 //     workgroups (mfma_model_us);
 // The MFMA kernel is the built-in choice from 3 tokens on (at 3-4 tokens the
@@ -53,10 +53,11 @@ Shape vector_shape(int N, int K, int T) {
     if (nblk >= 4096) {
         c.rb = 2;
         c.waves = 4;
-    } else if (T == 1 && nblk > 256 && nblk <= 512) {
+    } else if ((T == 1 || K <= 6144) && nblk > 256 && nblk <= 512) {
         // 257-512 row blocks: two row blocks of 8 waves per workgroup
         // (Qwen3-8B qkv 11.0 -> 10.4 us, 14B o 12.3 -> 11.6, 32B o
-        // 17.5 -> 15.6, 14B down 33.1 -> 27.7 with 3 splits)
+        // 17.5 -> 15.6, 14B down 33.1 -> 27.7 with 3 splits; at 2 tokens
+        // 14B o 12.9 -> 11.1, 8B qkv 11.2 -> 10.1)
         c.rb = 2;
         c.waves = 8;
     } else if (T == 1 && nblk > 512 && K <= 6144) {

@@ -72,7 +72,8 @@ def test_launch_shapes():
     assert shape(4096, 12288, 1) == (1, 1, 16, 1)         # down: 16 waves for K >= 8192
     assert shape(151936, 4096, 1) == (1, 2, 4, 1)         # lm_head: two row blocks per workgroup
     assert shape(5120, 17408, 2)[0] == 2                  # Qwen3-14B down at 2 tokens: MFMA
-    assert shape(7168, 5120, 2) == (1, 1, 8, 1)           # 14B qkv at 2 tokens: vector, unsplit
+    assert shape(7168, 5120, 2) == (1, 2, 8, 1)           # 14B qkv at 2 tokens: vector, unsplit, 2 row blocks
+    assert shape(5120, 8192, 2) == (1, 1, 16, 1)          # 32B o at 2 tokens: K > 6144 keeps one row block
     # the MFMA kernel's time model picks the shapes the MI355X sweeps found best
     assert shape(5120, 17408, 16)[:3] == (2, 4, 8)        # 14B down: four row blocks per wave
     assert shape(1024, 5120, 16)[:3] == (2, 1, 4)         # 14B k/v: 64 row blocks
