@@ -9,18 +9,18 @@ import torch
 from ._lib import Attn, check, lib
 
 
-SPAN = 64  # positions one workgroup covers at most
+SPAN = 80  # positions one workgroup covers at most
 MAX_SPLITS = 128
 
 
 def default_splits(n_kv, maxt):
-    """Position splits: each workgroup covers at most 64 positions, and there
+    """Position splits: each workgroup covers at most 80 positions, and there
     are at least 256 workgroups while each keeps >= 16 positions."""
     need = -(-maxt // SPAN)
     want = min(-(-256 // n_kv), -(-maxt // 16))
     s = max(1, need, want)
     if s > MAX_SPLITS:
-        raise ValueError("the attention kernel covers at most 8192 positions")
+        raise ValueError("the attention kernel covers at most 10240 positions")
     return int(s)
 
 

@@ -2,8 +2,8 @@
 // the 12-bit linears in a decode step (replaces rope_attn_k,
 // ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213).
 //
-// Grid (KV heads, splits), 256 threads.  Workgroup (g, sp) covers the
-// positions [lo, hi) of 0..pos, at most 64 of them:
+// Grid (KV heads, splits), 320 threads.  Workgroup (g, sp) covers the
+// positions [lo, hi) of 0..pos, at most 80 of them:
 //   0. first the step's own q/k/v values, then every cache value the
 //      workgroup reads are loaded: a quarter key row (HD/4 dims) per thread,
 //      4 threads per position, and the values of 16 (8) positions at a dim
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
         }
         return;
     }
-    const int n = (int)pos + 1;  // n <= 8192 and S <= 128: 32-bit products
+    const int n = (int)pos + 1;  // n <= 10240 and S <= 128: 32-bit products
     const int lo = (int)((uint32_t)(sp * n) / (uint32_t)S), hi = (int)((uint32_t)((sp + 1) * n) / (uint32_t)S);
     const int span = hi - lo;  // <= P (host)
     const int64_t row0 = (int64_t)g * p.maxt * HD;

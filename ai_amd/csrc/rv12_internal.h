@@ -92,12 +92,13 @@ struct AttnParams {
     int n_heads, n_kv, head_dim, maxt, kv_bf16;
     float eps, scale;
 };
-constexpr int kAttnThreads = 256;
-constexpr int kAttnSpan = 64;         // positions one attention workgroup covers at most
-constexpr int kAttnMaxSplits = 128;   // so the context is at most 8192 positions
+constexpr int kAttnThreads = 320;     // 4 per position of the span
+constexpr int kAttnSpan = 80;         // positions one attention workgroup covers at most
+constexpr int kAttnMaxSplits = 128;   // so the context is at most 10240 positions
 inline size_t attn_lds_bytes(int hd, int g) {
     const size_t pg = kAttnThreads / (hd / 2);  // position groups of the value sums
-    return 4 * ((size_t)g * hd + 2 * (size_t)hd + (size_t)kAttnSpan * g + 8 * (size_t)g + 2 * (size_t)g +
+    return 4 * ((size_t)g * hd + 2 * (size_t)hd + (size_t)kAttnSpan * g + 2 * (kAttnThreads / 64) * (size_t)g +
+                2 * (size_t)g +
                 pg * g * hd);
 }
 inline size_t attn_part_floats(int n_kv, int g, int hd, int splits) {

@@ -178,8 +178,8 @@ int rv12_decode_rows(const rv12_matrix* w, int first, int last, void* out, int o
  * attention of each head over positions 0..*pos (softmax(q.K * scale) V).
  * *pos is read on the device, so a captured graph can advance it; a *pos
  * outside [0, maxt) gives zeros and touches no cache.  The positions are spread
- * over `splits` workgroups per kv head, each covering at most 64 of them (so
- * splits >= maxt / 64, at most 128: maxt <= 8192); splits > 1 adds a combine
+ * over `splits` workgroups per kv head, each covering at most 80 of them (so
+ * splits >= maxt / 80, at most 128: maxt <= 10240); splits > 1 adds a combine
  * pass over partials in the workspace (rv12_attn_workspace_bytes).  Calls
  * sharing a workspace must be ordered on one stream.  Replaces rope_attn_k,
  * ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213. */

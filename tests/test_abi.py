@@ -198,8 +198,8 @@ def test_attention_argument_errors():
     assert call(A(maxt=0)) == _lib.RV12_E_SHAPE
     assert call(A(splits=0)) == _lib.RV12_E_CONFIG
     assert call(A(splits=129, maxt=8192)) == _lib.RV12_E_CONFIG
-    assert call(A(splits=35)) == _lib.RV12_E_CONFIG          # 66 positions per split
-    assert call(A(maxt=8193, splits=128)) == _lib.RV12_E_CONFIG
+    assert call(A(splits=28)) == _lib.RV12_E_CONFIG          # 83 positions per split
+    assert call(A(maxt=10241, splits=128)) == _lib.RV12_E_CONFIG  # 81 positions per split
     assert call(A(), out=None) == _lib.RV12_E_NULL
     assert call(A(), pos=None) == _lib.RV12_E_NULL
     assert call(A(), ws=0) == _lib.RV12_E_WORKSPACE

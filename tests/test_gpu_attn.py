@@ -112,18 +112,18 @@ def test_single_split_and_split_limits():
     torch.cuda.synchronize()
     assert torch.allclose(outs[0], outs[1], rtol=1e-5, atol=1e-6)
     assert torch.allclose(outs[0], outs[2], rtol=1e-5, atol=1e-6)
-    for mt, splits in ((300, 2), (9000, 128), (300, 129)):
+    for mt, splits in ((300, 2), (10241, 128), (300, 129)):
         with pytest.raises(ValueError):
             RopeAttn(H, KV, HD, mt, torch.float32, 1e-6, dev, splits=splits)(
                 qkv, ones, ones, inv, torch.tensor([0], device=dev), kc, vc, torch.zeros(H * HD, device=dev))
 
 
 def test_long_cache_many_splits():
-    """8192 positions over 128 splits, bf16 cache, against the float64
+    """10240 positions over 128 splits, bf16 cache, against the float64
     reference at a few positions."""
     from ai_amd.attn import RopeAttn
     dev = "cuda"
-    H, KV, HD, maxt = 32, 8, 128, 8192
+    H, KV, HD, maxt = 32, 8, 128, 10240
     g = torch.Generator(device=dev).manual_seed(11)
     inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
     qn = 1 + 0.1 * torch.randn(HD, device=dev, generator=g)
