@@ -198,6 +198,35 @@ def test_lm_head_full_size():
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("N,K,shape1,shape2", [
+    (1000, 2048, (1, 1, 8, 1), (1, 1, 8, 4)),    # 63 row blocks: unsplit at one token, split at two
+    (4100, 1024, (1, 2, 4, 1), (1, 2, 8, 1)),    # 257 row blocks of 32 K steps: two per workgroup
+    (6000, 4096, (1, 2, 8, 1), (1, 2, 8, 1)),    # 375 row blocks
+    (8300, 1024, (1, 1, 4, 1), (1, 1, 8, 1)),    # 519 row blocks, ragged: 4 waves at one token
+    (5000, 17408, (1, 2, 8, 3), None),           # 313 row blocks of a long K: 3 splits fill the round
+])
+def test_default_launch_shape_families(N, K, shape1, shape2):
+    """The built-in launch shape of each row-block range (asserted), every
+    mode, with and without the RMS prologue, at one and two tokens, against
+    the C oracle."""
+    from ai_amd import wcomp
+    print("shape", N, K, flush=True)
+    assert wcomp.launch_shape(N, K, 1) == shape1
+    if shape2 is not None:
+        assert wcomp.launch_shape(N, K, 2) == shape2
+    bits = _random_matrix(N, K, N + 5 * K, out_rows=0.001, out_cols=0.001)
+    cnp = cref.compress(bits)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    for T, mode, rms in ((1, 0, True), (1, 1, False), (1, 2, False), (2, 0, True), (2, 1, False), (2, 2, False)):
+        X, Y0, lnw = _inputs(cnp, T, mode, 11 + T + mode, rms)
+        ref = Y0.copy()
+        cref.gemv_12bit(cnp, X, ref, mode, lnw=lnw)
+        y = _run(cg, X, Y0, mode, T, lnw=lnw, use_tc=T > 1)
+        err = np.abs(y.astype(np.float64) - ref)
+        assert np.all(err <= ATOL + RTOL * np.abs(ref)), (N, K, T, mode, rms, float(err.max()))
+        assert float((err / (np.abs(ref) + 1.0)).max()) < 1e-4, (N, K, T, mode, float(err.max()))
+
+
 def test_tuned_launch_shapes_keep_parity(tmp_path):
     """tune() fills CFG1 / CFGT on the GPU; the linears then run with those
     launch shapes and still match the closed form."""
