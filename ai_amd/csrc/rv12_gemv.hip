@@ -10,7 +10,7 @@
 //      and the RMSNorm weight) for the split's K range, as straight-line code
 //      (the prologue variants are template arguments); a bare barrier puts
 //      every wave's activation loads ahead of the weight loads;
-//   2. each wave issues the loads of its first kDepth weight steps (buffer
+//   2. each wave issues the loads of its first D weight steps (buffer
 //      loads; a step past the split's end goes through a 0-byte descriptor,
 //      which returns zeros without a memory access);
 //   3. the activation loads are waited for (the weight loads stay in flight)
@@ -18,7 +18,7 @@
 //      squares for RMS; one barrier;
 //   4. main loop: per step each wave decodes 8 weights per lane and row block
 //      and does 8 FMAs per token into fp32 accumulators, and issues the load
-//      kDepth steps ahead;
+//      D steps ahead (D: the prefetch depth chosen per variant below);
 //   5. epilogue: one thread per output sums the lane quarters and waves in a
 //      fixed order (no atomics), rescales by 2^sc of its row, adds the
 //      products ev * x' of its row's exceptions whose column lies in the split
@@ -54,8 +54,12 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     constexpr int NXM = gemv_chunks(T);
     constexpr int NO = RB * 16 * T;  // outputs of the workgroup
     // weight steps in flight per wave: deeper prefetch delays the activation
-    // loads, which the memory system serves behind the weight stream
-    constexpr int D = kDepth;
+    // loads, which the memory system serves behind the weight stream.  At one
+    // token 6 steps beat 8, and 4 with the 2K silu(g)*u activations (Qwen3-8B
+    // qkv 11.02 -> 10.67 us, o 7.64 -> 7.46, down 16.59 -> 15.9; 32B down
+    // 38.8 -> 37.45); the one-row-block RMS variant (gu: many rounds of
+    // workgroups per CU) keeps 8 (8B gu 28.3 at 8, 28.9 at 6)
+    constexpr int D = T != 1 ? kDepth : (M2 ? 4 : (LN && RB == 1 ? kDepth : 6));
     extern __shared__ float smem[];
     const int W = blockDim.x >> 6;
     const int nthr = blockDim.x;
