@@ -58,8 +58,9 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     // token 6 steps beat 8, and 4 with the 2K silu(g)*u activations (Qwen3-8B
     // qkv 11.02 -> 10.67 us, o 7.64 -> 7.46, down 16.59 -> 15.9; 32B down
     // 38.8 -> 37.45); the one-row-block RMS variant (gu: many rounds of
-    // workgroups per CU) keeps 8 (8B gu 28.3 at 8, 28.9 at 6)
-    constexpr int D = T != 1 ? kDepth : (M2 ? 4 : (LN && RB == 1 ? kDepth : 6));
+    // workgroups per CU) keeps 8 (8B gu 28.3 at 8, 28.9 at 6).  At two tokens
+    // 6 beat 8 on every shape (14B o 12.28 -> 11.93, gate/up 28.7 -> 28.1)
+    constexpr int D = T > 2 ? kDepth : (T == 2 ? 6 : (M2 ? 4 : (LN && RB == 1 ? kDepth : 6)));
     extern __shared__ float smem[];
     const int W = blockDim.x >> 6;
     const int nthr = blockDim.x;
