@@ -318,14 +318,15 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
 }
 
 // second pass of a split linear: sum the partials of each output in split
-// order.  Every split's partial (and sum of squares) is loaded before any is
-// added, kReduceBatch at a time through a descriptor over the partials (one
-// memory round trip for up to 16 splits, where a load-add loop paid one per
-// split); the sum runs in split order, as before.
-constexpr int kReduceBatch = kReduceBatchMax;
+// order.  Every split's partial (and, with RMS, sum of squares) is loaded
+// before any is added, CB at a time through a descriptor over the partials
+// (one memory round trip for up to CB splits, where a load-add loop paid one
+// per split); the sum runs in split order.  CB = 8 where the splits fit,
+// else 16 (kReduceBatchMax).
+template <int CB, bool RMS>
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, const float* __restrict__ ssq,
                                                        float* __restrict__ y, int N, int npad, int T, int S,
-                                                       int mode, int rms, float eps, int K) {
+                                                       int mode, float eps, int K) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (int64_t)T * N) return;
     const int t = (int)(idx / N), n = (int)(idx % N);
@@ -333,25 +334,25 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
     const float old = mode == 0 ? 0.0f : *o;
     // byte offsets in 32 bits: the host rejects (S + 16) T npad 4 >= 2^31
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, (uint32_t)((int64_t)S * T * npad * 4));
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(ssq, rms ? (uint32_t)(S * T * 4) : 0u);
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(ssq, RMS ? (uint32_t)(S * T * 4) : 0u);
     float v = 0.0f, q = 0.0f;
-    for (int s0 = 0; s0 < S; s0 += kReduceBatch) {
-        float a[kReduceBatch], b[kReduceBatch];
+    for (int s0 = 0; s0 < S; s0 += CB) {
+        float a[CB], b[CB];
 #pragma unroll
-        for (int u = 0; u < kReduceBatch; ++u) {
+        for (int u = 0; u < CB; ++u) {
             const int sp = s0 + u;  // past S: out of the descriptor's range, reads 0 (not added)
             a[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, ((sp * T + t) * npad + n) * 4, 0, 0));
-            b[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, (sp * T + t) * 4, 0, 0));
+            b[u] = RMS ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, (sp * T + t) * 4, 0, 0)) : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < kReduceBatch; ++u) {
+        for (int u = 0; u < CB; ++u) {
             if (s0 + u < S) {
                 v += a[u];
                 q += b[u];
             }
         }
     }
-    if (rms) v *= 1.0f / sqrtf(q / (float)K + eps);
+    if (RMS) v *= 1.0f / sqrtf(q / (float)K + eps);
     *o = mode == 0 ? v : old + v;
 }
 
@@ -384,10 +385,22 @@ static int launch_rb(const LinearParams& p, int T, dim3 grid, int threads, size_
     return -1;
 }
 
-void launch_splitk_reduce(const LinearParams& p, int T, int splits, hipStream_t st) {
+template <int CB, bool RMS>
+static void launch_reduce_t(const LinearParams& p, int T, int splits, hipStream_t st) {
     const int64_t tot = (int64_t)T * p.N;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, p.part, p.ssq, p.y,
-                       p.N, p.npad, T, splits, p.mode, p.lnw != nullptr, p.eps, p.K);
+    hipLaunchKernelGGL((k_splitk_reduce<CB, RMS>), dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, p.part,
+                       p.ssq, p.y, p.N, p.npad, T, splits, p.mode, p.eps, p.K);
+}
+
+void launch_splitk_reduce(const LinearParams& p, int T, int splits, hipStream_t st) {
+    const bool rms = p.lnw != nullptr;
+    if (splits <= 8) {
+        if (rms) launch_reduce_t<8, true>(p, T, splits, st);
+        else launch_reduce_t<8, false>(p, T, splits, st);
+    } else {
+        if (rms) launch_reduce_t<kReduceBatchMax, true>(p, T, splits, st);
+        else launch_reduce_t<kReduceBatchMax, false>(p, T, splits, st);
+    }
 }
 
 int launch_gemv(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st) {
