@@ -313,9 +313,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
 // one split per thread, and the thread's value of every split, CB at a time)
 // is issued before anything waits, so the combine costs one memory round trip.
 // Descriptors over the head's partials read zeros past the last split.
-// CB values per thread at a time: 32 when the splits fit (8B decode at 2k
-// context: 11.49 -> 11.20 us per layer against 64, half of whose loads read
-// past the last split), else 64.
+// CB values per thread at a time: the smallest of 16, 32, 64 that holds the
+// splits (8B decode at 2k context, 32 splits: 11.49 -> 11.20 us per layer
+// with 32 against 64, half of whose loads read past the last split; 0.6B at
+// 12 splits: 7.42 -> 7.24 us with 16 against 32).
 template <int CB>
 __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out, int S,
                                                       int G, int HD) {
@@ -403,7 +404,10 @@ int launch_attn(const AttnParams& p, int S, hipStream_t st) {
     int rc = p.head_dim == 128 ? launch_attn_hd<128>(p, G, S, lds, st)
                                : (p.head_dim == 64 ? launch_attn_hd<64>(p, G, S, lds, st) : -1);
     if (rc) return rc;
-    if (S > 1 && S <= 32)
+    if (S > 1 && S <= 16)
+        hipLaunchKernelGGL(k_attn_combine<16>, dim3(p.n_heads), dim3(p.head_dim), 0, st, p.part, p.out, S, G,
+                           p.head_dim);
+    else if (S > 16 && S <= 32)
         hipLaunchKernelGGL(k_attn_combine<32>, dim3(p.n_heads), dim3(p.head_dim), 0, st, p.part, p.out, S, G,
                            p.head_dim);
     else if (S > 32)
