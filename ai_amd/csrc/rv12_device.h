@@ -58,6 +58,55 @@ __device__ __forceinline__ uint32_t h_to_bf16(uint32_t h, int sc) {
     return c ? ((h + ((uint32_t)sc << 7)) & 0xFFFFu) : h;
 }
 
+// Activation scaling.  The h values sit at the bottom of the float32 range
+// (2^-126 <= |h| < 2^-111 for in-window weights), so the kernels multiply them
+// by x' * 2^P, an exact power-of-two scaling folded back into the row's final
+// 2^(sc - P):
+//   fast path  P = 64, taken when every nonzero |x'| of the workgroup (of the
+//              wave in the MFMA kernel) lies in [2^-64, 2^63): every product
+//              with an in-window weight is a normal float below 2^16 and the
+//              bf16 parts of x' * 2^64 stay finite;
+//   slow path  otherwise: P = 100 - e, with e the float exponent (frexp) of the
+//              largest finite nonzero |x'| of the token, so max |x'| * 2^P is
+//              in [2^99, 2^100); values below max |x'| * 2^-225 are lost.
+// The exception products ev * x' use x' itself (x' * 2^P * 2^-P is exact).
+constexpr int kXScaleExp = 64;
+constexpr int kXSlowExp = 100;
+constexpr int kXRangeLo = -63;  // frexp exponent of 2^-64
+constexpr int kXRangeHi = 63;   // frexp exponent of the largest value below 2^63
+constexpr float kXScale = 0x1p64f;
+// The RMSNorm sum of squares runs over (x * 2^-32)^2 (exact scaling, the same
+// sums where no square under- or overflows), so it stays finite up to
+// |x| ~ 2^90; rs = 2^-32 / sqrt(S / K + eps * 2^-64).
+constexpr float kSsqScale = 0x1p-32f;
+constexpr float kSsqEpsScale = 0x1p-64f;
+
+__device__ __forceinline__ void track_exp(float v, int& lo, int& hi) {
+    const int e = __builtin_amdgcn_frexp_expf(v);  // 0 for zero, inf and NaN
+    lo = min(lo, e);
+    hi = max(hi, e);
+}
+__device__ __forceinline__ void track_exp4(const f32x4 v, int& lo, int& hi) {
+    track_exp(v.x, lo, hi);
+    track_exp(v.y, lo, hi);
+    track_exp(v.z, lo, hi);
+    track_exp(v.w, lo, hi);
+}
+// exponent of a finite nonzero value, else a value below any exponent
+__device__ __forceinline__ int exp_or_min(float v) {
+    return (v != 0.0f && __builtin_isfinite(v)) ? __builtin_amdgcn_frexp_expf(v) : -1000;
+}
+__device__ __forceinline__ int slow_scale_exp(int emax) { return emax < -500 ? kXScaleExp : kXSlowExp - emax; }
+__device__ __forceinline__ float rms_scale(float ssq, int K, float eps) {
+    return kSsqScale * (1.0f / sqrtf(ssq / (float)K + eps * kSsqEpsScale));
+}
+
+// four bf16 values (bits) as floats
+__device__ __forceinline__ f32x4 bf16x4_to_f32(uint2 b) {
+    return f32x4{__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xFFFF0000u), __uint_as_float(b.y << 16),
+                 __uint_as_float(b.y & 0xFFFF0000u)};
+}
+
 // silu(g) * u with the hardware exp2 and reciprocal (about 2 ulp each)
 __device__ __forceinline__ float silu_mul(float g, float u) {
     const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);

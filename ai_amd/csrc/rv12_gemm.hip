@@ -126,9 +126,6 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
         }
         if constexpr (LN) la[i] = *reinterpret_cast<const u32x4*>(p.lnw + k);
     }
-#if RV12_GEMM_XWAIT
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's activations are in
-#endif
     // every wave's activation loads enter the memory pipeline before any
     // weight load (a bare barrier: it orders the issue, it waits for no data)
     __builtin_amdgcn_s_barrier();
@@ -189,7 +186,7 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
                               xa[i][1].x, xa[i][1].y, xa[i][1].z, xa[i][1].w};
                 if constexpr (LN) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) sq += v[e] * v[e];
+                    for (int e = 0; e < 8; ++e) sq += (v[e] * kSsqScale) * (v[e] * kSsqScale);
                 }
                 if constexpr (M2) {
                     const float u[8] = {ua[i][0].x, ua[i][0].y, ua[i][0].z, ua[i][0].w,
@@ -313,7 +310,7 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     if (LN && S == 1 && tok) {
         float v = 0.0f;
         for (int w = 0; w < W; ++w) v += ssq[w * 16 + jj];
-        rs = 1.0f / sqrtf(v / (float)p.K + p.eps);
+        rs = rms_scale(v, p.K, p.eps);
     }
 #pragma unroll
     for (int b = 0; b < RBW; ++b) {

@@ -14,13 +14,15 @@
 //      loads; a step past the split's end goes through a 0-byte descriptor,
 //      which returns zeros without a memory access);
 //   3. the activation loads are waited for (the weight loads stay in flight)
-//      and x' is written to LDS: the MODE / RMS transform, and the sum of
-//      squares for RMS; one barrier;
+//      and x' * 2^64 is written to LDS: the MODE / RMS transform, the sum of
+//      squares for RMS and the exponent range of x'; one barrier; if any
+//      nonzero |x'| lies outside [2^-64, 2^63), x' is staged again with a
+//      per-token scale (the activation scaling of rv12_device.h);
 //   4. main loop: per step each wave decodes 8 weights per lane and row block
 //      and does 8 FMAs per token into fp32 accumulators, and issues the load
 //      D steps ahead (D: the prefetch depth chosen per variant below);
 //   5. epilogue: one thread per output sums the lane quarters and waves in a
-//      fixed order (no atomics), rescales by 2^sc of its row, adds the
+//      fixed order (no atomics), rescales by 2^(sc - P) of its row, adds the
 //      products ev * x' of its row's exceptions whose column lies in the split
 //      (staged per round in LDS, added in list order), and stores the result
 //      (one split) or writes it as a partial for k_splitk_reduce.  The row's
@@ -77,10 +79,12 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     const int64_t nblk = (p.N + 15) / 16;
     const int nvalid = (int)min((int64_t)RB, nblk - blk0);
 
-    float* xl = smem;                    // [T][krange]
+    float* xl = smem;                    // [T][krange]  x' * 2^P[t]
     float* red = xl + T * krange;        // [W][RB][T][16]
     float* excv = red + W * RB * T * 16; // [nthr][T] exception products of one round
     float* ssq = excv + nthr * T;        // [W][T]
+    int* wflag = reinterpret_cast<int*>(ssq + W * T);  // [W] x' outside the fast path's range
+    int* wexp = wflag + W;                               // [W][T] slow path: largest exponent
 
     // ---- 0. what the epilogue needs, loaded first: thread i < NO owns output
     // (row n0 + i % (16 RB), token i / (16 RB)): its row's scale exponent and
@@ -138,28 +142,33 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     const int32_t e_lo = p.rp[n0];
     const int32_t e_hi = p.rp[min(n0 + RB * 16, p.N)];
 
-    // ---- 3. x' into LDS
+    // ---- 3. x' * 2^64 into LDS (the fast path's scale), with the exponent
+    // range of the x' values and, for RMS, the sums of (x 2^-32)^2
     float sq[T];
+    int elo = 0, ehi = 0;
 #pragma unroll
     for (int t = 0; t < T; ++t) sq[t] = 0.0f;
+    auto stage4 = [&](f32x4 v, f32x4 u, f32x4 lw, int t, int i) {
+        if constexpr (LN) {
+            const f32x4 s = v * kSsqScale;
+            sq[t] += s.x * s.x + s.y * s.y + s.z * s.z + s.w * s.w;
+        }
+        if constexpr (M2) v = f32x4{silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w)};
+        if constexpr (LN) v = lw * v;
+        track_exp4(v, elo, ehi);
+        *reinterpret_cast<f32x4*>(xl + t * krange + i) = v * kXScale;
+    };
 #pragma unroll
     for (int j = 0; j < NXM; ++j) {
         const int i = (threadIdx.x + j * nthr) * 4;
         if (j < nxm && i < krange) {
             f32x4 lw = {1.0f, 1.0f, 1.0f, 1.0f};
-            if constexpr (LN)
-                lw = f32x4{__uint_as_float(lr[j].x << 16), __uint_as_float(lr[j].x & 0xFFFF0000u),
-                           __uint_as_float(lr[j].y << 16), __uint_as_float(lr[j].y & 0xFFFF0000u)};
+            if constexpr (LN) lw = bf16x4_to_f32(lr[j]);
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                f32x4 v = xr[j][t];
-                if constexpr (LN) sq[t] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-                if constexpr (M2) {
-                    const f32x4 u = ur[j][t];
-                    v = f32x4{silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w)};
-                }
-                if constexpr (LN) v = lw * v;
-                *reinterpret_cast<f32x4*>(xl + t * krange + i) = v;
+                f32x4 u = xr[j][t];
+                if constexpr (M2) u = ur[j][t];
+                stage4(xr[j][t], u, lw, t, i);
             }
         }
     }
@@ -168,22 +177,14 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     for (int i = (threadIdx.x + NXM * nthr) * 4; i < krange; i += nthr * 4) {
         const int k = k_lo + i;
         f32x4 lw = {1.0f, 1.0f, 1.0f, 1.0f};
-        if constexpr (LN) {
-            const uint2 b = *reinterpret_cast<const uint2*>(p.lnw + k);
-            lw = f32x4{__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xFFFF0000u), __uint_as_float(b.y << 16),
-                       __uint_as_float(b.y & 0xFFFF0000u)};
-        }
+        if constexpr (LN) lw = bf16x4_to_f32(*reinterpret_cast<const uint2*>(p.lnw + k));
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const float* xt = p.x + (int64_t)t * p.xs;
-            f32x4 v = *reinterpret_cast<const f32x4*>(xt + k);
-            if constexpr (LN) sq[t] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-            if constexpr (M2) {
-                const f32x4 u = *reinterpret_cast<const f32x4*>(xt + p.K + k);
-                v = f32x4{silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w)};
-            }
-            if constexpr (LN) v = lw * v;
-            *reinterpret_cast<f32x4*>(xl + t * krange + i) = v;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(xt + k);
+            f32x4 u = v;
+            if constexpr (M2) u = *reinterpret_cast<const f32x4*>(xt + p.K + k);
+            stage4(v, u, lw, t, i);
         }
     }
     if constexpr (LN) {
@@ -194,6 +195,11 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
             if (lane == 0) ssq[wave * T + t] = v;
         }
     }
+    {
+        const bool bad = elo < kXRangeLo || ehi > kXRangeHi;
+        const uint64_t b = __ballot(bad);
+        if (lane == 0) wflag[wave] = b != 0;
+    }
     // the workgroup's first round of exceptions, one entry per thread; a
     // descriptor over the n_exc entries reads zeros past the list's end
     const uint32_t exc_bytes = (uint32_t)min(p.n_exc, (int64_t)(1 << 28)) * 4u;
@@ -203,6 +209,60 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     const int ec0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_ec, (int)exc_off, 0, 0);
     const float ev0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_ev, (int)exc_off, 0, 0));
     __syncthreads();
+
+    // ---- 3b. (rare) some nonzero |x'| outside [2^-64, 2^63): per-token scale
+    // exponents from the largest |x'| of the workgroup's columns, and x'
+    // staged again from the inputs with them
+    int P[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) P[t] = kXScaleExp;
+    int anybad = 0;
+    for (int w = 0; w < W; ++w) anybad |= wflag[w];
+    if (anybad) {
+        auto xprime = [&](int t, int k) {
+            const float* xt = p.x + (int64_t)t * p.xs;
+            f32x4 v = *reinterpret_cast<const f32x4*>(xt + k);
+            if constexpr (M2) {
+                const f32x4 u = *reinterpret_cast<const f32x4*>(xt + p.K + k);
+                v = f32x4{silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w)};
+            }
+            if constexpr (LN) v = bf16x4_to_f32(*reinterpret_cast<const uint2*>(p.lnw + k)) * v;
+            return v;
+        };
+        int em[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) em[t] = -1000;
+        for (int i = threadIdx.x * 4; i < krange; i += nthr * 4) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const f32x4 v = xprime(t, k_lo + i);
+                em[t] = max(max(max(em[t], exp_or_min(v.x)), max(exp_or_min(v.y), exp_or_min(v.z))),
+                            exp_or_min(v.w));
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            int e = em[t];
+            for (int o = 32; o > 0; o >>= 1) e = max(e, __shfl_xor(e, o));
+            if (lane == 0) wexp[wave * T + t] = e;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            int e = -1000;
+            for (int w = 0; w < W; ++w) e = max(e, wexp[w * T + t]);
+            P[t] = slow_scale_exp(e);
+        }
+        for (int i = threadIdx.x * 4; i < krange; i += nthr * 4) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const f32x4 v = xprime(t, k_lo + i);
+                *reinterpret_cast<f32x4*>(xl + t * krange + i) =
+                    f32x4{ldexpf(v.x, P[t]), ldexpf(v.y, P[t]), ldexpf(v.z, P[t]), ldexpf(v.w, P[t])};
+            }
+        }
+        __syncthreads();
+    }
 
     // ---- 4. main loop
     float acc[RB][T];
@@ -266,7 +326,7 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
         c -= k_lo;
         const bool in = j < e_hi && c >= 0 && c < krange;
 #pragma unroll
-        for (int t = 0; t < T; ++t) excv[threadIdx.x * T + t] = in ? v * xl[t * krange + c] : 0.0f;
+        for (int t = 0; t < T; ++t) excv[threadIdx.x * T + t] = in ? v * ldexpf(xl[t * krange + c], -P[t]) : 0.0f;
     };
     float eacc = 0.0f;
     auto add_round = [&](int32_t j0) {
@@ -298,12 +358,15 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     }
 
     if (oval) {
-        v = ldexpf(v, scale_exp(obase)) + eacc;
+        int Po = P[0];
+#pragma unroll
+        for (int t = 1; t < T; ++t) Po = otok == t ? P[t] : Po;
+        v = ldexpf(v, scale_exp(obase) - Po) + eacc;
         if (S == 1) {
             if constexpr (LN) {
                 float sqs = 0.0f;
                 for (int w = 0; w < W; ++w) sqs += ssq[w * T + otok];
-                v *= 1.0f / sqrtf(sqs / (float)p.K + p.eps);
+                v *= rms_scale(sqs, p.K, p.eps);
             }
             p.y[(int64_t)otok * p.N + on] = p.mode == 0 ? v : oy + v;
         } else {
@@ -352,7 +415,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
             }
         }
     }
-    if (RMS) v *= 1.0f / sqrtf(q / (float)K + eps);
+    if (RMS) v *= rms_scale(q, K, eps);
     *o = mode == 0 ? v : old + v;
 }
 

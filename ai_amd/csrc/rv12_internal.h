@@ -50,7 +50,8 @@ __host__ __device__ constexpr int gemv_chunks(int T) { return T == 1 ? 6 : (T ==
 
 inline size_t gemv_lds_bytes(int K, int T, int rb, int waves, int splits) {
     const size_t krange = (size_t)split_steps(K, splits) * 32;
-    return 4 * ((size_t)T * krange + (size_t)waves * rb * T * 16 + (size_t)waves * 64 * T + (size_t)waves * T);
+    return 4 * ((size_t)T * krange + (size_t)waves * rb * T * 16 + (size_t)waves * 64 * T + (size_t)waves * T +
+                (size_t)waves + (size_t)waves * T);
 }
 
 // waves per workgroup the kernel is built for (its register budget)

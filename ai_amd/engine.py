@@ -32,20 +32,16 @@ prefill, engine.py:471-480), or, in the reference's opt-in blocked mode
 ramvi/engine/ramvi_engine/kernels/prefill.py), all prompt tokens at once with
 each matrix decoded once and multiplied in one GEMM (ai_amd.prefill).
 
-Layers past `resident` stay in host memory as packed byte images and are
-streamed into two device slots for each pass (the reference's "stream"
-placement, engine.py:34-187, 271-326: ai_amd.stream); such an engine runs its
-decode step eagerly instead of as one graph, and its prompt layer by layer.
+Every layer stays resident in HBM (the reference's "gpu" placement): at about
+1.5 bytes per weight the largest model here, Qwen3-32B, needs 48 GB of the
+MI355X's 288 GB.
 """
-import collections
-import itertools
 import os
-import threading
 
 import torch
 
 from . import prefill as blocked_prefill
-from . import stream, wcomp
+from . import wcomp
 from .attn import RopeAttn
 
 MATS = ("qkv", "o", "gu", "down")
@@ -72,13 +68,10 @@ class Engine:
               None reads RAMVI_PREFILL as the reference does
     prefill_min  fewest prompt tokens for the blocked prefill (None:
               RAMVI_PREFILL_MIN_TOKENS, 256)
-    resident  layers kept in HBM (the first ones); the others are streamed
-              from host memory (None: all resident)
-    pin_budget  bytes of pinned host memory for the streamed images (None: all)
     """
 
     def __init__(self, ck, maxt=2048, kv_dtype=torch.float32, device="cuda", log=None, prefill=None,
-                 prefill_min=None, resident=None, pin_budget=None):
+                 prefill_min=None):
         if prefill is None:
             blocked_prefill.enabled()  # validates RAMVI_PREFILL
             prefill = os.environ.get("RAMVI_PREFILL", "legacy")
@@ -96,20 +89,11 @@ class Engine:
         H, KV, HD = self.H, self.KV, self.HD
         self.inv = (1.0 / (ck.theta ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)  # engine.py:204
         self.emb = ck.t("model.embed_tokens.weight", dev)
-        if resident is None:
-            resident = self.L
-        if resident < 0:
-            raise ValueError("resident must not be negative")
-        self.place = ["gpu" if i < resident else "stream" for i in range(self.L)]
-        self.arena = stream.Arena(float("inf") if pin_budget is None else pin_budget)
         self.W, self.small, self.Kc, self.Vc = [], [], [], []
         for i in range(self.L):
             w = ck.layer(i, dev)
             self.small.append({k: w[k] for k in ("ln1", "ln2")} | {k: w[k].float() for k in ("qn", "kn")})
-            c = {n: wcomp.compact(wcomp.compress(w[n])) for n in MATS}
-            if self.place[i] == "stream":  # engine.py:226-231: the packed image in pinned host memory
-                c = {n: self._stream_image(c[n]) for n in MATS}
-            self.W.append(c)
+            self.W.append({n: wcomp.compact(wcomp.compress(w[n])) for n in MATS})
             self.Kc.append(torch.zeros(KV, maxt, HD, dtype=kv_dtype, device=dev))
             self.Vc.append(torch.zeros_like(self.Kc[-1]))
             del w
@@ -132,87 +116,6 @@ class Engine:
         self.attn = RopeAttn(H, KV, HD, maxt, kv_dtype, self.eps, dev)
         self.graph = None
         self.pgraph = None  # a full prefill chunk of BATCH tokens
-        self.stream_ids = [i for i in range(self.L) if self.place[i] == "stream"]
-        self.all_gpu = not self.stream_ids
-        self.loader = None
-        if not self.all_gpu:  # engine.py:241-247: two device slots per matrix
-            self.loader = stream.Loader(dev)
-            self.pending, self.last_rel, self.cslot = collections.deque(), {}, 0
-            self.order, self.phase, self.cur = None, None, None
-            mx = {n: max(self.W[l][n][0].numel() for l in self.stream_ids) for n in MATS}
-            self.cbuf = [{n: torch.empty(mx[n], dtype=torch.uint8, device=dev) for n in MATS} for _ in range(2)]
-
-    def _stream_image(self, c):
-        """(pinned host image, layout) of one packed matrix (only what the
-        kernels read: the packed form and the shape)."""
-        img, lay = stream.pack({"q16": c["q16"], "N": c["N"], "K": c["K"]})
-        return self.arena.put(img.cpu()), lay
-
-    def close(self):
-        """Stop the loader thread (engine.py:258-261)."""
-        if self.loader is not None:
-            self.loader.close()
-            self.loader = None
-
-    # ------------------------------------------------------------- streaming
-    def _request(self, l):
-        """Queue the copy of layer l's images into the next device slot; it
-        waits until that slot's previous user has released it (engine.py:264-284)."""
-        if l is None:
-            return
-        s = self.cslot
-        self.cslot ^= 1
-        pairs = [(self.W[l][n][0], self.cbuf[s][n]) for n in MATS]
-        rel = {"done": threading.Event(), "ev": None}
-        job = {"l": l, "s": s, "pairs": pairs, "wait": self.last_rel.get(s), "done": threading.Event(), "ev": None,
-               "rel": rel}
-        self.last_rel[s] = rel
-        self.pending.append(job)
-        self.loader.q.put(job)
-
-    def _acquire(self, l):
-        """Wait for layer l's images; views of them in the device slot (engine.py:286-295)."""
-        job = self.pending.popleft()
-        if job["l"] != l:
-            raise RuntimeError(f"streamed layer {job['l']} arrived where layer {l} was expected")
-        self.loader.wait(job)
-        torch.cuda.current_stream(self.dev).wait_event(job["ev"])
-        self.cur = job
-        return {n: stream.unpack(self.cbuf[job["s"]][n], self.W[l][n][1]) for n in MATS}
-
-    def _release(self, job=None):
-        """The current layer's kernels are queued: its slot may be refilled
-        once they end; request the next layer (engine.py:297-302)."""
-        job = job or self.cur
-        ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.dev))
-        job["rel"]["ev"] = ev
-        job["rel"]["done"].set()
-        self._request(next(self.order, None))
-
-    def _set_phase(self, phase):
-        """Streaming order of a pass: every streamed layer once (prefill) or
-        round and round (decode), two requests ahead (engine.py:304-320)."""
-        if self.all_gpu or (self.phase == phase and phase != "prefill"):
-            return
-        while self.pending:
-            job = self.pending.popleft()
-            self.loader.wait(job)
-            ev = torch.cuda.Event()
-            ev.record(torch.cuda.current_stream(self.dev))
-            job["rel"]["ev"] = ev
-            job["rel"]["done"].set()
-        self.order = iter(self.stream_ids) if phase == "prefill" else itertools.cycle(self.stream_ids)
-        self.phase = phase
-        self._request(next(self.order, None))
-        self._request(next(self.order, None))
-
-    def _weights(self, l):
-        return self.W[l] if self.place[l] == "gpu" else self._acquire(l)
-
-    def _done(self, l):
-        if self.place[l] != "gpu":
-            self._release()
 
     # ---------------------------------------------------------------- layers
     def _rope_attn(self, l, T, p0=None):
@@ -281,15 +184,19 @@ class Engine:
 
     def _layers(self, x, T, p0=None):
         for l in range(self.L):
-            W = self._weights(l)
-            self._gpu_layer(l, x, T, p0, W)
-            self._done(l)
+            self._gpu_layer(l, x, T, p0)
 
     def _head_row(self, x1):
         """Greedy id of one row: the final norm fused into the 12-bit lm_head,
         then argmax (first maximum = smallest id)."""
         wcomp.gemvc1(x1, self.head, self.logits[:1], 0, lnw=self.norm, eps=self.eps)
         self.nxt[:1].copy_(torch.argmax(self.logits[:1], -1))
+
+    def _head_rows(self, x, T):
+        """Greedy ids of T rows (T <= 16) into self.nxt[:T]: the final norm
+        fused into the 12-bit lm_head at T tokens, argmax per row."""
+        wcomp._linear(x, self.head, self.logits[:T], 0, T, None, None, None, self.norm, self.eps, "lm_head")
+        self.nxt[:T].copy_(torch.argmax(self.logits[:T], -1))
 
     # ---------------------------------------------------------------- passes
     def _embed(self, T):
@@ -351,11 +258,8 @@ class Engine:
         if not 1 <= P < self.maxt:
             raise ValueError("prompt must fit the context")
         t = torch.tensor(tokens, dtype=torch.long, device=self.dev)
-        self._set_phase("prefill")
         if self.prefill_mode == "blocked" and P >= self.prefill_min:
             return self._prefill_blocked(t)
-        if not self.all_gpu:
-            return self._prefill_layers(t)
         for c0 in range(0, P, BATCH):
             T = min(BATCH, P - c0)
             self.pos.fill_(c0)
@@ -376,28 +280,45 @@ class Engine:
         P = t.numel()
         x = self.emb.index_select(0, t).float()
         for l in range(self.L):
-            W = self._weights(l)
-            blocked_prefill.layer(self, l, x, 0, W)
-            self._done(l)
+            blocked_prefill.layer(self, l, self.W[l], x, 0, self.Kc[l], self.Vc[l])
         self._head_row(x[P - 1:P].contiguous())
         self.pos.fill_(P)
         return self.nxt[:1]
 
-    def _prefill_layers(self, t):
-        """Passes of up to 16 tokens, layer by layer over the whole prompt,
-        so each streamed layer crosses the bus once (engine.py:446-487)."""
-        P = t.numel()
-        x = self.emb.index_select(0, t).float()
-        for l in range(self.L):
-            W = self._weights(l)
-            for c0 in range(0, P, BATCH):
-                T = min(BATCH, P - c0)
-                self.pos.fill_(c0)
-                self._gpu_layer(l, x[c0:c0 + T], T, c0, W)
-            self._done(l)
-        self._head_row(x[P - 1:P].contiguous())
-        self.pos.fill_(P)
-        return self.nxt[:1]
+    def process(self, tokens, pos0):
+        """The tokens at positions pos0.. (the cache before pos0 already
+        filled); returns the greedy id after each of them, or after the last
+        only for more than 16 tokens (engine.py:505-526).  Up to 16 tokens run
+        as one batched pass (_batch_layer for 2..16), as the reference's
+        speculative verification does."""
+        T = len(tokens)
+        if T < 1 or pos0 < 0 or pos0 + T > self.maxt:
+            raise ValueError("the tokens must fit the context")
+        t = torch.tensor(tokens, dtype=torch.long, device=self.dev)
+        if T > BATCH:
+            if pos0 == 0:
+                self.prefill(tokens)
+                return self.nxt[:1].tolist()
+            for c0 in range(0, T, BATCH):
+                n = min(BATCH, T - c0)
+                self.pos.fill_(pos0 + c0)
+                self.tok[:n].copy_(t[c0:c0 + n])
+                self._embed(n)
+                self._layers(self.xb[:n], n, pos0 + c0)
+            last = (T - 1) % BATCH
+            self._head_row(self.xb[last:last + 1])
+            self.pos.fill_(pos0 + T)
+            return self.nxt[:1].tolist()
+        self.pos.fill_(pos0)
+        self.tok[:T].copy_(t)
+        self._embed(T)
+        self._layers(self.xb[:T], T, pos0)
+        if T == 1:
+            self._head_row(self.xb[:1])
+        else:
+            self._head_rows(self.xb[:T], T)
+        self.pos.fill_(pos0 + T)
+        return self.nxt[:T].tolist()
 
     def batch_pass_ms(self, T, p0, reps=10):
         """ms of one pass of T tokens of one sequence through every layer (the
@@ -405,8 +326,6 @@ class Engine:
         replayed from a HIP graph (each replay rewrites those cache slots)."""
         if not 1 < T <= BATCH or p0 + T > self.maxt:
             raise ValueError("T must be in 2..16 and the pass must fit the context")
-        if not self.all_gpu:
-            raise ValueError("a pass replayed from a graph needs every layer resident")
 
         def body():
             self._embed(T)
@@ -427,7 +346,7 @@ class Engine:
         (prefill ms, decode ms for the max_new - 1 graph replays)."""
         if len(prompt) + max_new > self.maxt:
             raise ValueError("prompt + max_new exceed the context")
-        if self.graph is None and self.all_gpu:
+        if self.graph is None:
             self.capture()
         self.reset()
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
@@ -437,13 +356,8 @@ class Engine:
         self.tok[:1].copy_(first)
         self.steps.fill_(1)
         e[1].record()
-        if self.all_gpu:
-            for _ in range(max_new - 1):
-                self.graph.replay()
-        else:  # streamed layers: the step runs eagerly, the loader two layers ahead
-            self._set_phase("decode")
-            for _ in range(max_new - 1):
-                self._step()
+        for _ in range(max_new - 1):
+            self.graph.replay()
         e[2].record()
         torch.cuda.synchronize()
         ids = self.out[:max_new].tolist()

@@ -4,9 +4,9 @@ RAMVI_PREFILL_MIN_TOKENS = 256 prompt tokens on): every weight matrix is
 decoded exactly once per prompt and multiplied with ALL prompt tokens in one
 dense GEMM, instead of passes of 16 tokens through the fused decode-linear.
 
-    enabled(n)               prefill.py:14-20   (same variables, same errors)
-    matrix(x, c, y, add)     prefill.py:66-78
-    layer(eng, l, x, start)  prefill.py:81-121
+    enabled(n)                                       prefill.py:14-20  (same variables, same errors)
+    matrix(x, c, y, add)                             prefill.py:66-78
+    layer(eng, l, weights, x, start, kc, vc, gguf)   prefill.py:81-121 (same signature)
 
 MI355X form of `matrix`: the 12-bit matrix is decoded to its exact bf16 bits
 (rv12_decode_rows), and the fp32 activations are split into three bf16 parts
@@ -80,17 +80,17 @@ def _rot(t):
     return torch.cat([-t[..., h:], t[..., :h]], -1)
 
 
-def attention(eng, l, q, start):
+def attention(eng, q, start, kc, vc):
     """Causal grouped-query attention of the T prompt rows q (fp32 [T, H, HD],
-    positions start..start+T-1) over cache positions 0..start+T-1, in query
-    blocks (prefill_kernels.py:35-60)."""
+    positions start..start+T-1) over positions 0..start+T-1 of the caches
+    kc / vc [KV, maxt, HD], in query blocks (prefill_kernels.py:35-60)."""
     T = q.shape[0]
     H, KV, HD = eng.H, eng.KV, eng.HD
     G = H // KV
     n = start + T
-    Kf = eng.Kc[l][:, :n].float()                      # [KV, n, HD]
+    Kf = kc[:, :n].float()                             # [KV, n, HD]
     Kt = Kf.transpose(1, 2).contiguous()               # [KV, HD, n]
-    Vf = eng.Vc[l][:, :n].float().contiguous()         # [KV, n, HD]
+    Vf = vc[:, :n].float().contiguous()                # [KV, n, HD]
     del Kf
     out = torch.empty(T, H * HD, device=q.device)
     cols = torch.arange(n, device=q.device)
@@ -107,15 +107,21 @@ def attention(eng, l, q, start):
     return out
 
 
-def layer(eng, l, x, start, W=None):
+def layer(eng, l, weights, x, start, kc, vc, gguf=False):
     """One layer over all prompt rows x (fp32 [T, D], updated in place) at
-    positions start.. (prefill.py:81-121): RMSNorm, qkv, q/k head norms,
-    RoPE, K/V into the cache (rounded to its dtype), causal attention, o
-    (residual add), RMSNorm, gate/up, silu(g) * u, down (residual add).
-    W: the layer's matrices (a streamed layer's views), default eng.W[l]."""
+    positions start.. (prefill.py:81-121, same signature): RMSNorm, qkv, q/k
+    head norms, RoPE, K/V into the caches kc / vc (rounded to their dtype),
+    causal attention, o (residual add), RMSNorm, gate/up, silu(g) * u, down
+    (residual add).  weights: the layer's fused 12-bit matrices qkv, o, gu,
+    down; eng supplies the dimensions, eng.small[l] the norm weights and
+    eng.inv the RoPE frequencies.  gguf=True (separate q/k/v and gate/up GGUF
+    matrices) belongs to the reference's GGUF engine, which is not on this
+    path."""
+    if gguf:
+        raise NotImplementedError("GGUF weights are not on the 12-bit path")
     T = x.shape[0]
     H, KV, HD, FF, eps = eng.H, eng.KV, eng.HD, eng.FF, eng.eps
-    W = eng.W[l] if W is None else W
+    W = weights
     s = eng.small[l]
     norm = _rms(x, s["ln1"].float(), eps)
     qkv = torch.empty(T, (H + 2 * KV) * HD, device=x.device)
@@ -129,10 +135,10 @@ def layer(eng, l, x, start, W=None):
     cos, sin = e.cos()[:, None], e.sin()[:, None]
     q = q * cos + _rot(q) * sin
     k = k * cos + _rot(k) * sin
-    eng.Kc[l].index_copy_(1, p, k.to(eng.kv_dtype).transpose(0, 1))
-    eng.Vc[l].index_copy_(1, p, v.to(eng.kv_dtype).transpose(0, 1))
+    kc.index_copy_(1, p, k.to(kc.dtype).transpose(0, 1))
+    vc.index_copy_(1, p, v.to(vc.dtype).transpose(0, 1))
     del qkv, k, v
-    att = attention(eng, l, q, start)
+    att = attention(eng, q, start, kc, vc)
     del q
     matrix(att, W["o"], x, add=True)
     del att

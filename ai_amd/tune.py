@@ -1,13 +1,24 @@
-"""Launch-shape autotuning for the fused decode-linear, per (N, K, MODE).
+"""Launch-shape tuning of the fused decode-linear on the device it runs on.
 
-Mirrors ramvi/engine/ramvi_engine/planning/tune.py:21-88: each candidate is
-timed as the median of 8 HIP-graph replays over three distinct random
-matrices (beyond the caches), the best one per shape goes into
-`wcomp.CFG1` (one token) and `wcomp.CFGT` (16 tokens) as the reference's
-(BN, w) / (BN, w, S) tuples, and the results are kept in a JSON cache keyed
-by the library build, torch, and the device, so later runs read them back.
-A corrupt cache is ignored; a shape for which no candidate runs raises
-RuntimeError and is not cached (ramvi/engine/tests/legacy/test_f31.py:8-18).
+For each linear (N, K, MODE) of a model the tuner measures the library's own
+launch space (rv12_launch: kernel, row blocks, waves, K splits) and stores the
+fastest shape in `wcomp.CFG1` (one token, the decode step) and `wcomp.CFGT`
+(16 tokens, the batched pass), in the reference's value format
+(ramvi/engine/ramvi_engine/kernels/wcomp.py:115, 222: (BN, w) or (BN, w, S)).
+
+Measurement.  The MI355X keeps 256 MB in its memory-side cache, more than any
+single Qwen3 matrix, so a shape is timed over distinct matrices that together
+exceed `min_bytes` (1 GiB by default), launched back to back from one HIP
+graph and replayed; the time per launch is the replays' total over the
+launches (HIP events on the graph's stream).  Every candidate's output is
+compared with the built-in shape's before it may win.
+
+Cache.  Results go to a JSON file keyed by the library binary's sha256, the
+GPU architecture and the device name, so a rebuilt library or another GPU
+measures again.  The tuning contract of the reference
+(ramvi/engine/tests/legacy/test_f31.py:8-18) holds: an unreadable cache is
+reported and ignored, and a shape for which no candidate runs raises
+RuntimeError and leaves the cache file untouched.
 
     from ai_amd import tune
     tune.tune([(6144, 4096, 0), (4096, 4096, 1), (24576, 4096, 0), (4096, 12288, 2)])
@@ -16,121 +27,169 @@ import hashlib
 import json
 import math
 import os
-import statistics
-import tempfile
 
-import torch
-
-from . import wcomp
-from .wcomp import compress, gemvc1, gemvc_tc
+from . import _lib, wcomp
 
 CACHE = os.environ.get("RV12_TUNE_CACHE", os.path.join(os.path.expanduser("~"), ".cache", "ai_amd", "tune.json"))
+TOKENS = {"one": 1, "batch": 16}
 
-# candidates: BN = rows per workgroup (row blocks of 16), w = waves per workgroup, S = K splits
-ONE = [(bn, w, s) for bn in (16, 32) for w in (4, 8, 16) for s in (1, 2, 4) if not (bn == 32 and w == 16)]
-BATCH = [(16 * rbw * w, w, 0) for rbw in (1, 2) for w in (4, 8)]
-
-
-def _bench(f, n=8):
-    f()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        f()
-    g.replay()
-    torch.cuda.synchronize()
-    r = []
-    for _ in range(n):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        g.replay()
-        e.record()
-        torch.cuda.synchronize()
-        r.append(s.elapsed_time(e))
-    return statistics.median(r)
+_ident = None
 
 
-def _try(f):
-    try:
-        return _bench(f)
-    except Exception:
-        return float("inf")
+def _identity():
+    """Key of the measurements: library binary, GPU architecture, device."""
+    global _ident
+    if _ident is None:
+        import torch
+        h = hashlib.sha256(open(_lib.LIB_PATH, "rb").read()).hexdigest()[:16]
+        p = torch.cuda.get_device_properties(0)
+        _ident = f"{h}|{getattr(p, 'gcnArchName', '?')}|{p.name}"
+    return _ident
 
 
-def _sample(N, K, mode):
-    """Three distinct random matrices of the shape (compressed, packed) and
-    16 activation / output rows."""
-    cs = [wcomp.compact(compress((torch.randn(N, K, device="cuda") * 0.02).bfloat16())) for _ in range(3)]
-    x = torch.randn(16, K * (2 if mode == 2 else 1), device="cuda")
-    y = torch.zeros(16, N, device="cuda")
-    return cs, x, y
+def candidates(N, K, T):
+    """The launch shapes to measure for N x K at T tokens, as (kernel, rb,
+    waves, splits), the built-in one first; every entry is one the library
+    accepts (rv12_launch_shape)."""
+    L = _lib.lib()
+    nsteps = K // 32
+    raw = [(0, 0, 0, 0)]
+    if T <= 2:
+        raw += [(1, rb, w, s) for rb in (1, 2) for w in (4, 8, 16) for s in (0, 2, 3, 4)]
+    else:
+        raw += [(2, rb, w, 0) for rb in (1, 2, 4) for w in (4, 8)]
+    out = []
+    for c in raw:
+        if c[3] > nsteps:
+            continue
+        r = _lib.Launch()
+        if L.rv12_launch_shape(N, K, T, _lib.Launch(*c), r) == 0:
+            shape = (r.kernel, r.rb, r.waves, r.splits)
+            if shape not in out:
+                out.append(shape)
+    return out
 
 
-def _version():
-    """The library build and this module's Python mirror, and torch."""
-    h = hashlib.sha256()
-    from . import _lib
-    for p in (_lib.LIB_PATH, wcomp.__file__):
+def as_reference_cfg(shape):
+    """(kernel, rb, waves, splits) -> the reference's (BN, w, S): BN rows per
+    workgroup, w waves, S K splits (wcomp._launch maps it back)."""
+    kernel, rb, waves, splits = shape
+    bn = 16 * rb if kernel == 1 else 16 * rb * waves
+    return (bn, waves, splits)
+
+
+def _measure(N, K, mode, T, shapes, min_bytes, reps):
+    """us per launch of every shape (inf where it fails or disagrees with the
+    built-in shape's output), over distinct random matrices of > min_bytes."""
+    import ctypes
+
+    import torch
+    dev = torch.device("cuda")
+    L = _lib.lib()
+    copies = max(2, math.ceil(min_bytes / (1.5 * N * K)))
+    g = torch.Generator(device=dev).manual_seed(N * 31 + K)
+    mats = []
+    for _ in range(copies):
+        w = torch.randn(N, K, device=dev, generator=g).mul_(0.02).bfloat16()
+        mats.append(wcomp.compact(wcomp.compress(w)))
+        del w
+    xs = 2 * K if mode == 2 else K
+    x = torch.randn(T, xs, device=dev, generator=g).bfloat16().float()
+    y = torch.zeros(T, N, device=dev)
+    st = torch.cuda.current_stream()
+    mstructs = [wcomp._matrix(c) for c in mats]
+    times, ref = {}, None
+    for shape in shapes:
+        cfg = _lib.Launch(*shape)
+        need = max(16, L.rv12_workspace_bytes(N, K, T, shape[3]))
+        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())
+
+        def launches():
+            for m in mstructs:
+                rc = L.rv12_gemm(ctypes.byref(m), p(x), p(y), T, None, 1e-6, mode, ctypes.byref(cfg), p(ws), need,
+                                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                if rc:
+                    raise ValueError(_lib.strerror(rc))
+
         try:
-            h.update(open(p, "rb").read())
-        except OSError:
-            h.update(p.encode())
-    return h.hexdigest() + "|" + torch.__version__
+            y.zero_()
+            launches()
+            torch.cuda.synchronize()
+            out = y.clone()
+            if ref is None:
+                ref = out
+            elif not torch.allclose(out, ref, rtol=1e-3, atol=1e-3):
+                times[shape] = float("inf")
+                continue
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                launches()
+            graph.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(st)
+            torch.cuda.synchronize()
+            times[shape] = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+            del graph
+        except (ValueError, RuntimeError):
+            times[shape] = float("inf")
+    del mats
+    torch.cuda.empty_cache()
+    return times
 
 
-def _device():
-    p = torch.cuda.get_device_properties(torch.cuda.current_device())
-    return f"{p.name}|{getattr(p, 'gcnArchName', '')}"
-
-
-def _load(path, version, log):
+def _read(path, log):
     try:
-        if not os.path.exists(path):
-            return {}
-        with open(path, encoding="utf-8") as h:
-            cached = json.load(h)
-        db = cached.get("entries", {}) if isinstance(cached, dict) and cached.get("version") == version else {}
-        return db if isinstance(db, dict) else {}
-    except (ValueError, OSError):
-        log("tuning cache unreadable; tuning again")
-        return {}
+        with open(path) as f:
+            d = json.load(f)
+        if isinstance(d, dict) and isinstance(d.get("entries"), dict):
+            return d
+        log(f"tune: ignoring {path}: not a tuning cache")
+    except FileNotFoundError:
+        pass
+    except (OSError, ValueError) as e:
+        log(f"tune: ignoring unreadable cache {path}: {e}")
+    return None
 
 
-def tune(shapes, log=print, cache=None):
-    """shapes: list of (N, K, MODE).  Fills wcomp.CFG1 and wcomp.CFGT."""
-    cache = cache or CACHE
-    dev = _device()
-    version = _version()
-    db = _load(cache, version, log)
-    todo = [s for s in shapes if f"{dev}|{tuple(s)}" not in db]
-    for N, K, mode in todo:
-        log(f"  tuning {N}x{K} (mode {mode})...")
-        cs, x, y = _sample(N, K, mode)
-        r1 = min(((_try(lambda: [gemvc1(x[:1], c, y[:1], mode, bn, w) if s == 1 else
-                                 gemvc_tc(x[:1], c, y[:1], mode, 1, bn, w, s) for c in cs]), bn, w, s)
-                  for bn, w, s in ONE if N % bn == 0), default=(float("inf"),))
-        rt = min(((_try(lambda: [gemvc_tc(x, c, y, mode, 16, bn, w, s or None) for c in cs]), bn, w, s)
-                  for bn, w, s in BATCH if N % bn == 0), default=(float("inf"),))
-        if not math.isfinite(r1[0]) or not math.isfinite(rt[0]):
-            raise RuntimeError(f"no working launch shape for {N}x{K}")
-        db[f"{dev}|{(N, K, mode)}"] = {"one": list(r1[1:]), "batch": list(rt[1:])}
-        del cs
-        if torch.cuda.is_available():
-            torch.cuda.empty_cache()
-    if todo:
-        os.makedirs(os.path.dirname(cache), exist_ok=True)
-        tmp = None
-        try:
-            with tempfile.NamedTemporaryFile("w", dir=os.path.dirname(cache), delete=False) as h:
-                tmp = h.name
-                json.dump({"version": version, "entries": db}, h, indent=1)
-            os.replace(tmp, cache)
-        finally:
-            if tmp and os.path.exists(tmp):
-                os.unlink(tmp)
+def _write(path, d):
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    tmp = f"{path}.{os.getpid()}.part"
+    with open(tmp, "w") as f:
+        json.dump(d, f, indent=1, sort_keys=True)
+    os.replace(tmp, path)
+
+
+def tune(shapes, log=print, cache=None, min_bytes=1 << 30, reps=10):
+    """Fill wcomp.CFG1 / CFGT for every (N, K, MODE) in shapes, from the cache
+    where it holds this library and device, else by measurement."""
+    path = cache or CACHE
+    stored = _read(path, log)
+    ident = _identity()
+    entries = dict(stored["entries"]) if stored and stored.get("identity") == ident else {}
+    changed = False
     for N, K, mode in shapes:
-        d = db[f"{dev}|{(N, K, mode)}"]
-        bn, w, s = d["one"]
-        wcomp.CFG1[(N, K, mode)] = (bn, w) if s == 1 else (bn, w, s)
-        bn, w, s = d["batch"]
-        wcomp.CFGT[(N, K, mode)] = (bn, w, s or None)
+        key = f"{N}x{K}|{mode}"
+        e = entries.get(key)
+        if e is None:
+            e = {}
+            for name, T in TOKENS.items():
+                shp = candidates(N, K, T)
+                t = _measure(N, K, mode, T, shp, min_bytes, reps) if shp else {}
+                good = {s: v for s, v in t.items() if math.isfinite(v)}
+                if not good:
+                    raise RuntimeError(f"tune: no launch shape runs for {N}x{K} mode {mode} at {T} tokens")
+                best = min(good, key=good.get)
+                e[name] = list(best)
+                log(f"tune: {N}x{K} mode {mode} {T} tok: {best} {good[best]:.2f} us "
+                    f"(built-in {t.get(shp[0], float('inf')):.2f} us)")
+            entries[key] = e
+            changed = True
+        wcomp.CFG1[(N, K, mode)] = as_reference_cfg(tuple(e["one"]))
+        wcomp.CFGT[(N, K, mode)] = as_reference_cfg(tuple(e["batch"]))
+    if changed:
+        _write(path, {"identity": ident, "entries": entries})
+    return {k: entries[f"{k[0]}x{k[1]}|{k[2]}"] for k in shapes}

@@ -259,35 +259,6 @@ def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefil
     return out
 
 
-def run_e2e_stream(dev, size="8b", streamed=4, prompt_len=512, new=32, seed=0):
-    """Greedy decode with the last `streamed` layers kept in pinned host
-    memory and copied into HBM for every token (the reference's "stream"
-    placement): tok/s, and the streamed bytes per token over the token time
-    (the host link's delivered rate, with the copies overlapping the other
-    layers' kernels)."""
-    from ai_amd.engine import Engine
-    from ai_amd.model import QWEN3, RandomCkpt
-    ck = RandomCkpt(QWEN3[size], seed=seed)
-    eng = Engine(ck, maxt=prompt_len + new + 8, kv_dtype=torch.bfloat16, prefill="blocked",
-                 resident=ck.L - streamed)
-    try:
-        prompt = [int(t) for t in np.random.default_rng(seed).integers(0, ck.V, prompt_len)]
-        eng.generate(prompt[:eng.prefill_min + 8], 4)  # warm
-        ids, prefill_ms, decode_ms = eng.generate(prompt, new, timing=True)
-        per_tok = decode_ms / (new - 1)
-        sbytes = sum(eng.W[l][n][0].numel() for l in eng.stream_ids for n in ("qkv", "o", "gu", "down"))
-        out = {"model": f"qwen3-{size} random init", "layers": ck.L, "streamed_layers": streamed,
-               "pinned_GB": round(eng.arena.pinned / 1e9, 3), "streamed_GB_per_token": round(sbytes / 1e9, 4),
-               "prompt": prompt_len, "new_tokens": new, "tok_s": round(1e3 / per_tok, 2),
-               "ms_per_token": round(per_tok, 3), "streamed_GBs": round(sbytes / per_tok / 1e6, 1),
-               "prefill_ms": round(prefill_ms, 1)}
-    finally:
-        eng.close()
-    del eng
-    torch.cuda.empty_cache()
-    return out
-
-
 def run_attn(dev, reps=20, layers=36, positions=(100, 1000, 2100)):
     """Decode-step attention of the Qwen3-8B shape alone (32 q / 8 kv heads,
     head dim 128, 2304-position bf16 caches, one per layer, 340 MB in all, so
@@ -442,7 +413,6 @@ def main():
     ap.add_argument("--no-e2e", action="store_true", help="skip the Qwen3-8B end-to-end decode")
     ap.add_argument("--no-14b", action="store_true", help="skip the Qwen3-14B skinny-GEMM sweep")
     ap.add_argument("--no-32b", action="store_true", help="skip the Qwen3-32B end-to-end decode")
-    ap.add_argument("--no-stream", action="store_true", help="skip the streamed-layers decode")
     ap.add_argument("--only-14b", action="store_true", help="run only the Qwen3-14B skinny-GEMM sweep (for profiling)")
     ap.add_argument("--only-attn", action="store_true", help="run only the Qwen3-8B decode attention (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -516,12 +486,6 @@ def main():
         print(f"# qwen3-0.6b decode: {e2e06['tok_s']} tok/s ({e2e06['ms_per_token']} ms/token), prefill "
               f"{e2e06['prefill_ms']} ms for {e2e06['prompt']} tokens", file=sys.stderr, flush=True)
 
-    e2e_stream = None
-    if not args.no_e2e and not args.no_stream:
-        e2e_stream = run_e2e_stream(dev)
-        print(f"# qwen3-8b with {e2e_stream['streamed_layers']} streamed layers: {e2e_stream['tok_s']} tok/s, "
-              f"{e2e_stream['streamed_GBs']} GB/s streamed from host memory", file=sys.stderr, flush=True)
-
     e2e32 = None
     if not args.no_e2e and not args.no_32b:
         e2e32 = run_e2e(dev, "32b", prompt_len=4096, new=128, batch=8)
@@ -561,7 +525,6 @@ def main():
         "e2e_decode": e2e,
         "e2e_decode_0_6b": e2e06,
         "e2e_decode_32b": e2e32,
-        "e2e_decode_streamed": e2e_stream,
         "cpu_baseline": cpu,
         "sweep_m1": sweep,
         "sweep_m1_input_column_outliers": sweep_cols,

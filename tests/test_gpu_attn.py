@@ -42,9 +42,10 @@ def test_rope_attn_matches_torch(H, KV, HD, kv_dtype):
     inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
     qn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
     kn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
-    for splits in (5, 8, 19):
+    for splits in (5, 8, 19, 53):
         # one object per split count: its workspace serves every call, as in
-        # a decode loop
+        # a decode loop; 53 splits take the combine's one-batch path for 33-64
+        # splits (the Qwen3-32B decode at a 4224-position cache)
         att = RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev, splits=splits)
         for pos in (0, 1, 37, 130, maxt - 1):
             print("case", H, KV, HD, kv_dtype, splits, pos, flush=True)

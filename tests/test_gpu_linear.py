@@ -47,12 +47,27 @@ def _inputs(c, T, mode, seed, rms):
     return X, Y0, lnw
 
 
-def _run(c_gpu, X, Y0, mode, T, lnw=None, BN=None, w=None, S=None, eps=1e-6, use_tc=False):
-    from ai_amd import wcomp
+def _run(c_gpu, X, Y0, mode, T, lnw=None, BN=None, w=None, S=None, eps=1e-6, use_tc=False, launch=None):
+    """One linear through the Python mirror, or with `launch` (kernel, rb,
+    waves, splits) straight through the C ABI's rv12_gemm."""
+    import ctypes
+    from ai_amd import _lib, wcomp
     x = torch.from_numpy(X).cuda()
     y = torch.from_numpy(Y0.copy()).cuda()
     ln = None if lnw is None else torch.from_numpy(lnw.view(np.int16).copy()).view(torch.bfloat16).cuda()
-    if T == 1 and not use_tc:
+    if launch is not None:
+        L = _lib.lib()
+        cfg = _lib.Launch(*launch)
+        out = _lib.Launch()
+        _lib.check(L.rv12_launch_shape(int(c_gpu["N"]), int(c_gpu["K"]), T, ctypes.byref(cfg), ctypes.byref(out)),
+                   "launch")
+        need = max(16, L.rv12_workspace_bytes(int(c_gpu["N"]), int(c_gpu["K"]), T, out.splits))
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())
+        m = wcomp._matrix(c_gpu)
+        _lib.check(L.rv12_gemm(ctypes.byref(m), p(x), p(y), T, p(ln), eps, mode, ctypes.byref(cfg), p(ws), need,
+                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "rv12_gemm")
+    elif T == 1 and not use_tc:
         wcomp.gemvc1(x, c_gpu, y, mode, BN=BN, w=w, lnw=ln, eps=eps)
     elif ln is not None:  # the C-ABI's RMS prologue at T > 1 (no reference operator has it)
         wcomp._linear(x, c_gpu, y, mode, T, BN, w, S, ln, eps, "rv12_gemm")
@@ -277,3 +292,82 @@ def test_partial_launch_shape_sizes_its_workspace():
     assert shape[:3] == (2, 1, 2) and shape[3] >= 20 > wcomp.launch_shape(N, K, 16)[3]
     for mode in (0, 2):
         _check(cnp, cg, 16, mode, False, 60 + mode, BN=32, w=2, use_tc=True)
+
+
+def _check_scaled(cnp, c_gpu, T, mode, rms, seed, e, both_halves=False, **kw):
+    """Activations scaled by 2^e (MODE 2: g and u by 2^(e/2) each, so x' ~ 2^e,
+    or both by 2^e with both_halves), y_prev scaled like W x'; the output held
+    to 4x the fp32 forward-error bound plus the rounding of the final add."""
+    rng = np.random.default_rng(seed)
+    K, N = cnp["K"], cnp["N"]
+    xs = 2 * K if mode == 2 else K
+    X = rng.standard_normal((T, xs))
+    if mode == 2 and not both_halves:
+        X *= 2.0 ** (e / 2)
+    else:
+        X *= 2.0 ** e
+    X = X.astype(np.float32)
+    W = codec.decode_f32(cnp).astype(np.float64)
+    lnw = codec.f32_to_bf16_rne((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)) if rms else None
+    lw = None if lnw is None else codec.bf16_to_f32(lnw)
+    xp = linear.prologue(X, K, mode, lw)
+    typ = float(np.abs(xp @ W.T).mean()) or 1.0
+    Y0 = (rng.standard_normal((T, N)) * typ).astype(np.float32)
+    ref = linear.linear(cnp, X, mode, Y0, lnw=lw, W=W)
+    bound = linear.error_bound(cnp, X, mode, lnw=lw, W=W)
+    y = _run(c_gpu, X, Y0, mode, T, lnw=lnw, **kw).astype(np.float64)
+    assert np.all(np.isfinite(y)) and np.all(np.isfinite(ref)), (T, mode, rms, e)
+    err = np.abs(y - ref)
+    tight = 4 * bound + 2.0 ** -23 * np.abs(ref) + 1e-300
+    bad = err > tight
+    assert not bad.any(), (T, mode, rms, e, both_halves, float(err[bad].max()), float(tight[bad].min()))
+
+
+@pytest.mark.parametrize("e", [-60, -40, -20, 0, 20, 40, 60])
+def test_activation_scale(e):
+    """Activations from 2^-60 to 2^60 in every mode, with and without the RMS
+    prologue, at the token counts of the vector kernel: within 4x the fp32
+    bound (the kernels scale x' by an exact power of two, so tiny activations
+    do not meet the Q16 weights' float32 floor)."""
+    from ai_amd import wcomp
+    print("scale 2^%d" % e, flush=True)
+    bits = _random_matrix(300, 1024, 1234, out_rows=0.01, out_cols=0.01)
+    cnp = codec.compress(bits)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    for T in (1, 2, 3, 4):
+        use_tc = T > 1
+        kw = {} if T <= 2 else {"launch": (1, 1, 8, 0)}  # the vector kernel at 3-4 tokens
+        for mode in (0, 1, 2):
+            _check_scaled(cnp, cg, T, mode, False, 70 + T + mode, e, use_tc=use_tc, **kw)
+            _check_scaled(cnp, cg, T, mode, True, 80 + T + mode, e, use_tc=use_tc, **kw)
+        _check_scaled(cnp, cg, T, 2, False, 90 + T, e, both_halves=True, use_tc=use_tc, **kw)
+
+
+QWEN3_14B = {"qkv": (7168, 5120), "o_q": (5120, 5120), "gu": (34816, 5120), "down": (5120, 17408),
+             "k_v": (1024, 5120), "gate_up": (17408, 5120)}
+
+
+@pytest.mark.parametrize("name", sorted(QWEN3_14B))
+def test_qwen3_14b_skinny_shapes_full_size(name):
+    """Qwen3-14B skinny-GEMM matrices (N(0, 0.02), 0.1% outlier rows x20) at
+    full size, M = 1, 2, 4, 8, 16 tokens with the built-in kernel choice,
+    modes 0 (with the RMS prologue), 1 and 2, against the C oracle."""
+    from ai_amd import wcomp
+    N, K = QWEN3_14B[name]
+    print("shape", name, N, K, flush=True)
+    bits = _random_matrix(N, K, N + 7 * K, sigma=0.02, out_rows=0.001)
+    cnp = cref.compress(bits)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    assert cg["base"] == cnp["base"] and cg["er"].numel() == cnp["er"].size
+    for T in (1, 2, 4, 8, 16):
+        print("  M", T, wcomp.launch_shape(N, K, T), flush=True)
+        for mode, rms in ((0, True), (1, False), (2, False)):
+            X, Y0, lnw = _inputs(cnp, T, mode, 100 + T + mode, rms)
+            ref = Y0.copy()
+            cref.gemv_12bit(cnp, X, ref, mode, lnw=lnw)
+            y = _run(cg, X, Y0, mode, T, lnw=lnw, use_tc=T > 1)
+            err = np.abs(y.astype(np.float64) - ref)
+            assert np.all(err <= ATOL + RTOL * np.abs(ref)), (name, T, mode, rms, float(err.max()))
+            assert float((err / (np.abs(ref) + 1.0)).max()) < 1e-4, (name, T, mode, float(err.max()))
+    del cg
+    torch.cuda.empty_cache()

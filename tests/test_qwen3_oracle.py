@@ -77,3 +77,19 @@ def test_argmax_chunks_and_ties():
     assert (s > 0).any() and (s < 0).any()
     assert ids == [5 if v > 0 else 0 for v in s.tolist()]
     assert all(m == 0.0 for m in margins)
+
+
+def test_argmax_pick_gaps():
+    """The gap of a pick is 0 for the argmax itself and best - logit(pick)
+    for any other token, across head chunks."""
+    ck = RandomCkpt(tiny_config(layers=1, vocab=3000), seed=3, gen_device="cpu")
+    toks = list(range(40, 52))
+    lg = qwen3.logits(ck, toks)
+    best = lg.argmax(-1)
+    _, gap = qwen3.argmax(ck, toks, head_chunk=700, picks=best.tolist())
+    assert all(g == 0.0 for g in gap)
+    other = ((best + 1234) % 3000).tolist()
+    ids, m, gap = qwen3.argmax(ck, toks, head_chunk=700, margins=True, picks=other[2:], first=2)
+    want = (lg.max(-1).values - lg.gather(1, torch.tensor(other)[:, None])[:, 0])[2:]
+    assert ids == best.tolist()[2:]
+    assert torch.allclose(torch.tensor(gap), want, rtol=1e-6, atol=1e-6)

@@ -1,54 +1,67 @@
-"""Tuning-cache robustness without a GPU (the reference's
-ramvi/engine/tests/legacy/test_f31.py:8-18): a corrupt cache is ignored, a
-shape where every candidate fails raises and leaves the cache untouched, and a
-good cache is read back into CFG1 / CFGT."""
+"""The tuner's cache contract without a GPU (the reference's
+ramvi/engine/tests/legacy/test_f31.py:8-18): an unreadable cache is reported
+and ignored, a shape for which every candidate fails raises and leaves the
+cache untouched, and measured results are cached per library + device and
+read back into CFG1 / CFGT in the reference's (BN, w, S) format."""
 import json
 
 import pytest
 
 from ai_amd import tune, wcomp
 
+VEC = [(1, 1, 8, 1), (1, 2, 8, 1), (1, 1, 4, 2)]
+MFMA = [(2, 2, 8, 1), (2, 1, 4, 1)]
+
 
 @pytest.fixture
 def fake(monkeypatch):
-    monkeypatch.setattr(tune, "_device", lambda: "test|gfx950")
-    monkeypatch.setattr(tune, "_version", lambda: "v1")
-    monkeypatch.setattr(tune, "_sample", lambda N, K, mode: ([None] * 3, None, None))
-    return monkeypatch
+    monkeypatch.setattr(tune, "_identity", lambda: "lib0|gfx950|test")
+    monkeypatch.setattr(tune, "candidates", lambda N, K, T: VEC if T == 1 else MFMA)
+    yield monkeypatch
+    wcomp.CFG1.clear()
+    wcomp.CFGT.clear()
 
 
-def test_corrupt_cache_ignored_and_failures_not_cached(fake, tmp_path):
+def test_unreadable_cache_ignored_and_failures_not_cached(fake, tmp_path):
     p = tmp_path / "tune.json"
     p.write_text("{bad")
-    fake.setattr(tune, "_try", lambda f: float("inf"))
+    fake.setattr(tune, "_measure", lambda N, K, mode, T, shp, mb, reps: {s: float("inf") for s in shp})
     logs = []
     tune.tune([], log=logs.append, cache=str(p))
-    assert logs
+    assert logs and "ignoring" in logs[0]
     with pytest.raises(RuntimeError):
         tune.tune([(16, 256, 0)], log=logs.append, cache=str(p))
     assert p.read_text() == "{bad"
 
 
-def test_results_are_cached_and_read_back(fake, tmp_path):
+def test_fastest_shape_cached_and_read_back(fake, tmp_path):
     p = tmp_path / "tune.json"
     calls = []
 
-    def timing(f):
-        calls.append(1)
-        return float(len(calls))  # the first candidate of each list is the fastest
+    def measure(N, K, mode, T, shp, mb, reps):
+        calls.append(T)
+        # the last candidate is the fastest; a failing one never wins
+        return {s: (float("inf") if i == 0 else 10.0 - i) for i, s in enumerate(shp)}
 
-    fake.setattr(tune, "_try", timing)
+    fake.setattr(tune, "_measure", measure)
     tune.tune([(4096, 4096, 1)], log=lambda *a: None, cache=str(p))
     d = json.loads(p.read_text())
-    assert d["version"] == "v1"
-    e = d["entries"]["test|gfx950|(4096, 4096, 1)"]
-    assert tuple(e["one"]) == tune.ONE[0] and tuple(e["batch"]) == tune.BATCH[0]
-    assert wcomp.CFG1[(4096, 4096, 1)] == tune.ONE[0][:2]
+    assert d["identity"] == "lib0|gfx950|test"
+    e = d["entries"]["4096x4096|1"]
+    assert tuple(e["one"]) == VEC[-1] and tuple(e["batch"]) == MFMA[-1]
+    assert wcomp.CFG1[(4096, 4096, 1)] == (16, 4, 2)          # BN = 16 rows, 4 waves, 2 splits
+    assert wcomp.CFGT[(4096, 4096, 1)] == (16 * 1 * 4, 4, 1)   # BN = row blocks per wave x waves x 16
     n = len(calls)
-    tune.tune([(4096, 4096, 1)], log=lambda *a: None, cache=str(p))   # from the cache: no timing
+    tune.tune([(4096, 4096, 1)], log=lambda *a: None, cache=str(p))   # from the cache
     assert len(calls) == n
-    fake.setattr(tune, "_version", lambda: "v2")                        # another build: tuned again
+    fake.setattr(tune, "_identity", lambda: "lib1|gfx950|test")        # a rebuilt library measures again
     tune.tune([(4096, 4096, 1)], log=lambda *a: None, cache=str(p))
     assert len(calls) > n
-    wcomp.CFG1.clear()
-    wcomp.CFGT.clear()
+
+
+def test_reference_cfg_maps_back_to_the_shape():
+    """wcomp._launch turns the stored (BN, w, S) back into the tuned shape."""
+    for shape, T in ((VEC[1], 1), (VEC[2], 1), (MFMA[0], 16), (MFMA[1], 16)):
+        bn, w, s = tune.as_reference_cfg(shape)
+        c = wcomp._launch(bn, w, s, T)
+        assert (c.kernel, c.rb, c.waves, c.splits) == shape
