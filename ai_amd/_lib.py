@@ -15,15 +15,16 @@ LIB_PATH = os.path.join(HERE, "librv12.so")
 
 RV12_OK = 0
 RV12_E_NULL, RV12_E_SHAPE, RV12_E_MODE, RV12_E_TOKENS = -1, -2, -3, -4
-RV12_E_WORKSPACE, RV12_E_CONFIG, RV12_E_BASE, RV12_E_ALIGN, RV12_E_SIZE = -5, -6, -7, -8, -9
+RV12_E_WORKSPACE, RV12_E_CONFIG, RV12_E_BASE, RV12_E_ALIGN, RV12_E_SIZE, RV12_E_SCRATCH = -5, -6, -7, -8, -9, -10
 RV12_E_LAUNCH = -20
 
 # every symbol include/rv12.h declares
 EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_pack_plan", "rv12_pack",
            "rv12_codec_to_bf16", "rv12_encode_stats", "rv12_encode", "rv12_encode_exc", "rv12_launch_shape",
            "rv12_workspace_bytes",
-           "rv12_gemv", "rv12_gemm", "rv12_decode_rows", "rv12_attn_workspace_bytes", "rv12_rope_attn")
+           "rv12_gemv", "rv12_gemm", "rv12_gemm_static", "rv12_decode_rows", "rv12_attn_workspace_bytes", "rv12_rope_attn")
 ABI_VERSION = 4
+STATIC_SCRATCH_BYTES = 8 << 20  # RV12_STATIC_SCRATCH_BYTES
 
 
 class Codec(ctypes.Structure):
@@ -95,6 +96,8 @@ def lib():
         L.rv12_gemv.argtypes = [ctypes.POINTER(Matrix), P, P, P, F, I, ctypes.POINTER(Launch), P, SZ, P]
         L.rv12_gemm.restype = I
         L.rv12_gemm.argtypes = [ctypes.POINTER(Matrix), P, P, I, P, F, I, ctypes.POINTER(Launch), P, SZ, P]
+        L.rv12_gemm_static.restype = I
+        L.rv12_gemm_static.argtypes = [ctypes.POINTER(Matrix), P, P, I, P, F, I, ctypes.POINTER(Launch), P]
         L.rv12_decode_rows.restype = I
         L.rv12_decode_rows.argtypes = [ctypes.POINTER(Matrix), I, I, P, I, P]
         L.rv12_attn_workspace_bytes.restype = SZ

@@ -234,6 +234,7 @@ const char* rv12_strerror(int s) {
         case RV12_E_BASE: return "base must be in [0, 241]";
         case RV12_E_ALIGN: return "x, y, lnw or tiles not aligned (16 bytes; lnw 8 bytes)";
         case RV12_E_SIZE: return "tiles buffer smaller than rv12_tiles_bytes()";
+        case RV12_E_SCRATCH: return "workspace of the launch exceeds the static scratch (RV12_STATIC_SCRATCH_BYTES, 8 MiB)";
         case RV12_E_LAUNCH: return "kernel launch failed";
     }
     return "unknown rv12 status";

@@ -35,6 +35,7 @@ enum rv12_status {
     RV12_E_BASE = -7,      /* base outside [0, 241] */
     RV12_E_ALIGN = -8,     /* x, y or tiles not 16-byte aligned */
     RV12_E_SIZE = -9,      /* output buffer smaller than rv12_tiles_bytes() */
+    RV12_E_SCRATCH = -10,  /* rv12_gemm_static: workspace beyond RV12_STATIC_SCRATCH_BYTES */
     RV12_E_LAUNCH = -20    /* hipGetLastError() after a launch */
 };
 
@@ -161,6 +162,21 @@ int rv12_gemv(const rv12_matrix* w, const float* x, float* y, const uint16_t* ln
  * ramvi/engine/ramvi_engine/kernels/wcomp.py:155-242. */
 int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps, int mode,
               const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream);
+
+/* rv12_gemm with the split-K workspace in a scratch array the library holds
+ * in device memory (RV12_STATIC_SCRATCH_BYTES on every GPU it runs on, until
+ * the process ends) instead of a caller-owned one: no device memory is
+ * allocated by the call.  A launch whose workspace (rv12_workspace_bytes for
+ * the shape it resolves to) exceeds the scratch returns RV12_E_SCRATCH before
+ * any device work.  The first call on a device looks up that device's scratch
+ * address (with the device current); every call on one GPU shares its scratch,
+ * so calls that overlap on one GPU (other streams, other threads) race.  No
+ * counterpart in the reference: it serves callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  Other arguments and statuses as rv12_gemm. */
+#define RV12_STATIC_SCRATCH_BYTES (8u << 20)
+int rv12_gemm_static(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps,
+                     int mode, const rv12_launch* cfg, void* stream);
 
 /* Bit-exact decode of rows [first, last) to bf16 bits (out_f32 == 0, out is
  * uint16[last-first, K]) or to float32 (out_f32 != 0, out is float[last-first, K]).

@@ -32,7 +32,7 @@ def test_abi_version_and_strerror():
     from ai_amd import _lib
     L = _lib.lib()
     assert L.rv12_abi_version() == 4
-    for s in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -20):
+    for s in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -20):
         assert _lib.strerror(s) and _lib.strerror(s) != "unknown rv12 status"
     assert _lib.strerror(-99) == "unknown rv12 status"
 
@@ -167,6 +167,20 @@ def test_pack_decode_encode_argument_errors():
                          ctypes.c_void_p(0x3000), ctypes.c_void_p(0x4000), None) == _lib.RV12_E_BASE
     assert L.rv12_encode(ctypes.c_void_p(0x1000), 4, 250, 256, 10, ctypes.c_void_p(0x2000),
                          ctypes.c_void_p(0x3000), ctypes.c_void_p(0x4000), None) == _lib.RV12_E_SHAPE
+
+
+def test_static_scratch_entry_rejects_oversized_workspace():
+    """rv12_gemm_static checks the launch's workspace against its static
+    scratch (8 MiB) before any device call."""
+    from ai_amd import _lib
+    L = _lib.lib()
+    assert L.rv12_gemm_static(None, None, None, 1, None, 1e-6, 0, None, None) == _lib.RV12_E_NULL
+    m = _lib.Matrix(0x1000, 0x2000, 0x3000, 0, 0, 0, 8192, 2048, 0)
+    cfg = _lib.Launch(1, 1, 4, 64)   # 64 splits x 4 tokens x 8192 rows of partials: 8 MiB + sums of squares
+    assert L.rv12_workspace_bytes(8192, 2048, 4, 64) > _lib.STATIC_SCRATCH_BYTES
+    p = ctypes.c_void_p(0x10000)
+    assert L.rv12_gemm_static(ctypes.byref(m), p, p, 4, None, 1e-6, 0, ctypes.byref(cfg), None) == _lib.RV12_E_SCRATCH
+    assert L.rv12_gemm_static(ctypes.byref(m), p, p, 17, None, 1e-6, 0, None, None) == _lib.RV12_E_TOKENS
 
 
 def test_python_mirror_rejects_cpu_tensors():
