@@ -218,6 +218,15 @@ bool shape_ok(int n, int k) { return n >= 1 && k >= 32 && k % 32 == 0 && k <= kM
 
 }  // namespace
 
+int64_t rv12::launch_ws_bytes(int n, int k, int t, const rv12_launch* cfg) {
+    if (!shape_ok(n, k)) return RV12_E_SHAPE;
+    if (t < 1 || t > 16) return RV12_E_TOKENS;
+    Shape c;
+    const int rc = resolve_launch(n, k, t, cfg, &c);
+    if (rc) return rc;
+    return (int64_t)ws_bytes_for(n, t, c.splits);
+}
+
 extern "C" {
 
 int rv12_abi_version(void) { return RV12_ABI_VERSION; }
@@ -318,6 +327,11 @@ size_t rv12_workspace_bytes(int n, int k, int t, int splits) {
     if (n < 1 || k < 32 || k % 32 || k > kMaxK || t < 1 || t > 16) return 0;
     if (splits == 0) splits = default_shape(n, k, t).splits;
     return ws_bytes_for(n, t, splits);
+}
+
+size_t rv12_launch_workspace_bytes(int n, int k, int t, const rv12_launch* cfg) {
+    const int64_t b = launch_ws_bytes(n, k, t, cfg);
+    return b < 0 ? 0 : (size_t)b;
 }
 
 int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps, int mode,

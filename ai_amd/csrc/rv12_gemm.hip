@@ -18,16 +18,23 @@
 //      = one step x one lane: token l%16, k = 8(l/16) + 0..7);
 //   2. each wave issues the loads of its first D weight steps (D = kDepth, half
 //      that with four row blocks per wave: the same bytes in flight);
-//   3. x' is formed (MODE / RMS transform), split into hi/mid/lo and written
-//      to LDS in B-operand lane order (tokens >= T are zeros); barrier;
+//   3. x' is formed (MODE / RMS transform), scaled by 2^64 and split into
+//      hi/mid/lo, and written to LDS in B-operand lane order (tokens >= T are
+//      zeros); barrier.  The scale lifts the products of the Q16 values
+//      (h << 16 is below 2^-111) with x' out of the float32 subnormal range
+//      that an unscaled x' of moderate size would put them in; where some
+//      nonzero |x'| of the split lies outside [2^-64, 2^63) (found by a ballot
+//      and an LDS flag per wave), the parts are staged again with x' * 2^P,
+//      P = 100 - the exponent of the split's largest |x'| per token;
 //   4. main loop: per step three ds_read_b128 fetch the B parts, each of the
 //      wave's row blocks is unpacked once and meets the three parts in three
 //      MFMAs into three independent accumulators;
 //   5. epilogue per wave: the exceptions of the wave's rows whose column is
 //      inside the split are added per (row, token) in list order (the entries
-//      found by a ballot, one at a time), x' taken from the LDS parts; the sum of
-//      the three accumulators is rescaled by 2^sc, the exception sums added,
-//      and stored (one split) or written as a partial for k_splitk_reduce.
+//      found by a ballot, one at a time), x' taken from the LDS parts times
+//      2^-P; the sum of the three accumulators is rescaled by 2^(sc - P), the
+//      exception sums added, and stored (one split) or written as a partial
+//      for k_splitk_reduce.
 //      The exception range, the row windows and the old y are loaded right
 //      after the weight prefetch, the first 64 exception entries right after
 //      the x' staging, so the epilogue waits for no memory in the common case.
@@ -104,6 +111,8 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     u32x4* xb = lds4;                                               // [nst][3][64]
     float* exc = reinterpret_cast<float*>(xb + (size_t)nst * 192);  // [W*RBW*16 rows][16 tokens]
     float* ssq = exc + W * RBW * 256;                               // [W][16]
+    int* wflag = reinterpret_cast<int*>(ssq + W * 16);              // [W] x' outside the fast path's range
+    int* wexp = wflag + W;                                          // [W][16] slow path: largest exponent
 
     // ---- 1. activations of this thread's B groups, as straight-line loads:
     // a group past the split's steps reads column k_lo again and a token
@@ -173,8 +182,10 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
             oy[b] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r_y, (min(jj, T - 1) * p.N + nb) * 4, 0, 0));
     }
 
-    // ---- 3. x' split into bf16 parts, in B-operand order
+    // ---- 3. x' * 2^64 split into bf16 parts, in B-operand order; the
+    // exponent range of x' is tracked for the fast path's check
     float sq = 0.0f;
+    int elo = 0, ehi = 0;
 #pragma unroll
     for (int i = 0; i < kGroupsPerThread; ++i) {
         const int g = threadIdx.x + i * nthr;
@@ -202,6 +213,11 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
                         v[2 * e + 1] *= __uint_as_float(lw[e] & 0xFFFF0000u);
                     }
                 }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    track_exp(v[e], elo, ehi);
+                    v[e] *= kXScale;
+                }
                 split3(v, hi, mid, lo);
             }
             u32x4* d = xb + (size_t)s * 192 + (g & 63);
@@ -214,6 +230,11 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
         sq += __shfl_xor(sq, 16);
         sq += __shfl_xor(sq, 32);
         if (lane < 16) ssq[wave * 16 + lane] = sq;
+    }
+    {
+        const bool bad = elo < kXRangeLo || ehi > kXRangeHi;
+        const uint64_t bm = __ballot(bad);
+        if (lane == 0) wflag[wave] = bm != 0;
     }
     // this wave's exception sums start at zero
     float* excw = exc + wu * RBW * 256;
@@ -229,6 +250,72 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     const int ec0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r_ec, (int)e_off, 0, 0);
     const float ev0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_ev, (int)e_off, 0, 0));
     __syncthreads();
+
+    // ---- 3b. (rare) some nonzero |x'| of the split outside [2^-64, 2^63):
+    // per-token scale exponents P from the largest |x'| of the split, and the
+    // parts staged again from the inputs with x' * 2^P.  Pj is the exponent of
+    // this thread's token jj, the token of its outputs and exception sums.
+    int Pj = kXScaleExp;
+    int anybad = 0;
+    for (int w = 0; w < W; ++w) anybad |= wflag[w];
+    if (anybad) {
+        auto xprime = [&](int k, float (&v)[8]) {
+            const f32x4 a0 = *reinterpret_cast<const f32x4*>(xrow + k);
+            const f32x4 a1 = *reinterpret_cast<const f32x4*>(xrow + k + 4);
+            v[0] = a0.x, v[1] = a0.y, v[2] = a0.z, v[3] = a0.w, v[4] = a1.x, v[5] = a1.y, v[6] = a1.z, v[7] = a1.w;
+            if constexpr (M2) {
+                const f32x4 u0 = *reinterpret_cast<const f32x4*>(xrow + p.K + k);
+                const f32x4 u1 = *reinterpret_cast<const f32x4*>(xrow + p.K + k + 4);
+                const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = silu_mul(v[e], u[e]);
+            }
+            if constexpr (LN) {
+                const u32x4 l = *reinterpret_cast<const u32x4*>(p.lnw + k);
+                const uint32_t lw[4] = {l.x, l.y, l.z, l.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[2 * e] *= __uint_as_float(lw[e] << 16);
+                    v[2 * e + 1] *= __uint_as_float(lw[e] & 0xFFFF0000u);
+                }
+            }
+        };
+        int em = -1000;
+        for (int i = 0; i < kGroupsPerThread; ++i) {
+            const int s = (threadIdx.x + i * nthr) >> 6;
+            if (s < nst && tok) {
+                float v[8];
+                xprime(k_lo + s * 32 + (lane >> 4) * 8, v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) em = max(em, exp_or_min(v[e]));
+            }
+        }
+        // lanes jj, jj + 16, jj + 32, jj + 48 hold token jj
+        em = max(em, __shfl_xor(em, 16));
+        em = max(em, __shfl_xor(em, 32));
+        if (lane < 16) wexp[wave * 16 + lane] = em;
+        __syncthreads();
+        em = -1000;
+        for (int w = 0; w < W; ++w) em = max(em, wexp[w * 16 + jj]);
+        Pj = slow_scale_exp(em);
+        for (int i = 0; i < kGroupsPerThread; ++i) {
+            const int g = threadIdx.x + i * nthr;
+            const int s = g >> 6;
+            if (s < nst && tok) {
+                float v[8];
+                xprime(k_lo + s * 32 + (lane >> 4) * 8, v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = ldexpf(v[e], Pj);
+                u32x4 hi, mid, lo;
+                split3(v, hi, mid, lo);
+                u32x4* d = xb + (size_t)s * 192 + (g & 63);
+                d[0] = hi;
+                d[64] = mid;
+                d[128] = lo;
+            }
+        }
+        __syncthreads();
+    }
 
     // ---- 4. main loop
     f32x4 acc[RBW][3];
@@ -297,7 +384,7 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
                     const float xv = bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o)) +
                                      bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o + 1024)) +
                                      bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o + 2048));
-                    excw[rr * 16 + lane] += vv * xv;
+                    excw[rr * 16 + lane] += vv * ldexpf(xv, -Pj);
                 }
             }
         }
@@ -325,7 +412,7 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
         }
         float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = ldexpf(av[i], scale_exp(ob[i])) + excw[(b * 16 + q * 4 + i) * 16 + jj];
+        for (int i = 0; i < 4; ++i) v[i] = ldexpf(av[i], scale_exp(ob[i]) - Pj) + excw[(b * 16 + q * 4 + i) * 16 + jj];
         if (!tok) continue;
         if (S == 1) {
             if constexpr (LN) {

@@ -73,7 +73,9 @@ constexpr size_t kGemmMaxLds = 131072;
 constexpr int kGemmMaxWaves = 8;
 inline size_t gemm_lds_bytes(int K, int rbw, int waves, int splits) {
     const size_t steps = (size_t)split_steps(K, splits);
-    return steps * 3 * 1024 + (size_t)waves * rbw * 16 * 16 * 4 + 16 * 4 * (size_t)waves;
+    // parts, exception sums, sums of squares, range flags, slow-path exponents
+    return steps * 3 * 1024 + (size_t)waves * rbw * 16 * 16 * 4 + 16 * 4 * (size_t)waves + 4 * (size_t)waves +
+           16 * 4 * (size_t)waves;
 }
 inline bool gemm_fits(int K, int rbw, int waves, int splits) {
     return waves <= kGemmMaxWaves && gemm_lds_bytes(K, rbw, waves, splits) <= kGemmMaxLds;
@@ -109,6 +111,9 @@ int launch_attn(const AttnParams& p, int splits, hipStream_t st);
 
 int launch_gemv(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st);
 int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st);
+// workspace bytes of the launch rv12_gemm resolves (n, k, t, cfg) to; a
+// negative status where it rejects the shape or cfg
+int64_t launch_ws_bytes(int n, int k, int t, const rv12_launch* cfg);
 void launch_splitk_reduce(const LinearParams& p, int T, int splits, hipStream_t st);
 void launch_codec_to_bf16(const rv12_codec& c, uint16_t* w, hipStream_t st);
 void launch_pack_plan(const uint16_t* w, int N, int K, int32_t* rbase, int32_t* row_exc, hipStream_t st);

@@ -50,11 +50,9 @@ extern "C" int rv12_gemm_static(const rv12_matrix* w, const float* x, float* y, 
     // every argument check of rv12_gemm that needs the launch shape, and the
     // scratch bound, before any device call
     if (!w) return RV12_E_NULL;
-    rv12_launch shape;
-    const int rc = rv12_launch_shape(w->n, w->k, t, cfg, &shape);
-    if (rc) return rc;
-    const size_t need = rv12_workspace_bytes(w->n, w->k, t, shape.splits);
-    if (need > (size_t)RV12_STATIC_SCRATCH_BYTES) return RV12_E_SCRATCH;
+    const int64_t need = rv12::launch_ws_bytes(w->n, w->k, t, cfg);
+    if (need < 0) return (int)need;
+    if (need > (int64_t)RV12_STATIC_SCRATCH_BYTES) return RV12_E_SCRATCH;
     void* ws = nullptr;
     const int sr = scratch_ptr(&ws);
     if (sr) return sr;

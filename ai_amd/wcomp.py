@@ -212,21 +212,30 @@ def launch_shape(N, K, T, cfg=None):
 _SK_RETIRED = []  # workspaces replaced by larger ones: kept alive for graphs that captured them
 
 
-def _sk_buf(N, S, dev, K=None, T=16):
-    """Workspace for split partial sums, cached per (N, device) (wcomp.py:226-230).
-    Sized, as the reference's, for 16 tokens and at least 8 splits, so one
-    buffer serves every batch size; a buffer that must grow is retired, not
-    freed, because a captured HIP graph may still hold its address."""
+def _sk_buf(N, S, dev, K=None, T=16, cfg=None):
+    """Workspace for split partial sums, cached per (N, device)
+    (wcomp.py:226-230): at least what the launch (N, K, T, cfg) resolves to
+    needs, and what the built-in 16-token launch needs, so one buffer serves
+    every batch size; a buffer that must grow is retired, not freed, because a
+    captured HIP graph may still hold its address (the retired ones go with
+    _SK when the caches are cleared)."""
     L = lib()
     K = int(K or 32 * max(S, 1))
-    need = max(L.rv12_workspace_bytes(int(N), K, int(T), int(S)), L.rv12_workspace_bytes(int(N), K, 16, 0),
-               L.rv12_workspace_bytes(int(N), K, 16, min(max(int(S), 8), K // 32)))
+    need = max(L.rv12_launch_workspace_bytes(int(N), K, int(T), None if cfg is None else ctypes.byref(cfg)),
+               L.rv12_workspace_bytes(int(N), K, 16, 0))
     k = (N, str(dev))
     if k not in _SK or _SK[k].numel() < need:
         if k in _SK:
             _SK_RETIRED.append(_SK[k])
         _SK[k] = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
     return _SK[k]
+
+
+def clear_caches():
+    """Drop every cached workspace, the retired ones too (the engine's
+    caches are cleared with the last session, model_loader.py:385-390)."""
+    _SK.clear()
+    _SK_RETIRED.clear()
 
 
 def _linear(x, c, y, mode, T, BN, w, S, lnw, eps, where):
@@ -248,8 +257,8 @@ def _linear(x, c, y, mode, T, BN, w, S, lnw, eps, where):
             raise ValueError(f"{where}: lnw must be a contiguous bf16 vector of K entries")
     m = _matrix(c)
     cfg = _launch(BN, w, S, T)
-    splits = launch_shape(N, K, T, cfg)[3]  # the split count the launch resolves to
-    ws = _sk_buf(N, splits, x.device, K, T)
+    launch_shape(N, K, T, cfg)  # validates the configuration (ValueError)
+    ws = _sk_buf(N, 0, x.device, K, T, cfg)
     rc = lib().rv12_gemm(ctypes.byref(m), _ptr(x), _ptr(y), int(T), _ptr(lnw), float(eps), int(mode),
                          ctypes.byref(cfg), _ptr(ws), ws.numel(), _stream(x.device))
     check(rc, where)

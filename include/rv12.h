@@ -145,8 +145,15 @@ int rv12_encode_exc(const uint16_t* w, int n, int k, int base, const int32_t* rp
 
 /* Workspace bytes a linear needs: splits * t * ceil(n/16)*16 partial sums and
  * splits * t sums of squares (0 when splits == 1).  splits == 0 asks for the
- * built-in choice for (n, k, t). */
+ * built-in choice for (n, k, t).  No counterpart in the reference, whose
+ * wcomp.py:226-230 allocates the split buffer itself. */
 size_t rv12_workspace_bytes(int n, int k, int t, int splits);
+
+/* Workspace bytes of exactly the launch rv12_gemm resolves (n, k, t, cfg) to
+ * (cfg NULL: the built-in shape; a cfg with only some fields set has the rest
+ * filled in as rv12_launch_shape does); 0 where it needs none or where
+ * rv12_gemm would reject the arguments. */
+size_t rv12_launch_workspace_bytes(int n, int k, int t, const rv12_launch* cfg);
 
 /* T = 1 fused decode + GEMV:  y (=|+=) W_dec . x'
  *   mode 0: y = W x';  1: y += W x';  2: x' = silu(x[0:K]) * x[K:2K], y += W x'

@@ -46,6 +46,17 @@ def test_sizes():
     assert L.rv12_workspace_bytes(4096, 4096, 1, 1) == 0
     assert L.rv12_workspace_bytes(4096, 4096, 2, 4) == 4 * (4 * 2 * 4096 + 4 * 2)
     assert L.rv12_workspace_bytes(4096, 4096, 17, 1) == 0
+    # the exact launch: the split count rv12_gemm resolves (n, k, t, cfg) to
+    lw = lambda n, k, t, cfg=None: L.rv12_launch_workspace_bytes(n, k, t, None if cfg is None else ctypes.byref(cfg))
+    assert lw(4096, 4096, 1) == 0
+    assert lw(1024, 4096, 2, _lib.Launch(1, 1, 4, 4)) == 4 * (4 * 2 * 1024 + 4 * 2)
+    for n, k, t, cfg in ((5120, 5120, 8, None), (1024, 5120, 16, None), (5120, 17408, 16, None),
+                         (2048, 5120, 16, _lib.Launch(2, 1, 2, 0))):    # the split count left to the library
+        c = _lib.Launch()
+        assert L.rv12_launch_shape(n, k, t, None if cfg is None else ctypes.byref(cfg), ctypes.byref(c)) == 0
+        assert c.splits > 1 and lw(n, k, t, cfg) == L.rv12_workspace_bytes(n, k, t, c.splits)
+    assert lw(4096, 4096, 1, _lib.Launch(3, 1, 4, 2)) == 0                 # rejected: 0
+    assert lw(4096, 100, 1) == 0 and lw(4096, 4096, 17) == 0
 
 
 def test_launch_shapes():

@@ -144,13 +144,13 @@ def test_shapes_and_launch_shapes(N, K):
         for mode in (0, 2):
             _check(cnp, cg, 1, mode, mode == 0, 7, BN=BN, w=w)
             _check(cnp, cg, 2, mode, False, 8, BN=BN, w=w, S=S, use_tc=True)
-    # MFMA kernel (the built-in choice from 3 tokens): BN = row blocks per wave x waves x 16
-    for BN, w, S in ((16, 1, None), (64, 2, None), (128, 4, None), (64, 4, nsteps), (256, 8, None)):
-        if N % BN:
-            BN = None
-        print("  mfma launch", BN, w, S, flush=True)
-        for mode in (0, 2):
-            _check(cnp, cg, 3, mode, False, 9, BN=BN, w=w, S=S, use_tc=True)
+    # MFMA kernel (the built-in choice from 3 tokens): every row-block count
+    # per wave and wave count it takes (the split count left to the library),
+    # straight through the C ABI
+    for rb, w, S in [(rb, w, 0) for rb in (1, 2, 4) for w in (1, 2, 4, 8)] + [(1, 4, nsteps), (4, 2, nsteps // 4)]:
+        print("  mfma launch", rb, w, S, flush=True)
+        for T, mode, rms in ((3, 0, True), (3, 2, False), (16, 1, False), (11, 2, True)):
+            _check(cnp, cg, T, mode, rms, 9 + T, launch=(2, rb, w, S))
 
 
 def test_bn_must_divide_rows():
@@ -334,13 +334,39 @@ def test_activation_scale(e):
     bits = _random_matrix(300, 1024, 1234, out_rows=0.01, out_cols=0.01)
     cnp = codec.compress(bits)
     cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
-    for T in (1, 2, 3, 4):
+    cases = [(1, {}), (2, {}), (3, {"launch": (1, 1, 8, 0)}), (4, {"launch": (1, 1, 8, 0)}),  # vector kernel
+             (3, {}), (8, {}), (16, {}), (16, {"launch": (2, 2, 4, 0)})]                        # MFMA kernel
+    for T, kw in cases:
         use_tc = T > 1
-        kw = {} if T <= 2 else {"launch": (1, 1, 8, 0)}  # the vector kernel at 3-4 tokens
         for mode in (0, 1, 2):
             _check_scaled(cnp, cg, T, mode, False, 70 + T + mode, e, use_tc=use_tc, **kw)
             _check_scaled(cnp, cg, T, mode, True, 80 + T + mode, e, use_tc=use_tc, **kw)
         _check_scaled(cnp, cg, T, 2, False, 90 + T, e, both_halves=True, use_tc=use_tc, **kw)
+
+
+def test_activation_scale_mixed_tokens():
+    """Tokens of very different scales in one batch (2^-50, 1, 2^50, and one
+    token of zeros): each keeps the fp32 bound (the MFMA kernel's scale is
+    per token)."""
+    from ai_amd import wcomp
+    bits = _random_matrix(200, 2048, 4321, out_rows=0.01)
+    cnp = codec.compress(bits)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    W = codec.decode_f32(cnp).astype(np.float64)
+    rng = np.random.default_rng(5)
+    for T, kw in ((2, {}), (4, {"launch": (1, 1, 8, 0)}), (7, {}), (16, {})):
+        for mode in (0, 2):
+            K = cnp["K"]
+            X = rng.standard_normal((T, 2 * K if mode == 2 else K))
+            X *= np.array([2.0 ** (-50 if t % 3 == 0 else (50 if t % 3 == 1 else 0)) for t in range(T)])[:, None]
+            X[T // 2] = 0.0
+            X = X.astype(np.float32)
+            Y0 = np.zeros((T, cnp["N"]), np.float32)
+            ref = linear.linear(cnp, X, mode, Y0, W=W)
+            bound = linear.error_bound(cnp, X, mode, W=W)
+            y = _run(cg, X, Y0, mode, T, use_tc=True, **kw).astype(np.float64)
+            err = np.abs(y - ref)
+            assert not (err > 4 * bound + 2.0 ** -23 * np.abs(ref) + 1e-300).any(), (T, mode, float(err.max()))
 
 
 QWEN3_14B = {"qkv": (7168, 5120), "o_q": (5120, 5120), "gu": (34816, 5120), "down": (5120, 17408),
