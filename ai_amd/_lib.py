@@ -21,7 +21,7 @@ RV12_E_LAUNCH = -20
 # every symbol include/rv12.h declares
 EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_pack_plan", "rv12_pack",
            "rv12_codec_to_bf16", "rv12_encode_stats", "rv12_encode", "rv12_encode_exc", "rv12_launch_shape",
-           "rv12_workspace_bytes", "rv12_launch_workspace_bytes",
+           "rv12_workspace_bytes", "rv12_launch_workspace_bytes", "rv12_head_argmax", "rv12_head_workspace_bytes",
            "rv12_gemv", "rv12_gemm", "rv12_gemm_static", "rv12_decode_rows", "rv12_attn_workspace_bytes", "rv12_rope_attn")
 ABI_VERSION = 4
 STATIC_SCRATCH_BYTES = 8 << 20  # RV12_STATIC_SCRATCH_BYTES
@@ -98,6 +98,10 @@ def lib():
         L.rv12_gemv.argtypes = [ctypes.POINTER(Matrix), P, P, P, F, I, ctypes.POINTER(Launch), P, SZ, P]
         L.rv12_gemm.restype = I
         L.rv12_gemm.argtypes = [ctypes.POINTER(Matrix), P, P, I, P, F, I, ctypes.POINTER(Launch), P, SZ, P]
+        L.rv12_head_argmax.restype = I
+        L.rv12_head_argmax.argtypes = [ctypes.POINTER(Matrix), P, I, P, F, P, P, ctypes.POINTER(Launch), P, SZ, P]
+        L.rv12_head_workspace_bytes.restype = SZ
+        L.rv12_head_workspace_bytes.argtypes = [I, I, I, ctypes.POINTER(Launch)]
         L.rv12_gemm_static.restype = I
         L.rv12_gemm_static.argtypes = [ctypes.POINTER(Matrix), P, P, I, P, F, I, ctypes.POINTER(Launch), P]
         L.rv12_decode_rows.restype = I

@@ -227,6 +227,73 @@ int64_t rv12::launch_ws_bytes(int n, int k, int t, const rv12_launch* cfg) {
     return (int64_t)ws_bytes_for(n, t, c.splits);
 }
 
+namespace {
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Workspace of a greedy pick (rv12_head_argmax), each part 256-byte aligned:
+// the linear's split partials, then either the fused pick's per-workgroup
+// pairs (vector kernel, one split) or the logits, then the first pick
+// stage's pairs where more than one chunk is reduced.
+struct HeadWs {
+    bool fused;
+    int64_t m;  // entries the pick reduces per token
+    size_t pv, pi, logits, tv, ti, total;
+};
+
+HeadWs head_ws(int n, int t, const Shape& c) {
+    HeadWs h{};
+    h.fused = c.kernel == 1 && c.splits == 1;
+    size_t o = align256(ws_bytes_for(n, t, c.splits));
+    if (h.fused) {
+        h.m = (nblocks(n) + c.rb - 1) / c.rb;  // workgroups of the vector kernel
+        h.pv = o;
+        o = align256(o + (size_t)t * h.m * 4);
+        h.pi = o;
+        o = align256(o + (size_t)t * h.m * 4);
+    } else {
+        h.m = n;
+        h.logits = o;
+        o = align256(o + (size_t)t * n * 4);
+    }
+    const int64_t nc = h.m > kPickChunk ? pick_chunks(h.m) : 0;
+    h.tv = o;
+    o = align256(o + (size_t)t * nc * 4);
+    h.ti = o;
+    o = align256(o + (size_t)t * nc * 4);
+    h.total = o;
+    return h;
+}
+
+void fill_params(LinearParams& p, const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw,
+                 float eps, int mode, void* ws, int splits, bool split_ws) {
+    p.tiles = w->tiles;
+    p.rp = w->rp;
+    p.er = w->er;
+    p.ec = w->ec;
+    p.ev = w->ev;
+    p.x = x;
+    p.y = y;
+    p.lnw = lnw;
+    p.part = (float*)ws;
+    p.ssq = split_ws ? (float*)ws + (size_t)splits * t * (size_t)(nblocks(w->n) * 16) : nullptr;
+    p.N = w->n;
+    p.K = w->k;
+    p.npad = (int)(nblocks(w->n) * 16);
+    p.rbase = w->rbase;
+    p.mode = mode;
+    p.xs = mode == 2 ? 2 * w->k : w->k;
+    p.n_exc = w->n_exc;
+    p.eps = eps;
+}
+
+// the reduce pass addresses the partials with 32-bit byte offsets
+bool split_in_range(int n, int t, int splits) {
+    return splits <= 1 || (int64_t)(splits + kReduceBatchMax) * t * nblocks(n) * 16 * 4 < ((int64_t)1 << 31);
+}
+
+}  // namespace
+
 extern "C" {
 
 int rv12_abi_version(void) { return RV12_ABI_VERSION; }
@@ -346,34 +413,59 @@ int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint1
     rc = resolve_launch(w->n, w->k, t, cfg, &c);
     if (rc) return rc;
     const int splits = c.splits;
-    // the reduce pass addresses the partials with 32-bit byte offsets
-    if (splits > 1 && (int64_t)(splits + kReduceBatchMax) * t * nblocks(w->n) * 16 * 4 >= ((int64_t)1 << 31))
-        return RV12_E_CONFIG;
+    if (!split_in_range(w->n, t, splits)) return RV12_E_CONFIG;
     const size_t need = ws_bytes_for(w->n, t, splits);
     if (need && (!ws || ws_bytes < need)) return RV12_E_WORKSPACE;
     if (need && !aligned16(ws)) return RV12_E_ALIGN;
     LinearParams p;
-    p.tiles = w->tiles;
-    p.rp = w->rp;
-    p.er = w->er;
-    p.ec = w->ec;
-    p.ev = w->ev;
-    p.x = x;
-    p.y = y;
-    p.lnw = lnw;
-    p.part = (float*)ws;
-    p.ssq = need ? (float*)ws + (size_t)splits * t * (size_t)(nblocks(w->n) * 16) : nullptr;
-    p.N = w->n;
-    p.K = w->k;
-    p.npad = (int)(nblocks(w->n) * 16);
-    p.rbase = w->rbase;
-    p.mode = mode;
-    p.xs = mode == 2 ? 2 * w->k : w->k;
-    p.n_exc = w->n_exc;
-    p.eps = eps;
+    fill_params(p, w, x, y, t, lnw, eps, mode, ws, splits, need != 0);
     const int lrc = c.kernel == 1 ? launch_gemv(p, t, c.rb, c.waves, splits, (hipStream_t)stream)
                                   : launch_gemm(p, t, c.rb, c.waves, splits, (hipStream_t)stream);
     if (lrc) return RV12_E_CONFIG;
+    return launch_status();
+}
+
+size_t rv12_head_workspace_bytes(int n, int k, int t, const rv12_launch* cfg) {
+    if (!shape_ok(n, k) || t < 1 || t > 16) return 0;
+    Shape c;
+    if (resolve_launch(n, k, t, cfg, &c)) return 0;
+    return head_ws(n, t, c).total;
+}
+
+int rv12_head_argmax(const rv12_matrix* w, const float* x, int t, const uint16_t* lnw, float eps, float* logits,
+                     int64_t* ids, const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream) {
+    int rc = check_matrix(w);
+    if (rc) return rc;
+    if (!x || !ids) return RV12_E_NULL;
+    if (t < 1 || t > 16) return RV12_E_TOKENS;
+    if (!aligned16(x) || (logits && !aligned16(logits)) || ((uintptr_t)lnw & 7u) || ((uintptr_t)ids & 7u))
+        return RV12_E_ALIGN;
+    Shape c;
+    rc = resolve_launch(w->n, w->k, t, cfg, &c);
+    if (rc) return rc;
+    if (!split_in_range(w->n, t, c.splits)) return RV12_E_CONFIG;
+    const HeadWs h = head_ws(w->n, t, c);
+    if (!ws || ws_bytes < h.total) return RV12_E_WORKSPACE;
+    if (!aligned16(ws)) return RV12_E_ALIGN;
+    char* b = (char*)ws;
+    hipStream_t st = (hipStream_t)stream;
+    LinearParams p;
+    float* y = h.fused ? logits : (logits ? logits : (float*)(b + h.logits));
+    fill_params(p, w, x, y, t, lnw, eps, 0, ws, c.splits, c.splits > 1);
+    int lrc;
+    if (h.fused) {
+        p.amv = (float*)(b + h.pv);
+        p.ami = (int32_t*)(b + h.pi);
+        lrc = launch_gemv(p, t, c.rb, c.waves, 1, st);
+    } else {
+        lrc = c.kernel == 1 ? launch_gemv(p, t, c.rb, c.waves, c.splits, st)
+                            : launch_gemm(p, t, c.rb, c.waves, c.splits, st);
+    }
+    if (lrc) return RV12_E_CONFIG;
+    if (h.fused)
+        launch_pick(p.amv, p.ami, h.m, h.m, t, (float*)(b + h.tv), (int32_t*)(b + h.ti), ids, st);
+    else
+        launch_pick(y, nullptr, h.m, w->n, t, (float*)(b + h.tv), (int32_t*)(b + h.ti), ids, st);
     return launch_status();
 }
 

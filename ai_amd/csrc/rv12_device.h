@@ -101,6 +101,15 @@ __device__ __forceinline__ float rms_scale(float ssq, int K, float eps) {
     return kSsqScale * (1.0f / sqrtf(ssq / (float)K + eps * kSsqEpsScale));
 }
 
+// greedy pick order: (av, ai) replaces (bv, bi) when av is larger, or equal
+// with a smaller index; NaN counts as larger than any number (the first NaN
+// wins), as torch.argmax orders them
+__device__ __forceinline__ bool pick_beats(float av, int ai, float bv, int bi) {
+    const bool an = av != av, bn = bv != bv;
+    if (an || bn) return an && (!bn || ai < bi);
+    return av > bv || (av == bv && ai < bi);
+}
+
 // four bf16 values (bits) as floats
 __device__ __forceinline__ f32x4 bf16x4_to_f32(uint2 b) {
     return f32x4{__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xFFFF0000u), __uint_as_float(b.y << 16),

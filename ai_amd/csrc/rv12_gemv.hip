@@ -98,7 +98,8 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     const int onc = min(on, p.N - 1);
     const int obase = p.rbase[onc];  // raw: the scale exponent is formed in the epilogue
     const int32_t oe0 = p.rp[onc], oe1 = p.rp[onc + 1];
-    const float oy = p.y[(int64_t)min(otok, T - 1) * p.N + onc];
+    float oy = 0.0f;  // y is read only when accumulating (a greedy pick may pass no y)
+    if (p.mode != 0) oy = p.y[(int64_t)min(otok, T - 1) * p.N + onc];
 
     // ---- 1. activations of this thread: the chunks j < nxm hold the split's
     // columns (lanes past its end load column k_lo again, unused)
@@ -357,6 +358,7 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
         add_round(j0);
     }
 
+    float yv = 0.0f;  // the stored output
     if (oval) {
         int Po = P[0];
 #pragma unroll
@@ -368,9 +370,31 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
                 for (int w = 0; w < W; ++w) sqs += ssq[w * T + otok];
                 v *= rms_scale(sqs, p.K, p.eps);
             }
-            p.y[(int64_t)otok * p.N + on] = p.mode == 0 ? v : oy + v;
+            yv = p.mode == 0 ? v : oy + v;
+            if (p.y) p.y[(int64_t)otok * p.N + on] = yv;
         } else {
             p.part[((int64_t)sp * T + otok) * p.npad + on] = v;
+        }
+    }
+    // ---- 6. fused greedy pick (one split; the host checks): the 16 RB owners
+    // of a token are consecutive lanes of one wave, aligned to 16 RB, so an
+    // xor butterfly over them leaves their best (output, row) pair in every
+    // one; the first writes it for the second pass (launch_pick)
+    if (p.amv) {
+        float bv = oval ? yv : -__builtin_inff();
+        int bi = oval ? on : 0x7FFFFFFF;
+#pragma unroll
+        for (int o = 1; o < RB * 16; o <<= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bi, o);
+            if (pick_beats(ov, oi, bv, bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (owner && orow == 0) {
+            p.amv[(int64_t)otok * gridDim.x + blockIdx.x] = bv;
+            p.ami[(int64_t)otok * gridDim.x + blockIdx.x] = bi;
         }
     }
     if (LN && S > 1 && blockIdx.x == 0 && threadIdx.x < T) {
@@ -417,6 +441,80 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
     }
     if (RMS) v *= rms_scale(q, K, eps);
     *o = mode == 0 ? v : old + v;
+}
+
+// greedy pick over entries [c * len, min(n, (c + 1) * len)) of token
+// blockIdx.y, c = blockIdx.x: the best (value, index) pair (pick_beats order,
+// which makes the result independent of the order of combination) goes to
+// tv / ti [token][chunk], or to ids[token] when ids is given (one chunk)
+__global__ __launch_bounds__(kPickThreads) void k_pick(const float* __restrict__ v, const int32_t* __restrict__ ix,
+                                                       int64_t n, int64_t stride, int64_t len, float* tv,
+                                                       int32_t* ti, int64_t* ids) {
+    __shared__ float sv[kPickThreads / 64];
+    __shared__ int si[kPickThreads / 64];
+    const int t = blockIdx.y;
+    const int64_t lo = (int64_t)blockIdx.x * len, hi = min(n, lo + len);
+    const float* vt = v + (int64_t)t * stride;
+    const int32_t* it = ix ? ix + (int64_t)t * stride : nullptr;
+    float bv = -__builtin_inff();
+    int bi = 0x7FFFFFFF;
+    // four independent loads per thread in flight per round
+    for (int64_t i0 = lo + threadIdx.x; i0 < hi; i0 += 4 * (int64_t)kPickThreads) {
+        float a[4];
+        int ai[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = i0 + (int64_t)u * kPickThreads;
+            a[u] = i < hi ? vt[i] : -__builtin_inff();
+            ai[u] = i < hi ? (it ? it[i] : (int)i) : 0x7FFFFFFF;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (pick_beats(a[u], ai[u], bv, bi)) {
+                bv = a[u];
+                bi = ai[u];
+            }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (pick_beats(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kPickThreads / 64; ++w)
+            if (pick_beats(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+        if (ids) {
+            ids[t] = bi;
+        } else {
+            tv[(int64_t)t * gridDim.x + blockIdx.x] = bv;
+            ti[(int64_t)t * gridDim.x + blockIdx.x] = bi;
+        }
+    }
+}
+
+void launch_pick(const float* v, const int32_t* ix, int64_t n, int64_t stride, int T, float* tv, int32_t* ti,
+                 int64_t* ids, hipStream_t st) {
+    if (n <= kPickChunk) {
+        hipLaunchKernelGGL(k_pick, dim3(1, T), dim3(kPickThreads), 0, st, v, ix, n, stride, n, nullptr, nullptr, ids);
+        return;
+    }
+    const int64_t nc = pick_chunks(n);
+    hipLaunchKernelGGL(k_pick, dim3((unsigned)nc, T), dim3(kPickThreads), 0, st, v, ix, n, stride,
+                       (int64_t)kPickChunk, tv, ti, nullptr);
+    hipLaunchKernelGGL(k_pick, dim3(1, T), dim3(kPickThreads), 0, st, tv, ti, nc, nc, nc, nullptr, nullptr, ids);
 }
 
 // ------------------------------------------------------------------ launch

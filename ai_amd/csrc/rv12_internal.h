@@ -20,6 +20,8 @@ struct LinearParams {
     const int32_t* rbase;  // exponent window start of each row
     float* part;           // split partials [splits][T][npad]
     float* ssq;            // split sums of squares [splits][T]
+    float* amv = nullptr;    // fused greedy pick (vector kernel, one split): per token and
+    int32_t* ami = nullptr;  // workgroup the largest output and its row, [T][workgroups]
     int N, K, npad, mode, xs;
     int64_t n_exc;
     float eps;
@@ -115,6 +117,17 @@ int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hi
 // negative status where it rejects the shape or cfg
 int64_t launch_ws_bytes(int n, int k, int t, const rv12_launch* cfg);
 void launch_splitk_reduce(const LinearParams& p, int T, int splits, hipStream_t st);
+
+// --- greedy pick: per token the largest value of n entries and its index
+// (the smallest index on ties; NaN counts as larger than any number)
+constexpr int kPickThreads = 1024;
+constexpr int kPickChunk = 8192;  // entries one workgroup of the first stage reduces
+inline int64_t pick_chunks(int64_t n) { return (n + kPickChunk - 1) / kPickChunk; }
+// the entries of token t are v[t * stride + i] (index ix[t * stride + i], or i
+// where ix is NULL), i < n; one stage where n <= kPickChunk, else a first
+// stage into tv / ti (T * pick_chunks(n) pairs) and a second into ids
+void launch_pick(const float* v, const int32_t* ix, int64_t n, int64_t stride, int T, float* tv, int32_t* ti,
+                 int64_t* ids, hipStream_t st);
 void launch_codec_to_bf16(const rv12_codec& c, uint16_t* w, hipStream_t st);
 void launch_pack_plan(const uint16_t* w, int N, int K, int32_t* rbase, int32_t* row_exc, hipStream_t st);
 void launch_pack(const uint16_t* w, int N, int K, const int32_t* rbase, const int32_t* rp, uint32_t* tiles,

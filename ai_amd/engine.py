@@ -106,7 +106,6 @@ class Engine:
         f = lambda n: torch.zeros(BATCH, n, device=dev)
         self.xb, self.hb, self.qkvb, self.attb, self.gub = f(self.D), f(self.D), f((H + 2 * KV) * HD), f(H * HD), f(
             2 * self.FF)
-        self.logits = f(self.V)
         self.pos = torch.zeros(1, dtype=torch.long, device=dev)
         self.tok = torch.zeros(BATCH, dtype=torch.long, device=dev)
         self.nxt = torch.zeros(BATCH, dtype=torch.long, device=dev)
@@ -187,16 +186,14 @@ class Engine:
             self._gpu_layer(l, x, T, p0)
 
     def _head_row(self, x1):
-        """Greedy id of one row: the final norm fused into the 12-bit lm_head,
-        then argmax (first maximum = smallest id)."""
-        wcomp.gemvc1(x1, self.head, self.logits[:1], 0, lnw=self.norm, eps=self.eps)
-        self.nxt[:1].copy_(torch.argmax(self.logits[:1], -1))
+        """Greedy id of one row into self.nxt[0]: the final norm fused into the
+        12-bit lm_head, the pick (smallest id on ties) fused into its epilogue
+        (head.py:59-88)."""
+        wcomp.greedy(x1, self.head, 1, self.nxt, lnw=self.norm, eps=self.eps)
 
     def _head_rows(self, x, T):
-        """Greedy ids of T rows (T <= 16) into self.nxt[:T]: the final norm
-        fused into the 12-bit lm_head at T tokens, argmax per row."""
-        wcomp._linear(x, self.head, self.logits[:T], 0, T, None, None, None, self.norm, self.eps, "lm_head")
-        self.nxt[:T].copy_(torch.argmax(self.logits[:T], -1))
+        """Greedy ids of T rows (T <= 16) into self.nxt[:T]."""
+        wcomp.greedy(x, self.head, T, self.nxt, lnw=self.norm, eps=self.eps)
 
     # ---------------------------------------------------------------- passes
     def _embed(self, T):

@@ -7,6 +7,7 @@ with the same names, argument meaning and error behaviour:
     decompress(c) -> bf16[N, K]          wcomp.py:35-45
     gemvc1(x, c, y, mode, BN, w, lnw, eps)    wcomp.py:118-126
     gemvc_tc(x, c, y, mode, T, BN, w, S)      wcomp.py:233-242
+    greedy(x, c, T, out, lnw, eps, logits)    head.py:59-88 (the greedy pick, on the 12-bit head)
     CFG1, CFGT, _SK                      wcomp.py:115, 222-230
 
 plus decode_rows(c, first, last) (prefill_kernels.py:100-110) and prepare(c),
@@ -235,6 +236,7 @@ def clear_caches():
     """Drop every cached workspace, the retired ones too (the engine's
     caches are cleared with the last session, model_loader.py:385-390)."""
     _SK.clear()
+    _HEAD_WS.clear()
     _SK_RETIRED.clear()
 
 
@@ -262,6 +264,48 @@ def _linear(x, c, y, mode, T, BN, w, S, lnw, eps, where):
     rc = lib().rv12_gemm(ctypes.byref(m), _ptr(x), _ptr(y), int(T), _ptr(lnw), float(eps), int(mode),
                          ctypes.byref(cfg), _ptr(ws), ws.numel(), _stream(x.device))
     check(rc, where)
+
+
+_HEAD_WS = {}  # (N, device) -> workspace tensor of the greedy pick
+
+
+def greedy(x, c, T, out, lnw=None, eps=1e-6, logits=None):
+    """Greedy ids of T rows (1 <= T <= 16) over the 12-bit head c into the
+    int64 device tensor out[:T]: the row of the largest logit, the smallest id
+    on ties (head.py:59-88, tie rule :76-79), NaN counting as the largest
+    value.  x' as gemvc1 mode 0 (lnw: the final RMSNorm fused).  logits (fp32
+    [T, N]) also receives the logits when given.  Device-side only: no host
+    synchronisation, so it can be captured in a HIP graph once its workspace
+    exists (the first call allocates it)."""
+    _need_cuda(x, "x")
+    _need_cuda(out, "out")
+    T = int(T)
+    if not 1 <= T <= 16:
+        raise ValueError("T must be in [1, 16]")
+    N, K = int(c["N"]), int(c["K"])
+    if x.dtype != torch.float32 or not x.is_contiguous() or x.numel() < T * K:
+        raise ValueError(f"greedy: x must be contiguous float32 with {T}x{K} entries")
+    if out.dtype != torch.int64 or not out.is_contiguous() or out.numel() < T:
+        raise ValueError("greedy: out must be a contiguous int64 tensor of at least T entries")
+    if logits is not None:
+        _need_cuda(logits, "logits")
+        if logits.dtype != torch.float32 or not logits.is_contiguous() or logits.numel() < T * N:
+            raise ValueError(f"greedy: logits must be contiguous float32 with {T}x{N} entries")
+    if lnw is not None:
+        _need_cuda(lnw, "lnw")
+        if lnw.dtype != torch.bfloat16 or lnw.numel() < K or not lnw.is_contiguous():
+            raise ValueError("greedy: lnw must be a contiguous bf16 vector of K entries")
+    L = lib()
+    need = max(L.rv12_head_workspace_bytes(N, K, T, None), L.rv12_head_workspace_bytes(N, K, 16, None))
+    k = (N, K, str(x.device))
+    if k not in _HEAD_WS or _HEAD_WS[k].numel() < need:
+        if k in _HEAD_WS:
+            _SK_RETIRED.append(_HEAD_WS[k])
+        _HEAD_WS[k] = torch.empty(need, dtype=torch.uint8, device=x.device)
+    ws = _HEAD_WS[k]
+    rc = L.rv12_head_argmax(ctypes.byref(_matrix(c)), _ptr(x), T, _ptr(lnw), float(eps), _ptr(logits), _ptr(out),
+                            None, _ptr(ws), ws.numel(), _stream(x.device))
+    check(rc, "greedy")
 
 
 def gemvc1(x, c, y, mode, BN=None, w=None, lnw=None, eps=1e-6):

@@ -170,6 +170,28 @@ int rv12_gemv(const rv12_matrix* w, const float* x, float* y, const uint16_t* ln
 int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps, int mode,
               const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream);
 
+/* Greedy next-token ids over the 12-bit lm_head, 1 <= T <= 16 rows:
+ * ids[t] = the row n with the largest (W_dec . x'[t])[n], the smallest n on
+ * ties, a NaN logit counting as larger than any number (the first NaN wins).
+ * x' as rv12_gemm mode 0 (lnw: the final RMSNorm fused).  logits: NULL, or
+ * float[T][N] that also receives the logits.  With the vector kernel and no
+ * K split (the built-in launch at 1-2 tokens for a vocabulary head) the pick
+ * is fused into the linear's epilogue (a (value, row) pair per workgroup and
+ * token) and finished by a second small pass, with no atomics and, when
+ * logits is NULL, no logits written; other launches write the logits (into
+ * the workspace when logits is NULL) and reduce them in two passes.  ws:
+ * rv12_head_workspace_bytes(n, k, t, cfg) bytes, 16-byte aligned; ids: 8-byte
+ * aligned, written on the device (no host synchronisation).  Replaces the
+ * greedy branch of Head.pick (int8 bounds + exact CPU rows, smallest id on
+ * ties), ramvi/engine/ramvi_engine/generation/head.py:59-88 (tie rule
+ * :76-79) and vocab_a_k, ramvi/engine/ramvi_engine/kernels/vocab8.py:19-44. */
+int rv12_head_argmax(const rv12_matrix* w, const float* x, int t, const uint16_t* lnw, float eps, float* logits,
+                     int64_t* ids, const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream);
+
+/* Workspace bytes of rv12_head_argmax for (n, k, t, cfg) (never 0 for valid
+ * arguments; 0 where rv12_head_argmax would reject them). */
+size_t rv12_head_workspace_bytes(int n, int k, int t, const rv12_launch* cfg);
+
 /* rv12_gemm with the split-K workspace in a scratch array the library holds
  * in device memory (RV12_STATIC_SCRATCH_BYTES on every GPU it runs on, until
  * the process ends) instead of a caller-owned one: no device memory is

@@ -145,6 +145,48 @@ def test_gemm_argument_errors():
     assert call(m) == _lib.RV12_E_NULL
 
 
+def test_head_argmax_argument_errors_and_workspace():
+    """The greedy pick's checks (before any device work) and its workspace:
+    the fused pick's per-workgroup pairs at 1-2 tokens, the logits and chunk
+    pairs of the two-pass pick otherwise (each part 256-byte aligned)."""
+    from ai_amd import _lib
+    L = _lib.lib()
+    P = ctypes.c_void_p
+    x, ids, ws, lg = P(0x10000), P(0x20000), P(0x30000), P(0x50000)
+
+    def call(m, t=1, xx=x, ii=ids, logits=None, cfg=None, wsb=1 << 20):
+        return L.rv12_head_argmax(ctypes.byref(m) if m is not None else None, xx, t, None, 1e-6, logits, ii,
+                                  ctypes.byref(cfg) if cfg else None, ws, wsb, None)
+
+    assert call(None) == _lib.RV12_E_NULL
+    assert call(_mat(), ii=None) == _lib.RV12_E_NULL
+    assert call(_mat(), xx=None) == _lib.RV12_E_NULL
+    assert call(_mat(), t=0) == _lib.RV12_E_TOKENS
+    assert call(_mat(), t=17) == _lib.RV12_E_TOKENS
+    assert call(_mat(), ii=P(0x20004)) == _lib.RV12_E_ALIGN
+    assert call(_mat(), logits=P(0x50004)) == _lib.RV12_E_ALIGN
+    assert call(_mat(k=100)) == _lib.RV12_E_SHAPE
+    assert call(_mat(), cfg=_lib.Launch(3, 1, 4, 1)) == _lib.RV12_E_CONFIG
+    need = L.rv12_head_workspace_bytes(64, 256, 1, None)
+    assert need > 0 and call(_mat(), wsb=need - 1) == _lib.RV12_E_WORKSPACE
+    a = lambda b: (b + 255) // 256 * 256
+    hw = lambda n, k, t, cfg=None: L.rv12_head_workspace_bytes(n, k, t, None if cfg is None else ctypes.byref(cfg))
+    # Qwen3-8B head at one token: the vector kernel, 9496 workgroups (two row
+    # blocks each), more pairs than one pick chunk (8192): two passes
+    c = _lib.Launch()
+    assert L.rv12_launch_shape(151936, 4096, 1, None, ctypes.byref(c)) == 0 and c.kernel == 1 and c.splits == 1
+    m = (151936 // 16 + c.rb - 1) // c.rb
+    nc = (m + 8191) // 8192 if m > 8192 else 0
+    assert hw(151936, 4096, 1) == 2 * a(4 * m) + 2 * a(4 * nc)
+    # 16 tokens (MFMA): split partials, logits, 19 chunk pairs per token
+    assert L.rv12_launch_shape(151936, 4096, 16, None, ctypes.byref(c)) == 0 and c.kernel == 2
+    split = L.rv12_workspace_bytes(151936, 4096, 16, c.splits)
+    assert hw(151936, 4096, 16) == a(split) + a(16 * 151936 * 4) + 2 * a(16 * 19 * 4)
+    # a split vector launch is not fused: logits, one chunk (no pair pass)
+    assert hw(1000, 4096, 1, _lib.Launch(1, 1, 4, 4)) == a(L.rv12_workspace_bytes(1000, 4096, 1, 4)) + a(1000 * 4)
+    assert hw(64, 100, 1) == 0 and hw(64, 256, 17) == 0
+
+
 def test_pack_decode_encode_argument_errors():
     from ai_amd import _lib
     L = _lib.lib()
