@@ -249,6 +249,8 @@ def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefil
            "tok_s": round(1e3 / per_tok, 2), "ms_per_token": round(per_tok, 4), "prefill_ms": round(prefill_ms, 1),
            "prefill": prefill if prefill != "blocked" or prompt_len >= eng.prefill_min else "legacy (below the blocked minimum)",
            "load_s": round(load_s, 1), "first_ids": ids[:8]}
+    if new <= 64:
+        out["ids"] = ids
     if batch:
         ms = eng.batch_pass_ms(batch, prompt_len)
         out["batch_pass"] = {"tokens_per_pass": batch, "ms_per_pass": round(ms, 3), "tok_s": round(batch * 1e3 / ms, 2),
@@ -360,35 +362,111 @@ def run_skinny(name, reps, dev, min_bytes=1.2e9):
     return out
 
 
-def cpu_baseline(seconds=12.0):
-    """The reference CPU path's linear (matmat16: bf16 weights, fp32 sums,
-    ramvi/engine/ramvi_engine/cpu/cpu_layer.py:35-48) restated in C, on one
-    Qwen3-8B layer's four matrices at M=1, repeated for ~`seconds`."""
-    from oracle import cref
+def _cpu_threads():
+    """Threads of the CPU legs: every core this process may run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS where the host sets it (the
+    GPU hosts give each GPU a share of their cores that way)."""
+    aff = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return (min(aff, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else aff), aff, omp
+
+
+def _timed(fn, budget):
+    """(passes, seconds) of fn repeated for about `budget` seconds (at least once)."""
+    fn()  # warm: page in, thread pool up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget:
+            return n, dt
+
+
+def cpu_baseline(dev, gpu_ids_0_6b=None, budget=0.7):
+    """The reference's CPU paths restated in C (oracle/), timed on this host:
+      gemv_12bit  the 12-bit block decode + dot product of the native CPU path
+                  (native/qmm.cpp:195-212: decode a 256-chunk of a row to fp32,
+                  dot it with every token), from the reference codec's own
+                  arrays, per Qwen3-8B shape at M=1;
+      matmat16    the CPU layer's bf16 linear (cpu/cpu_layer.py:35-48), per shape;
+      e2e_qwen3_0_6b  config 1 end to end: CpuLayer.__call__ over 28 layers +
+                  the exact greedy head (cpu/cpu_layer.py:155-175,
+                  generation/head.py:19-26), 128-token prompt, 64 new tokens.
+    value: the gemv_12bit leg over one Qwen3-8B layer's qkv / o / gu / down
+    (with their RMS and silu prologues), compressed GB/s, the same bytes as the
+    GPU line's value."""
+    from ai_amd import wcomp
+    from ai_amd.model import QWEN3, RandomCkpt
+    from oracle import cpu_qwen3, cref
     if not os.path.exists(cref.LIB_PATH):
         cref.build()
-    threads = min(16, os.cpu_count() or 1)
+    threads, aff, omp = _cpu_threads()
+    gen = torch.Generator().manual_seed(7)
     rng = np.random.default_rng(0)
-    mats, xs = [], []
+
+    def host_codec(w):
+        c = wcomp.compress(w)
+        return {k: (c[k].cpu().numpy() if torch.is_tensor(c[k]) else c[k]) for k in
+                ("m8", "e4", "base", "rp", "er", "ec", "ev", "N", "K", "CH")}
+
+    legs = {"gemv_12bit": {}, "matmat16": {}}
+    for name, (N, K, _) in SWEEP.items():
+        w = make_matrix(N, K, gen, dev)
+        c = host_codec(w)
+        wb = w.view(torch.int16).cpu().numpy().view(np.uint16)
+        del w
+        # distinct copies of > 1 GB in all, so that no pass is served from the
+        # host's last-level cache
+        copies = max(1, -(-(1 << 30) // (2 * N * K)))
+        cs = [c] + [{k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in c.items()} for _ in range(copies - 1)]
+        wbs = [wb] + [wb.copy() for _ in range(copies - 1)]
+        x = rng.standard_normal((1, K)).astype(np.float32)
+        y = np.zeros((1, N), np.float32)
+        cb = int(1.5 * N * K) + 12 * int(c["er"].size) + 4 * (N + 1)
+        n, dt = _timed(lambda: [cref.gemv_12bit(ci, x, y, 0, threads=threads) for ci in cs], budget)
+        n *= copies
+        legs["gemv_12bit"][name] = {"us": round(dt / n * 1e6, 1), "comp_GBs": round(cb * n / dt / 1e9, 2),
+                                    "copies": copies}
+        n, dt = _timed(lambda: [cref.gemv_bf16(wi, x, y, add=False, threads=threads) for wi in wbs], budget)
+        n *= copies
+        legs["matmat16"][name] = {"us": round(dt / n * 1e6, 1), "bf16_GBs": round(2 * N * K * n / dt / 1e9, 2),
+                                  "comp_equiv_GBs": round(cb * n / dt / 1e9, 2), "copies": copies}
+        del c, wb, cs, wbs
+    # value: one Qwen3-8B layer through the 12-bit leg, prologues included
+    layer, cbytes = [], 0
     for name, N, K, mode, rms in LAYER:
-        w = torch.randn(N, K, generator=torch.Generator().manual_seed(N + K)).mul_(0.02).bfloat16()
-        mats.append(w.view(torch.int16).numpy().view(np.uint16))
-        xs.append(rng.standard_normal((1, K)).astype(np.float32))
-    ys = [np.zeros((1, m.shape[0]), np.float32) for m in mats]
-    nbytes = sum(int(1.5 * m.shape[0] * m.shape[1]) for m in mats)
-    for m, x, y in zip(mats, xs, ys):   # warm (page in)
-        cref.gemv_bf16(m, x, y, add=False, threads=threads)
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        for m, x, y in zip(mats, xs, ys):
-            cref.gemv_bf16(m, x, y, add=False, threads=threads)
-        reps += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(nbytes * reps / dt / 1e9, 3), "unit": "GB/s (12-bit-equivalent bytes)",
-            "cores": threads, "kind": "port",
-            "sample": f"{reps} passes over one Qwen3-8B layer's qkv/o/gu/down at M=1 in {dt:.1f} s "
-                      "(matmat16 restatement: bf16 weights, fp32 sums, OpenMP)",
-            "cpu_model": _cpu_model()}
+        c = host_codec(make_matrix(N, K, gen, dev))
+        X = rng.standard_normal((1, 2 * K if mode == 2 else K)).astype(np.float32)
+        lnw = np.ones(K, np.uint16) * 0x3F80 if rms else None
+        layer.append((c, X, np.zeros((1, N), np.float32), mode, lnw))
+        cbytes += int(1.5 * N * K) + 12 * int(c["er"].size) + 4 * (N + 1)
+
+    def one_layer():
+        for c, X, Y, mode, lnw in layer:
+            cref.gemv_12bit(c, X, Y, mode, lnw=lnw, threads=threads)
+
+    n, dt = _timed(one_layer, 3.0)  # 0.33 GB of codec arrays per pass: beyond the host caches
+    value = cbytes * n / dt / 1e9
+    del layer
+    # config 1 end to end (weights drawn on the GPU, as the GPU engine's)
+    ck = RandomCkpt(QWEN3["0.6b"], seed=0)
+    m = cpu_qwen3.load(ck, dev)
+    prompt = [int(t) for t in np.random.default_rng(0).integers(0, ck.V, 128)]
+    ids, pre_s, dec_s = cpu_qwen3.generate(m, prompt, 64, threads=threads)
+    e2e = {"model": "qwen3-0.6b random init", "prompt": 128, "new_tokens": 64, "kv_cache": "fp32",
+           "decode_tok_s": round(63 / dec_s, 2), "ms_per_token": round(dec_s / 63 * 1e3, 2),
+           "prefill_s": round(pre_s, 2), "first_ids": ids[:8]}
+    if gpu_ids_0_6b:
+        e2e["ids_equal_to_gpu_engine"] = sum(a == b for a, b in zip(ids, gpu_ids_0_6b))
+        e2e["gpu_engine_kv_cache"] = "bf16"
+    del m
+    return {"value": round(value, 3), "unit": "GB/s (compressed bytes)", "cores": threads, "kind": "port",
+            "sample": f"{n} passes over one Qwen3-8B layer's qkv/o/gu/down at M=1 (12-bit block decode + dot, "
+                      f"RMS and silu prologues) in {dt:.1f} s; per-shape legs {budget} s each; config-1 decode "
+                      f"of 64 tokens",
+            "nproc": os.cpu_count(), "affinity_cores": aff, "omp_num_threads": omp, "cpu_model": _cpu_model(),
+            "legs": legs, "e2e_qwen3_0_6b": e2e}
 
 
 def _cpu_model():
@@ -496,7 +574,12 @@ def main():
     hbm = measure_hbm(dev)
     print(f"# measured HBM: copy {hbm['copy_GBs']:.0f} GB/s, sum {hbm['sum_read_GBs']:.0f} GB/s read, bf16 mv "
           f"{hbm['bf16_gemv_read_GBs']:.0f} GB/s read", file=sys.stderr, flush=True)
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(dev, e2e06.get("ids") if e2e06 else None)
+        print(f"# cpu ({cpu['cores']} threads of {cpu['nproc']}, {cpu['cpu_model']}): 8B layer 12-bit "
+              f"{cpu['value']} GB/s; " + ", ".join(f"{k} {v['comp_GBs']}" for k, v in cpu["legs"]["gemv_12bit"].items())
+              + f"; 0.6B decode {cpu['e2e_qwen3_0_6b']['decode_tok_s']} tok/s", file=sys.stderr, flush=True)
     line = {
         "metric": "Qwen3-8B bs1 decode tok/s; fused GEMV effective HBM GB/s vs peak",
         "value": round(value, 2),

@@ -12,7 +12,12 @@
  *  rvo_gemv_12bit    the same product straight from the 12-bit codec: decode one
  *                    CH-chunk of a row to fp32, dot it, then add the row's
  *                    exceptions (the order of wcomp.py:80-108), with the MODE /
- *                    RMS prologue of wcomp.py:57-86.
+ *                    RMS prologue of wcomp.py:57-86 (the block decode + dot of
+ *                    the reference's native CPU path, native/qmm.cpp:195-212).
+ *  rvo_rms_rows, rvo_qk_rope_attn, rvo_silu_mul
+ *                    the reference CPU layer's other steps
+ *                    (cpu/cpu_layer.py:51-59, 62-131, 134-140): with
+ *                    rvo_gemv_bf16 they make CpuLayer.__call__ (:155-175).
  */
 #include <math.h>
 #include <stdint.h>
@@ -142,12 +147,14 @@ int rvo_gemv_12bit(const uint8_t* m8, const uint8_t* e4, int base, const int32_t
     if (!xp) return -3;
     prologue(X, xs, K, T, mode, lnw, eps, xp);
     int half = CH / 2;
+    const uint32_t ub = (uint32_t)base;
 #ifdef _OPENMP
     if (threads > 0) omp_set_num_threads(threads);
 #pragma omp parallel
 #endif
     {
-        float* wrow = (float*)malloc(sizeof(float) * (size_t)CH);
+        /* the decoded chunk as float bits; both loops below vectorise */
+        uint32_t* wb = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)CH);
 #ifdef _OPENMP
 #pragma omp for schedule(static)
 #endif
@@ -156,20 +163,25 @@ int rvo_gemv_12bit(const uint8_t* m8, const uint8_t* e4, int base, const int32_t
             const uint8_t* mr = m8 + (int64_t)n * K;
             const uint8_t* er = e4 + (int64_t)n * (K / 2);
             for (int c = 0; c < K / CH; c++) {
+                const uint8_t* eb = er + (int64_t)c * half;
+                const uint8_t* mb = mr + (int64_t)c * CH;
                 for (int i = 0; i < half; i++) {
-                    uint8_t byte = er[(int64_t)c * half + i];
-                    int c0 = byte & 15, c1 = byte >> 4;
-                    uint32_t m0 = mr[(int64_t)c * CH + i], m1 = mr[(int64_t)c * CH + half + i];
-                    uint32_t b0 = c0 == 15 ? 0u : (((m0 >> 7) << 31) | ((uint32_t)(c0 + base) << 23) | ((m0 & 0x7F) << 16));
-                    uint32_t b1 = c1 == 15 ? 0u : (((m1 >> 7) << 31) | ((uint32_t)(c1 + base) << 23) | ((m1 & 0x7F) << 16));
-                    memcpy(wrow + i, &b0, 4);
-                    memcpy(wrow + half + i, &b1, 4);
+                    const uint32_t byte = eb[i], c0 = byte & 15u, c1 = byte >> 4;
+                    const uint32_t m0 = mb[i], m1 = mb[half + i];
+                    const uint32_t b0 = ((m0 >> 7) << 31) | ((c0 + ub) << 23) | ((m0 & 0x7Fu) << 16);
+                    const uint32_t b1 = ((m1 >> 7) << 31) | ((c1 + ub) << 23) | ((m1 & 0x7Fu) << 16);
+                    wb[i] = c0 == 15u ? 0u : b0;
+                    wb[half + i] = c1 == 15u ? 0u : b1;
                 }
                 for (int t = 0; t < T; t++) {
                     const float* x = xp + (int64_t)t * K + (int64_t)c * CH;
                     float s = 0.0f;
 #pragma omp simd reduction(+ : s)
-                    for (int i = 0; i < CH; i++) s += wrow[i] * x[i];
+                    for (int i = 0; i < CH; i++) {
+                        float w;
+                        memcpy(&w, wb + i, 4);
+                        s += w * x[i];
+                    }
                     acc[t] += s;
                 }
             }
@@ -180,8 +192,103 @@ int rvo_gemv_12bit(const uint8_t* m8, const uint8_t* e4, int base, const int32_t
                 else Y[(int64_t)t * N + n] += acc[t];
             }
         }
-        free(wrow);
+        free(wb);
     }
     free(xp);
     return 0;
+}
+
+/* rms_rows (cpu_layer.py:51-59): out[t] = w * (X[t] / sqrt(mean(X[t]^2) + eps)),
+ * sequential fp32 sums */
+void rvo_rms_rows(const float* X, const float* w, float* out, int T, int D, float eps) {
+    for (int t = 0; t < T; t++) {
+        const float* x = X + (int64_t)t * D;
+        float s = 0.0f;
+        for (int i = 0; i < D; i++) s += x[i] * x[i];
+        const float r = 1.0f / sqrtf(s / (float)D + eps);
+        for (int i = 0; i < D; i++) out[(int64_t)t * D + i] = w[i] * (x[i] * r);
+    }
+}
+
+/* head RMSNorm + rotate-half RoPE at position p of one head (HD values at
+ * src, weights nw) into dst (cpu_layer.py:70-83, 95-105) */
+static void norm_rope(const float* src, const float* nw, const float* inv, int p, int HD, float eps, float* dst) {
+    const int half = HD / 2;
+    float s = 0.0f;
+    for (int d = 0; d < HD; d++) s += src[d] * src[d];
+    const float r = 1.0f / sqrtf(s / (float)HD + eps);
+    for (int d = 0; d < half; d++) {
+        const float ang = (float)p * inv[d];
+        const float c = cosf(ang), sn = sinf(ang);
+        const float a = nw[d] * (src[d] * r), b = nw[d + half] * (src[d + half] * r);
+        dst[d] = a * c - b * sn;
+        dst[d + half] = b * c + a * sn;
+    }
+}
+
+/* qk_rope_attn (cpu_layer.py:62-131): q/k head norms and RoPE, k and v of the
+ * T rows into the float32 caches Kc / Vc [KV][maxt][HD] at positions
+ * pos0..pos0+T-1, then per (row, head) the causal softmax attention over
+ * positions 0..pos0+t (max-subtracted exponentials, fp32 sums) into out
+ * [T][H*HD].  QKV rows hold q (H heads), k (KV), v (KV). */
+void rvo_qk_rope_attn(const float* QKV, const float* qn, const float* kn, const float* inv, int pos0, float* Kc,
+                      float* Vc, int maxt, float* out, int T, int H, int KV, int HD, float eps, int threads) {
+    const int G = H / KV, W = (H + 2 * KV) * HD;
+    for (int t = 0; t < T; t++) {
+        const int p = pos0 + t;
+        const float* row = QKV + (int64_t)t * W;
+        for (int g = 0; g < KV; g++) {
+            norm_rope(row + (H + g) * HD, kn, inv, p, HD, eps, Kc + ((int64_t)g * maxt + p) * HD);
+            memcpy(Vc + ((int64_t)g * maxt + p) * HD, row + (H + KV + g) * HD, sizeof(float) * HD);
+        }
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel
+#endif
+    {
+        float* q = (float*)malloc(sizeof(float) * HD);
+        float* sc = (float*)malloc(sizeof(float) * (pos0 + T));
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int th = 0; th < T * H; th++) {
+            const int t = th / H, h = th % H, g = h / G, p = pos0 + t, n = p + 1;
+            norm_rope(QKV + (int64_t)t * W + h * HD, qn, inv, p, HD, eps, q);
+            float m = -1e30f;
+            for (int j = 0; j < n; j++) {
+                const float* k = Kc + ((int64_t)g * maxt + j) * HD;
+                float s = 0.0f;
+                for (int d = 0; d < HD; d++) s += q[d] * k[d];
+                s *= scale;
+                sc[j] = s;
+                if (s > m) m = s;
+            }
+            float l = 0.0f;
+            for (int j = 0; j < n; j++) {
+                sc[j] = expf(sc[j] - m);
+                l += sc[j];
+            }
+            float* o = out + (int64_t)t * H * HD + h * HD;
+            for (int d = 0; d < HD; d++) o[d] = 0.0f;
+            for (int j = 0; j < n; j++) {
+                const float w = sc[j] / l;
+                const float* v = Vc + ((int64_t)g * maxt + j) * HD;
+                for (int d = 0; d < HD; d++) o[d] += w * v[d];
+            }
+        }
+        free(q);
+        free(sc);
+    }
+}
+
+/* silu_mul (cpu_layer.py:134-140): M[t, i] = g / (1 + exp(-g)) * u, g = GU[t, i],
+ * u = GU[t, FF + i] */
+void rvo_silu_mul(const float* GU, float* M, int T, int FF) {
+    for (int t = 0; t < T; t++)
+        for (int i = 0; i < FF; i++) {
+            const float g = GU[(int64_t)t * 2 * FF + i];
+            M[(int64_t)t * FF + i] = g / (1.0f + expf(-g)) * GU[(int64_t)t * 2 * FF + FF + i];
+        }
 }

@@ -34,6 +34,12 @@ def lib():
         L.rvo_gemv_bf16.argtypes = [P, P, P, I, I, I, I, I]
         L.rvo_gemv_12bit.restype = I
         L.rvo_gemv_12bit.argtypes = [P, P, I, P, P, P, P, P, P, F, I, I, I, I, I, I]
+        L.rvo_rms_rows.restype = None
+        L.rvo_rms_rows.argtypes = [P, P, P, I, I, F]
+        L.rvo_qk_rope_attn.restype = None
+        L.rvo_qk_rope_attn.argtypes = [P, P, P, P, I, P, P, I, P, I, I, I, I, F, I]
+        L.rvo_silu_mul.restype = None
+        L.rvo_silu_mul.argtypes = [P, P, I, I]
         _lib = L
     return _lib
 
@@ -90,3 +96,20 @@ def gemv_12bit(c, X, Y, mode, lnw=None, eps=1e-6, threads=0):
                               c["CH"], T, mode, threads)
     if rc:
         raise ValueError(f"rvo_gemv_12bit: {rc}")
+
+
+def rms_rows(X, w, out, eps):
+    """rms_rows restatement (cpu_layer.py:51-59)."""
+    T, D = X.shape
+    lib().rvo_rms_rows(_p(X), _p(w), _p(out), T, D, eps)
+
+
+def qk_rope_attn(QKV, qn, kn, inv, pos0, Kc, Vc, out, H, KV, HD, eps, threads=0):
+    """qk_rope_attn restatement (cpu_layer.py:62-131), float32 caches [KV, maxt, HD]."""
+    lib().rvo_qk_rope_attn(_p(QKV), _p(qn), _p(kn), _p(inv), int(pos0), _p(Kc), _p(Vc), Kc.shape[1], _p(out),
+                           QKV.shape[0], H, KV, HD, eps, threads)
+
+
+def silu_mul(GU, M, FF):
+    """silu_mul restatement (cpu_layer.py:134-140)."""
+    lib().rvo_silu_mul(_p(GU), _p(M), GU.shape[0], FF)

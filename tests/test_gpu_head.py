@@ -170,3 +170,26 @@ def test_vocabulary_head_full_size():
         assert np.array_equal(ids, np.argmax(lg, 1))
     del cg
     torch.cuda.empty_cache()
+
+
+def test_head_class_greedy_and_sampling():
+    """ai_amd.head.Head with the reference's interface: greedy picks equal
+    wcomp.greedy's; sampling at a tiny temperature picks the greedy id where
+    there is no tie, and top_p = 0 keeps only the most likely id."""
+    from ai_amd.head import Head
+    N, K = 4000, 256
+    bits = _matrix(N, K, 8, tied=(30, 3000))
+    hd = Head(bits, TM=16)
+    row = codec.bf16_to_f32(bits[30])
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((4, K)).astype(np.float32)
+    X[0] = np.sign(row)
+    h = torch.from_numpy(X).cuda()
+    ids = hd.pick(h, 4)
+    assert ids[0] == 30
+    want, _ = _pick(hd.c, X)
+    assert ids == want.tolist()
+    # token 0 ties rows 30 and 3000: sampling may take either, top_p = 0 keeps
+    # the first of the stable order (the smaller id)
+    assert hd.pick(h, 4, temperature=1e-6, rng=np.random.default_rng(0))[1:] == ids[1:]
+    assert hd.pick(h, 4, temperature=1.0, top_p=0.0, rng=np.random.default_rng(0)) == ids
