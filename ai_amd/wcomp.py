@@ -14,12 +14,14 @@ plus decode_rows(c, first, last) (prefill_kernels.py:100-110) and prepare(c),
 which re-tiles a dict built elsewhere (the reference's own compress, a file)
 for the kernels.  Every call goes through librv12.so; there is no other path.
 
-The dict keeps the reference keys m8, e4, base, rp, er, ec, ev, N, K, CH (bit
-for bit what the reference's compress builds) and adds "q16", the packed form
-the kernels read: "tiles" (the weights in the Q16 layout, 1.5 bytes per
-weight), "rbase" (one exponent window per row) and that layout's own
-exception list "rp"/"er"/"ec"/"ev".  `compact(c)` drops m8/e4 once only the
-kernels read the dict.
+The dict (Codec12) stores the reference keys base, rp, er, ec, ev, N, K, CH
+(bit for bit what the reference's compress builds) and the packed form the
+kernels read as top-level tensors q16_tiles (the weights in the Q16 layout,
+1.5 bytes per weight), q16_rbase (one exponent window per row) and that
+layout's own exception list q16_rp / q16_er / q16_ec / q16_ev; the
+reference's m8 / e4 are derived on request (c["m8"]), so the device holds
+about 1.5 bytes per weight and the reference's _pack / _unpack stream exactly
+the kernels' bytes.
 Launch parameters keep the reference meaning: BN = rows per workgroup
 (rounded up to 16, 32 or 64), w = waves per workgroup, S = K splits.
 """
@@ -56,9 +58,62 @@ def _window_base(hist):
     return int((cs[15:] - cs[:-15]).argmax())
 
 
+PACKED = ("q16_tiles", "q16_rbase", "q16_rp", "q16_er", "q16_ec", "q16_ev")
+
+
+class Codec12(dict):
+    """The dict compress() returns.  Stored: the reference keys base, rp, er,
+    ec, ev, N, K, CH (bit for bit the reference's) and the kernels' packed
+    form as top-level tensors q16_tiles, q16_rbase, q16_rp, q16_er, q16_ec,
+    q16_ev, about 1.5 bytes per weight in all.  The reference's m8 and e4 (1.5
+    bytes per weight more) are not kept: c["m8"] and c["e4"] re-derive them
+    on the GPU from the packed form, bit for bit what the reference compress
+    builds (keep_codec() stores them).  So the reference Engine's budget of
+    about 1.5 bytes per weight holds (planning/plan.py:38), and its
+    _pack / _unpack (core/engine.py:34-56), which carry the top-level tensors,
+    carry exactly what the kernels read."""
+
+    def __missing__(self, k):
+        if k in ("m8", "e4") and "q16_tiles" in self:
+            return _reference_arrays(self)[0 if k == "m8" else 1]
+        raise KeyError(k)
+
+    def keep_codec(self):
+        """Store m8 / e4 in the dict (the reference's full codec)."""
+        m8, e4 = _reference_arrays(self)
+        self["m8"], self["e4"] = m8, e4
+        return self
+
+
+def _reference_arrays(c):
+    """(m8, e4) of the reference codec from the packed form: the exact bf16
+    weights, encoded again with the stored base (the same encoder compress
+    runs), on the dict's device."""
+    home = c["q16_tiles"].device
+    dev = home if home.type == "cuda" else torch.device("cuda")
+    g = c if home.type == "cuda" else {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in c.items()}
+    W = decode_rows(g, 0, int(c["N"]), torch.bfloat16)
+    N, K, CH = int(c["N"]), int(c["K"]), int(c["CH"])
+    m8 = torch.empty(N, K, dtype=torch.uint8, device=dev)
+    e4 = torch.empty(N, K // 2, dtype=torch.uint8, device=dev)
+    row_exc = torch.empty(N, dtype=torch.int32, device=dev)
+    check(lib().rv12_encode(_ptr(W), N, K, CH, int(c["base"]), _ptr(m8), _ptr(e4), _ptr(row_exc), _stream(dev)),
+          "compress")
+    return m8.to(home), e4.to(home)
+
+
 def compress(W, CH=256):
-    """W [N, K] bf16 on the GPU -> codec dict (wcomp.py:13-32), plus "q16"."""
-    _need_cuda(W, "W")
+    """W [N, K] bf16 -> codec dict (wcomp.py:13-32): the reference keys and the
+    packed form (Codec12).  W on the GPU, or on the CPU as the reference
+    allows: the work then runs on the current GPU and the dict's tensors are
+    returned on the CPU (a GPU is required either way)."""
+    if not torch.is_tensor(W):
+        raise ValueError("W must be a tensor")
+    home = W.device
+    if home.type != "cuda":
+        if not torch.cuda.is_available():
+            raise RuntimeError("compress: librv12 runs on the GPU and none is available")
+        W = W.to("cuda")
     if W.dtype != torch.bfloat16 or W.dim() != 2:
         raise ValueError("W must be a 2-D bfloat16 tensor")
     N, K = W.shape
@@ -84,15 +139,23 @@ def compress(W, CH=256):
     ev = torch.empty(E, dtype=torch.float32, device=dev)
     if E:
         check(L.rv12_encode_exc(_ptr(W), N, K, base, _ptr(rp), _ptr(er), _ptr(ec), _ptr(ev), st), "compress")
-    c = {"m8": m8, "e4": e4, "base": base, "rp": rp, "er": er, "ec": ec, "ev": ev, "N": N, "K": K, "CH": CH}
+    c = Codec12(base=base, rp=rp, er=er, ec=ec, ev=ev, N=N, K=K, CH=CH)
     if K % 32 == 0 and CH % 16 == 0:
-        c["q16"] = pack(W)
+        c.update(pack(W))
+        del m8, e4
+    else:  # no packed form for this K: the dict keeps the reference arrays
+        c["m8"], c["e4"] = m8, e4
+    if home.type != "cuda":
+        for k, v in list(c.items()):
+            if torch.is_tensor(v):
+                c[k] = v.to(home)
     return c
 
 
 def pack(W):
-    """bf16 W [N, K] on the GPU -> the kernels' packed form: Q16 tiles with one
-    exponent window per row and that layout's own exception list."""
+    """bf16 W [N, K] on the GPU -> the kernels' packed form (keys q16_*): Q16
+    tiles with one exponent window per row and that layout's own exception
+    list."""
     N, K = W.shape
     dev = W.device
     L = lib()
@@ -112,11 +175,12 @@ def pack(W):
     ev = torch.empty(E, dtype=torch.float32, device=dev)
     check(L.rv12_pack(_ptr(W), N, K, _ptr(rbase), _ptr(rp), E, _ptr(tiles), nbytes, _ptr(er), _ptr(ec), _ptr(ev),
                       st), "pack")
-    return {"tiles": tiles, "rbase": rbase, "rp": rp, "er": er, "ec": ec, "ev": ev}
+    return {"q16_tiles": tiles, "q16_rbase": rbase, "q16_rp": rp, "q16_er": er, "q16_ec": ec, "q16_ev": ev}
 
 
 def to_bf16(c):
-    """The bf16 matrix a codec dict encodes, bit for bit (NaN payloads kept)."""
+    """The bf16 matrix a reference codec dict (m8, e4, ...) encodes, bit for
+    bit (NaN payloads kept)."""
     dev = c["m8"].device
     N, K = int(c["N"]), int(c["K"])
     W = torch.empty(N, K, dtype=torch.bfloat16, device=dev)
@@ -127,9 +191,17 @@ def to_bf16(c):
 
 
 def prepare(c, device=None):
-    """Pack a dict built elsewhere (the reference's own compress, a file) for
-    the kernels, moving CPU / numpy arrays to the GPU first.  Idempotent."""
-    if "q16" in c:
+    """Ready a dict for the kernels, in place: one built elsewhere (the
+    reference's own compress, a file; numpy or CPU arrays) is moved to the GPU
+    and packed; a packed one on the CPU (compress of a CPU tensor, the
+    reference's _unpack of a host image) has its tensors moved to the GPU.
+    Idempotent."""
+    if "q16_tiles" in c:
+        if not c["q16_tiles"].is_cuda:
+            dev = torch.device(device) if device is not None else torch.device("cuda")
+            for k, v in list(c.items()):
+                if torch.is_tensor(v):
+                    c[k] = v.to(dev)
         return c
     dev = torch.device(device) if device is not None else (
         c["m8"].device if torch.is_tensor(c["m8"]) and c["m8"].is_cuda else torch.device("cuda"))
@@ -139,31 +211,30 @@ def prepare(c, device=None):
         if not torch.is_tensor(v):
             v = torch.as_tensor(v)
         c[k] = v.to(device=dev, dtype=dt).contiguous()
-    c["q16"] = pack(to_bf16(c))
+    c.update(pack(to_bf16(c)))
     return c
 
 
 def compact(c):
-    """Drop m8/e4 (the kernels read only the packed form)."""
+    """Drop stored m8 / e4 (the kernels read only the packed form)."""
     prepare(c)
-    c.pop("m8", None)
-    c.pop("e4", None)
+    dict.pop(c, "m8", None)
+    dict.pop(c, "e4", None)
     return c
 
 
 def _matrix(c):
-    if "q16" not in c:
+    if "q16_tiles" not in c or not c["q16_tiles"].is_cuda:
         prepare(c)
-    q = c["q16"]
-    return Matrix(_ptr(q["tiles"]), _ptr(q["rbase"]), _ptr(q["rp"]), _ptr(q["er"]), _ptr(q["ec"]), _ptr(q["ev"]),
-                  int(c["N"]), int(c["K"]), int(q["er"].numel()))
+    return Matrix(_ptr(c["q16_tiles"]), _ptr(c["q16_rbase"]), _ptr(c["q16_rp"]), _ptr(c["q16_er"]),
+                  _ptr(c["q16_ec"]), _ptr(c["q16_ev"]), int(c["N"]), int(c["K"]), int(c["q16_er"].numel()))
 
 
 def decode_rows(c, first, last, dtype=torch.float32):
     """Rows [first, last) decoded exactly: float32 (as prefill_kernels.decode_rows)
     or bfloat16 (the original bit patterns, NaN payloads included)."""
     m = _matrix(c)
-    dev = c["q16"]["tiles"].device
+    dev = c["q16_tiles"].device
     out = torch.empty((last - first, int(c["K"])), dtype=dtype, device=dev)
     f32 = 1 if dtype == torch.float32 else 0
     if dtype not in (torch.float32, torch.bfloat16):

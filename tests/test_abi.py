@@ -236,11 +236,18 @@ def test_static_scratch_entry_rejects_oversized_workspace():
     assert L.rv12_gemm_static(ctypes.byref(m), p, p, 17, None, 1e-6, 0, None, None) == _lib.RV12_E_TOKENS
 
 
-def test_python_mirror_rejects_cpu_tensors():
+def test_python_mirror_fails_loudly_without_a_gpu():
+    """compress takes a CPU tensor as the reference's does, but runs on the
+    GPU: with none it raises (there is no CPU path); the linears want device
+    tensors."""
     import torch
     from ai_amd import wcomp
-    with pytest.raises(ValueError):
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(RuntimeError):
         wcomp.compress(torch.zeros(4, 256, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        wcomp.gemvc1(torch.zeros(256), {"N": 4, "K": 256}, torch.zeros(4), 0)
 
 
 def test_attention_argument_errors():

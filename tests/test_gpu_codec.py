@@ -59,11 +59,11 @@ def test_pack_matches_layout_model(golden):
         print("case", name, flush=True)
         t, rb, rp, er, ec, ev = q.pack(g["w"])
         got = wcomp.pack(_w(g["w"]))
-        assert np.array_equal(got["tiles"].cpu().numpy().view(np.uint32), t.reshape(-1)), name
-        assert np.array_equal(got["rbase"].cpu().numpy(), rb), name
-        for k, v in (("rp", rp), ("er", er), ("ec", ec)):
+        assert np.array_equal(got["q16_tiles"].cpu().numpy().view(np.uint32), t.reshape(-1)), name
+        assert np.array_equal(got["q16_rbase"].cpu().numpy(), rb), name
+        for k, v in (("q16_rp", rp), ("q16_er", er), ("q16_ec", ec)):
             assert np.array_equal(got[k].cpu().numpy(), v), (name, k)
-        assert np.array_equal(got["ev"].cpu().numpy().view(np.uint32), ev.view(np.uint32)), name
+        assert np.array_equal(got["q16_ev"].cpu().numpy().view(np.uint32), ev.view(np.uint32)), name
 
 
 def test_decode_rows_ranges_and_f32(golden):
@@ -116,7 +116,7 @@ def test_outlier_rows_stay_out_of_the_packed_exception_list():
     w = w.bfloat16()
     c = wcomp.compress(w)
     ref_rows = torch.bincount(c["er"].long(), minlength=N)
-    own_rows = torch.diff(c["q16"]["rp"].long())
+    own_rows = torch.diff(c["q16_rp"].long())
     assert int(ref_rows[rows].min()) > 500
     assert int(own_rows[rows].max()) < 20
     assert torch.equal(wcomp.decompress(c).view(torch.int16), w.view(torch.int16))
