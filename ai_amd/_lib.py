@@ -3,7 +3,9 @@
 torch is imported first so that the library binds to the HIP runtime torch
 already loaded (both carry the soname libamdhip64.so.7): device pointers and
 streams from torch are then valid in the library.  Loading fails loudly when
-the library is missing; there is no fallback path.
+the library is missing or does not match its build manifest (the sha256 of
+the binary and of every source, the flags, the ABI version: ai_amd/build.py);
+there is no fallback path.
 """
 import ctypes
 import os
@@ -68,6 +70,10 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"librv12.so not built at {LIB_PATH}: run `python -m ai_amd.build`")
+        from . import build
+        bad = build.manifest_problem()
+        if bad:
+            raise RuntimeError(f"librv12.so does not match its build manifest ({bad}): run `python -m ai_amd.build`")
         L = ctypes.CDLL(LIB_PATH)
         P, I, I64, F, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
         L.rv12_abi_version.restype = I

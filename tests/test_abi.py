@@ -278,3 +278,21 @@ def test_attention_argument_errors():
     assert call(A(), pos=None) == _lib.RV12_E_NULL
     assert call(A(), ws=0) == _lib.RV12_E_WORKSPACE
     assert call(A(), ws_bytes=1000) == _lib.RV12_E_WORKSPACE
+
+
+def test_build_manifest_checked_at_load(monkeypatch):
+    """librv12.so loads only while it matches its manifest: the binary's and
+    every source's sha256, the code-generation flags and the ABI version (as
+    the reference's native/write_manifest.py + cpu/gcpu.py:121-160)."""
+    import json
+    from ai_amd import build
+    assert build.manifest_problem() is None
+    m = json.load(open(build.MANIFEST))
+    assert set(m["sources"]) == {f"ai_amd/csrc/{n}" for n in build.SOURCES + build.HEADERS} | {"include/rv12.h"}
+    assert "-packed-fp32-ops" in m["flags"] and "--offload-arch=gfx950" in m["flags"]
+    changed = dict(build.inputs(), **{"ai_amd/csrc/rv12_gemv.hip": "0" * 64})
+    monkeypatch.setattr(build, "inputs", lambda: changed)
+    assert "sources changed" in build.manifest_problem()
+    monkeypatch.undo()
+    monkeypatch.setattr(build, "CODEGEN", build.CODEGEN[:-4])
+    assert "other flags" in build.manifest_problem()
