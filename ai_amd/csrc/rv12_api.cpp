@@ -232,9 +232,9 @@ namespace {
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // Workspace of a greedy pick (rv12_head_argmax), each part 256-byte aligned:
-// the linear's split partials, then either the fused pick's per-workgroup
-// pairs (vector kernel, one split) or the logits, then the first pick
-// stage's pairs where more than one chunk is reduced.
+// the linear's split partials, the logits, the fused pick's per-workgroup
+// pairs (vector kernel, one split), then the first pick stage's pairs where
+// more than one chunk is reduced.
 struct HeadWs {
     bool fused;
     int64_t m;  // entries the pick reduces per token
@@ -245,6 +245,10 @@ HeadWs head_ws(int n, int t, const Shape& c) {
     HeadWs h{};
     h.fused = c.kernel == 1 && c.splits == 1;
     size_t o = align256(ws_bytes_for(n, t, c.splits));
+    // logits: the output of a launch that is not fused, or, fused, what the
+    // vector kernel reads as y (it loads y before it knows the mode)
+    h.logits = o;
+    o = align256(o + (size_t)t * n * 4);
     if (h.fused) {
         h.m = (nblocks(n) + c.rb - 1) / c.rb;  // workgroups of the vector kernel
         h.pv = o;
@@ -253,8 +257,6 @@ HeadWs head_ws(int n, int t, const Shape& c) {
         o = align256(o + (size_t)t * h.m * 4);
     } else {
         h.m = n;
-        h.logits = o;
-        o = align256(o + (size_t)t * n * 4);
     }
     const int64_t nc = h.m > kPickChunk ? pick_chunks(h.m) : 0;
     h.tv = o;
@@ -450,10 +452,11 @@ int rv12_head_argmax(const rv12_matrix* w, const float* x, int t, const uint16_t
     char* b = (char*)ws;
     hipStream_t st = (hipStream_t)stream;
     LinearParams p;
-    float* y = h.fused ? logits : (logits ? logits : (float*)(b + h.logits));
+    float* y = logits ? logits : (float*)(b + h.logits);
     fill_params(p, w, x, y, t, lnw, eps, 0, ws, c.splits, c.splits > 1);
     int lrc;
     if (h.fused) {
+        p.store_y = logits != nullptr;
         p.amv = (float*)(b + h.pv);
         p.ami = (int32_t*)(b + h.pi);
         lrc = launch_gemv(p, t, c.rb, c.waves, 1, st);

@@ -98,8 +98,7 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     const int onc = min(on, p.N - 1);
     const int obase = p.rbase[onc];  // raw: the scale exponent is formed in the epilogue
     const int32_t oe0 = p.rp[onc], oe1 = p.rp[onc + 1];
-    float oy = 0.0f;  // y is read only when accumulating (a greedy pick may pass no y)
-    if (p.mode != 0) oy = p.y[(int64_t)min(otok, T - 1) * p.N + onc];
+    const float oy = p.y[(int64_t)min(otok, T - 1) * p.N + onc];
 
     // ---- 1. activations of this thread: the chunks j < nxm hold the split's
     // columns (lanes past its end load column k_lo again, unused)
@@ -371,7 +370,7 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
                 v *= rms_scale(sqs, p.K, p.eps);
             }
             yv = p.mode == 0 ? v : oy + v;
-            if (p.y) p.y[(int64_t)otok * p.N + on] = yv;
+            if (p.store_y) p.y[(int64_t)otok * p.N + on] = yv;
         } else {
             p.part[((int64_t)sp * T + otok) * p.npad + on] = v;
         }

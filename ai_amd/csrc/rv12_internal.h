@@ -23,6 +23,7 @@ struct LinearParams {
     float* amv = nullptr;    // fused greedy pick (vector kernel, one split): per token and
     int32_t* ami = nullptr;  // workgroup the largest output and its row, [T][workgroups]
     int N, K, npad, mode, xs;
+    int store_y = 1;  // 0: the vector kernel's fused greedy pick without logits (y is then only read)
     int64_t n_exc;
     float eps;
 };

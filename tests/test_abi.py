@@ -147,8 +147,9 @@ def test_gemm_argument_errors():
 
 def test_head_argmax_argument_errors_and_workspace():
     """The greedy pick's checks (before any device work) and its workspace:
-    the fused pick's per-workgroup pairs at 1-2 tokens, the logits and chunk
-    pairs of the two-pass pick otherwise (each part 256-byte aligned)."""
+    split partials, the logits (the output of an unfused launch; what the
+    fused one reads as y), the fused pick's per-workgroup pairs at 1-2 tokens,
+    the chunk pairs of a two-pass pick (each part 256-byte aligned)."""
     from ai_amd import _lib
     L = _lib.lib()
     P = ctypes.c_void_p
@@ -177,7 +178,7 @@ def test_head_argmax_argument_errors_and_workspace():
     assert L.rv12_launch_shape(151936, 4096, 1, None, ctypes.byref(c)) == 0 and c.kernel == 1 and c.splits == 1
     m = (151936 // 16 + c.rb - 1) // c.rb
     nc = (m + 8191) // 8192 if m > 8192 else 0
-    assert hw(151936, 4096, 1) == 2 * a(4 * m) + 2 * a(4 * nc)
+    assert hw(151936, 4096, 1) == a(4 * 151936) + 2 * a(4 * m) + 2 * a(4 * nc)
     # 16 tokens (MFMA): split partials, logits, 19 chunk pairs per token
     assert L.rv12_launch_shape(151936, 4096, 16, None, ctypes.byref(c)) == 0 and c.kernel == 2
     split = L.rv12_workspace_bytes(151936, 4096, 16, c.splits)
