@@ -1,7 +1,9 @@
-"""Decode-step attention of one layer through librv12.so (rv12_rope_attn):
-q/k head RMSNorm, RoPE at a device-side position, K/V into the cache,
-grouped-query attention over positions 0..pos.  The MI355X kernel for the
-reference's rope_attn_k (ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213)."""
+"""Attention of one layer through librv12.so: q/k head RMSNorm, RoPE at a
+device-side position, K/V into the cache, grouped-query attention.  One token
+(rv12_rope_attn: the reference's rope_attn_k,
+ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213) or a batch of up to 16
+tokens of one sequence, each attending causally (rv12_rope_attn_batch: the
+reference's qk_rope_cache_k + attn_k, tkernels.py:82-150)."""
 import ctypes
 
 import torch
@@ -34,6 +36,8 @@ class RopeAttn:
                       splits or default_splits(n_kv, maxt), float(eps), float(head_dim ** -0.5))
         need = lib().rv12_attn_workspace_bytes(ctypes.byref(self.a))
         self.ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+        need = lib().rv12_attn_batch_workspace_bytes(ctypes.byref(self.a), 16)
+        self.wsb = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
 
     def __call__(self, qkv, qn, kn, inv, pos, kc, vc, out):
         for t in (qkv, qn, kn, inv, out):
@@ -46,3 +50,17 @@ class RopeAttn:
                                   p(self.ws), self.ws.numel(),
                                   ctypes.c_void_p(torch.cuda.current_stream(qkv.device).cuda_stream))
         check(rc, "rope_attn")
+
+    def batch(self, qkv, qn, kn, inv, pos, kc, vc, out, T):
+        """T <= 16 tokens at positions pos .. pos + T - 1: rows of qkv in, rows
+        of out written; K/V of the T positions into the caches."""
+        for t in (qkv, qn, kn, inv, out):
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                raise ValueError("qkv, qn, kn, inv and out must be contiguous float32")
+        if pos.dtype != torch.int64:
+            raise ValueError("pos must be int64")
+        p = lambda t: ctypes.c_void_p(t.data_ptr())
+        rc = lib().rv12_rope_attn_batch(ctypes.byref(self.a), int(T), p(qkv), p(qn), p(kn), p(inv), p(pos), p(kc),
+                                        p(vc), p(out), p(self.wsb), self.wsb.numel(),
+                                        ctypes.c_void_p(torch.cuda.current_stream(qkv.device).cuda_stream))
+        check(rc, "rope_attn_batch")

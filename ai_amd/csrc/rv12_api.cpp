@@ -536,4 +536,47 @@ int rv12_rope_attn(const rv12_attn* a, const float* qkv, const float* qn, const 
     return launch_status();
 }
 
+size_t rv12_attn_batch_workspace_bytes(const rv12_attn* a, int t) {
+    if (check_attn(a) || t < 1 || t > 16) return 0;
+    if (attn_batch_lds_bytes(a->head_dim) > kMaxLds) return 0;
+    const size_t q = align256((size_t)t * a->n_heads * a->head_dim * 4);
+    const size_t rows = (size_t)t * (a->n_heads / a->n_kv);
+    return q + (a->splits > 1 ? 4 * (size_t)a->n_kv * a->splits * rows * (a->head_dim + 2) : 0);
+}
+
+int rv12_rope_attn_batch(const rv12_attn* a, int t, const float* qkv, const float* qn, const float* kn,
+                         const float* inv, const int64_t* pos, void* kc, void* vc, float* out, void* ws,
+                         size_t ws_bytes, void* stream) {
+    int rc = check_attn(a);
+    if (rc) return rc;
+    if (t < 1 || t > 16) return RV12_E_TOKENS;
+    if (!qkv || !qn || !kn || !inv || !pos || !kc || !vc || !out) return RV12_E_NULL;
+    if (!aligned16(qkv) || !aligned16(kc) || !aligned16(vc) || !aligned16(out)) return RV12_E_ALIGN;
+    const size_t need = rv12_attn_batch_workspace_bytes(a, t);
+    if (!need) return RV12_E_CONFIG;
+    if (!ws || ws_bytes < need) return RV12_E_WORKSPACE;
+    if (!aligned16(ws)) return RV12_E_ALIGN;
+    AttnParams p;
+    p.qkv = qkv;
+    p.qn = qn;
+    p.kn = kn;
+    p.inv = inv;
+    p.pos = pos;
+    p.kc = kc;
+    p.vc = vc;
+    p.out = out;
+    p.qo = (float*)ws;
+    p.part = (float*)((char*)ws + align256((size_t)t * a->n_heads * a->head_dim * 4));
+    p.n_heads = a->n_heads;
+    p.n_kv = a->n_kv;
+    p.head_dim = a->head_dim;
+    p.maxt = a->maxt;
+    p.kv_bf16 = a->kv_bf16 ? 1 : 0;
+    p.eps = a->eps;
+    p.scale = a->scale;
+    p.T = t;
+    if (launch_attn_batch(p, a->splits, (hipStream_t)stream)) return RV12_E_CONFIG;
+    return launch_status();
+}
+
 }  // extern "C"

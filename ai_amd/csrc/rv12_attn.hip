@@ -317,16 +317,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
 // splits (8B decode at 2k context, 32 splits: 11.49 -> 11.20 us per layer
 // with 32 against 64, half of whose loads read past the last split; 0.6B at
 // 12 splits: 7.42 -> 7.24 us with 16 against 32).
+// R rows per kv head (G at one token, T G for a batch: row i is token i / G,
+// head i % G of the group); out is [T][n_heads][HD].
 template <int CB>
 __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out, int S,
-                                                      int G, int HD) {
+                                                      int G, int HD, int R, int H) {
     __shared__ float wts[kAttnMaxSplits];
     __shared__ float red[2][2];
     const int h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6, nw = HD >> 6;
-    const int g = h / G, i = h % G;
-    const int stride = G * (HD + 2) * 4;  // bytes from one split's partial of head h to the next
+    const int g = h / R, i = h % R;
+    const int stride = R * (HD + 2) * 4;  // bytes from one split's partial of row i to the next
     const __amdgpu_buffer_rsrc_t r =
-        attn_rsrc(part + ((int64_t)g * S * G + i) * (HD + 2), (uint32_t)((S - 1) * stride + (HD + 2) * 4));
+        attn_rsrc(part + ((int64_t)g * S * R + i) * (HD + 2), (uint32_t)((S - 1) * stride + (HD + 2) * 4));
     // statistics of splits d, d + HD (HD >= 64 threads, S <= 128)
     float m[2], l[2];
 #pragma unroll
@@ -370,7 +372,268 @@ __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ 
         for (int u = 0; u < CB; ++u)
             num = fmaf(a[u], s0 + u < S ? wts[min(s0 + u, kAttnMaxSplits - 1)] : 0.0f, num);
     }
-    out[(int64_t)h * HD + d] = num / den;
+    out[((int64_t)(i / G) * H + g * G + i % G) * HD + d] = num / den;
+}
+
+// the combine pass over R rows per kv head (nothing to do for one split)
+static void launch_combine(const AttnParams& p, int S, int G, int R, hipStream_t st) {
+    const dim3 grid((unsigned)(p.n_kv * R)), block((unsigned)p.head_dim);
+    if (S > 1 && S <= 16)
+        hipLaunchKernelGGL(k_attn_combine<16>, grid, block, 0, st, p.part, p.out, S, G, p.head_dim, R, p.n_heads);
+    else if (S > 16 && S <= 32)
+        hipLaunchKernelGGL(k_attn_combine<32>, grid, block, 0, st, p.part, p.out, S, G, p.head_dim, R, p.n_heads);
+    else if (S > 32)
+        hipLaunchKernelGGL(k_attn_combine<64>, grid, block, 0, st, p.part, p.out, S, G, p.head_dim, R, p.n_heads);
+}
+
+// ---------------------------------------------------------------- batches
+// T tokens of one sequence at positions p0 = *pos .. p0 + T - 1 (the
+// reference's batched companions qk_rope_cache_k + attn_k,
+// ramvi/engine/ramvi_engine/kernels/tkernels.py:82-150).  A batch that does
+// not fit the cache (p0 < 0 or p0 + T > maxt) gives zeros and writes no cache.
+
+// 1. one wave per (head, token): q heads get their RMSNorm and RoPE into qo;
+// k heads the same, rounded to the cache dtype, into the cache at p0 + t; v
+// heads rounded into the cache.
+template <int HD, bool BF16>
+__global__ __launch_bounds__(64) void k_qk_rope_cache(AttnParams p) {
+    constexpr int half = HD / 2;
+    const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int H = p.n_heads, KV = p.n_kv;
+    const int64_t p0 = *p.pos;
+    if (p0 < 0 || p0 + p.T > p.maxt) return;
+    const int64_t pos = p0 + t;
+    const float* row = p.qkv + (int64_t)t * (H + 2 * KV) * HD;
+    if (h < H + KV) {
+        const int la = lane < half ? lane : 0;
+        const float msk = lane < half ? 1.0f : 0.0f;
+        const float a = msk * row[h * HD + la], b = msk * row[h * HD + la + half];
+        const float* nw = h < H ? p.qn : p.kn;
+        float sn, cs;
+        sincosf((float)pos * p.inv[la], &sn, &cs);
+        const float rs = 1.0f / sqrtf(wave_sum(a * a + b * b) / (float)HD + p.eps);
+        if (lane < half) {
+            const float x = nw[la] * (a * rs), y = nw[la + half] * (b * rs);
+            const float o0 = x * cs - y * sn, o1 = y * cs + x * sn;
+            if (h < H) {
+                float* dst = p.qo + ((int64_t)t * H + h) * HD;
+                dst[la] = o0;
+                dst[la + half] = o1;
+            } else {
+                const int64_t off = ((int64_t)(h - H) * p.maxt + pos) * HD;
+                if constexpr (BF16) {
+                    reinterpret_cast<uint16_t*>(p.kc)[off + la] = f2bf16(o0);
+                    reinterpret_cast<uint16_t*>(p.kc)[off + la + half] = f2bf16(o1);
+                } else {
+                    reinterpret_cast<float*>(p.kc)[off + la] = o0;
+                    reinterpret_cast<float*>(p.kc)[off + la + half] = o1;
+                }
+            }
+        }
+    } else {
+        const int64_t off = ((int64_t)(h - H - KV) * p.maxt + pos) * HD;
+        for (int d = lane; d < HD; d += 64) {
+            const float v = row[h * HD + d];
+            if constexpr (BF16) reinterpret_cast<uint16_t*>(p.vc)[off + d] = f2bf16(v);
+            else reinterpret_cast<float*>(p.vc)[off + d] = v;
+        }
+    }
+}
+
+// 2. grid (kv heads, splits, row chunks), 320 threads: workgroup (g, sp, c)
+// covers the positions [lo, hi) of 0..p0 + T - 1 (at most 80) for rows
+// c R16 .. c R16 + 15 of kv head g (row i: token i / G, head i % G of the
+// group; R16 = kAttnRows), each row seeing positions j <= p0 + its token.
+// The phases of k_rope_attn: cache values loaded first (a quarter key row per
+// thread, value pairs of 16 (8) positions), the chunk's q rows staged in
+// LDS, quarter-dim scores joined by lane exchanges, per-row softmax
+// statistics in one pass, value sums over position groups joined in a fixed
+// order; out (one split) or (acc, m, l) partials for k_attn_combine.
+template <int HD, bool BF16>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_rows(AttnParams p) {
+    extern __shared__ float lds[];
+    constexpr int RC = kAttnRows;
+    constexpr int NW = kAttnThreads / 64;
+    constexpr int P = kAttnSpan;
+    constexpr int EB = BF16 ? 2 : 4;
+    constexpr int QD = HD / 4;
+    constexpr int KW = QD * EB / 16;
+    constexpr int DP = HD / 2;
+    constexpr int PG = kAttnThreads / DP;
+    constexpr int PPG = P / PG;
+    const int g = blockIdx.x, sp = blockIdx.y, S = gridDim.y, c = blockIdx.z;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int H = p.n_heads, G = H / p.n_kv, R = p.T * G;
+    const int r0 = c * RC;  // first row of the chunk
+    const int64_t p0 = *p.pos;
+    float* qs = lds;                 // [RC][HD]
+    float* wt = qs + RC * HD;        // [P][RC] weights exp(s - m)
+    float* red = wt + P * RC;        // [2][NW][RC] per-wave maxima, sums
+    float* stat = red + 2 * NW * RC; // [2 RC] m, l
+    float* wacc = stat + 2 * RC;     // [PG][RC][HD] value sums of the position groups
+    float* part = p.part + ((int64_t)g * S + sp) * R * (HD + 2);  // [n_kv][S][R][HD + 2]
+    if (p0 < 0 || p0 + p.T > p.maxt) {  // zeros out (or partials that combine to zeros), no cache access
+        for (int o = t; o < RC * (HD + 2); o += kAttnThreads) {
+            const int i = o / (HD + 2), d = o % (HD + 2), r = r0 + i;
+            if (r >= R) continue;
+            if (S == 1) {
+                if (d < HD) p.out[((int64_t)(r / G) * H + g * G + r % G) * HD + d] = 0.0f;
+            } else {
+                part[r * (HD + 2) + d] =
+                    d < HD ? 0.0f : (d == HD ? (sp == 0 ? 0.0f : -INFINITY) : (sp == 0 ? 1.0f : 0.0f));
+            }
+        }
+        return;
+    }
+    const int n = (int)p0 + p.T;  // positions 0..n-1; n <= 10240 and S <= 128: 32-bit products
+    const int lo = (int)((uint32_t)(sp * n) / (uint32_t)S), hi = (int)((uint32_t)((sp + 1) * n) / (uint32_t)S);
+    const int span = hi - lo;  // <= P (host)
+    const int64_t row0 = (int64_t)g * p.maxt * HD;
+
+    // ---- 0. cache values of positions [lo, hi): descriptors end at hi
+    const uint32_t cbytes = (uint32_t)hi * HD * EB;
+    const __amdgpu_buffer_rsrc_t kr = attn_rsrc(reinterpret_cast<const char*>(p.kc) + row0 * EB, cbytes);
+    const __amdgpu_buffer_rsrc_t vr = attn_rsrc(reinterpret_cast<const char*>(p.vc) + row0 * EB, cbytes);
+    const int pl = t >> 2, qq = t & 3;
+    uint32_t kw[KW][4];
+    load_words<KW>(kr, ((lo + pl) * HD + qq * QD) * EB, kw);
+    const int dp = t % DP, pg = t / DP;
+    uint32_t vw[PPG][2];
+#pragma unroll
+    for (int r = 0; r < PPG; ++r) {
+        const int off = ((lo + pg * PPG + r) * HD + 2 * dp) * EB;
+        if constexpr (BF16) {
+            vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(vr, off, 0, 0);
+            vw[r][1] = 0;
+        } else {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(vr, off, 0, 0);
+            vw[r][0] = v[0];
+            vw[r][1] = v[1];
+        }
+    }
+    // the chunk's q rows (rows past R read as zeros)
+    for (int o = t; o < RC * HD; o += kAttnThreads) {
+        const int i = o / HD, d = o % HD, r = r0 + i;
+        qs[o] = r < R ? p.qo[((int64_t)(r / G) * H + g * G + r % G) * HD + d] : 0.0f;
+    }
+    __syncthreads();
+
+    // ---- 1. scores; row i sees position j when j <= p0 + its token
+    const int j = lo + pl;
+    float sc[RC];
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+        const float* qrow = qs + i * HD + qq * QD;
+        float s = 0.0f;
+#pragma unroll
+        for (int d = 0; d < QD; d += 4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(qrow + d);
+            s = fmaf(q4.x, word_val<BF16>(kw, d), s);
+            s = fmaf(q4.y, word_val<BF16>(kw, d + 1), s);
+            s = fmaf(q4.z, word_val<BF16>(kw, d + 2), s);
+            s = fmaf(q4.w, word_val<BF16>(kw, d + 3), s);
+        }
+        s += dpp<kDppXor1>(s);
+        s += dpp<kDppXor2>(s);
+        const int r = r0 + i;
+        const bool vis = pl < span && r < R && j <= (int)p0 + r / G;
+        sc[i] = vis ? s * p.scale : -INFINITY;
+    }
+
+    // ---- 2. per-row softmax statistics in one pass (as k_rope_attn); a row
+    // that sees none of the split's positions gets m = -inf, l = 0
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+        const float mw = wave_max(sc[i]);
+        const float e = sc[i] > -INFINITY ? expf(sc[i] - mw) : 0.0f;
+        const float lw = wave_sum(qq == 0 ? e : 0.0f);
+        if (lane == 0) {
+            red[wave * RC + i] = mw;
+            red[(NW + wave) * RC + i] = lw;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+        float m = red[i];
+        for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w * RC + i]);
+        if (qq == 0 && pl < P) wt[pl * RC + i] = sc[i] > -INFINITY ? expf(sc[i] - m) : 0.0f;
+    }
+    if (t < RC) {
+        float m = red[t];
+        for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w * RC + t]);
+        float l = 0.0f;
+        for (int w = 0; w < NW; ++w) {
+            const float lw = red[(NW + w) * RC + t];
+            l += lw > 0.0f ? lw * expf(red[w * RC + t] - m) : 0.0f;
+        }
+        stat[t] = m;
+        stat[RC + t] = l;
+    }
+    __syncthreads();
+
+    // ---- 3. weighted values: thread (dp, pg) over its PPG positions
+    float acc[RC][2];
+#pragma unroll
+    for (int i = 0; i < RC; ++i) acc[i][0] = acc[i][1] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < PPG; ++r) {
+        const int pj = pg * PPG + r;
+        const float v0 = pair_val<BF16>(vw[r], 0), v1 = pair_val<BF16>(vw[r], 1);
+#pragma unroll
+        for (int i = 0; i < RC; ++i) {
+            const float w8 = wt[pj * RC + i];  // zero where the row does not see the position
+            acc[i][0] = fmaf(w8, v0, acc[i][0]);
+            acc[i][1] = fmaf(w8, v1, acc[i][1]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+        wacc[(pg * RC + i) * HD + 2 * dp] = acc[i][0];
+        wacc[(pg * RC + i) * HD + 2 * dp + 1] = acc[i][1];
+    }
+    __syncthreads();
+
+    // ---- 4. output or partials
+    for (int o = t; o < RC * HD; o += kAttnThreads) {
+        const int i = o / HD, d = o % HD, r = r0 + i;
+        if (r >= R) continue;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < PG; ++w) v += wacc[(w * RC + i) * HD + d];
+        if (S == 1) p.out[((int64_t)(r / G) * H + g * G + r % G) * HD + d] = v / stat[RC + i];
+        else part[r * (HD + 2) + d] = v;
+    }
+    if (S > 1 && t < RC && r0 + t < R) {
+        part[(r0 + t) * (HD + 2) + HD] = stat[t];
+        part[(r0 + t) * (HD + 2) + HD + 1] = stat[RC + t];
+    }
+}
+
+template <int HD, bool BF16>
+static void launch_batch_t(const AttnParams& p, int S, hipStream_t st) {
+    const int R = p.T * (p.n_heads / p.n_kv);
+    hipLaunchKernelGGL((k_qk_rope_cache<HD, BF16>), dim3(p.n_heads + 2 * p.n_kv, p.T), dim3(64), 0, st, p);
+    const size_t lds = attn_batch_lds_bytes(HD);
+    if (lds > kDefaultLds)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_rows<HD, BF16>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL((k_attn_rows<HD, BF16>), dim3(p.n_kv, S, (R + kAttnRows - 1) / kAttnRows),
+                       dim3(kAttnThreads), lds, st, p);
+}
+
+int launch_attn_batch(const AttnParams& p, int S, hipStream_t st) {
+    if (p.head_dim == 128) {
+        if (p.kv_bf16) launch_batch_t<128, true>(p, S, st);
+        else launch_batch_t<128, false>(p, S, st);
+    } else if (p.head_dim == 64) {
+        if (p.kv_bf16) launch_batch_t<64, true>(p, S, st);
+        else launch_batch_t<64, false>(p, S, st);
+    } else {
+        return -1;
+    }
+    launch_combine(p, S, p.n_heads / p.n_kv, p.T * (p.n_heads / p.n_kv), st);
+    return 0;
 }
 
 template <int HD, int G, bool BF16>
@@ -404,15 +667,7 @@ int launch_attn(const AttnParams& p, int S, hipStream_t st) {
     int rc = p.head_dim == 128 ? launch_attn_hd<128>(p, G, S, lds, st)
                                : (p.head_dim == 64 ? launch_attn_hd<64>(p, G, S, lds, st) : -1);
     if (rc) return rc;
-    if (S > 1 && S <= 16)
-        hipLaunchKernelGGL(k_attn_combine<16>, dim3(p.n_heads), dim3(p.head_dim), 0, st, p.part, p.out, S, G,
-                           p.head_dim);
-    else if (S > 16 && S <= 32)
-        hipLaunchKernelGGL(k_attn_combine<32>, dim3(p.n_heads), dim3(p.head_dim), 0, st, p.part, p.out, S, G,
-                           p.head_dim);
-    else if (S > 32)
-        hipLaunchKernelGGL(k_attn_combine<64>, dim3(p.n_heads), dim3(p.head_dim), 0, st, p.part, p.out, S, G,
-                           p.head_dim);
+    launch_combine(p, S, G, G, st);
     return 0;
 }
 

@@ -94,9 +94,11 @@ struct AttnParams {
     void* kc;
     void* vc;
     float* out;
-    float* part;  // split partials [n_kv][splits][G][HD + 2]
+    float* part;  // split partials [n_kv][splits][rows][HD + 2]
     int n_heads, n_kv, head_dim, maxt, kv_bf16;
     float eps, scale;
+    float* qo = nullptr;  // batch: the T tokens' normed, roped q rows [T][n_heads][HD]
+    int T = 1;            // batch: tokens at positions *pos .. *pos + T - 1
 };
 constexpr int kAttnThreads = 320;     // 4 per position of the span
 constexpr int kAttnSpan = 80;         // positions one attention workgroup covers at most
@@ -111,6 +113,14 @@ inline size_t attn_part_floats(int n_kv, int g, int hd, int splits) {
     return (size_t)n_kv * splits * g * (hd + 2);
 }
 int launch_attn(const AttnParams& p, int splits, hipStream_t st);
+// batch of T tokens: rows of one kv head = T * G, handled kAttnRows at a time
+constexpr int kAttnRows = 16;
+inline size_t attn_batch_lds_bytes(int hd) {
+    const size_t pg = kAttnThreads / (hd / 2);
+    return 4 * ((size_t)kAttnRows * hd + (size_t)kAttnSpan * kAttnRows + 2 * (kAttnThreads / 64) * kAttnRows +
+                2 * kAttnRows + pg * kAttnRows * hd);
+}
+int launch_attn_batch(const AttnParams& p, int splits, hipStream_t st);
 
 int launch_gemv(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st);
 int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st);

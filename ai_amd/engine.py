@@ -48,15 +48,6 @@ MATS = ("qkv", "o", "gu", "down")
 BATCH = 16  # largest batch of one pass, as the reference's graph buckets (engine.py:31)
 
 
-def _rms(x, w, eps):
-    return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
-
-
-def _rot(t):
-    h = t.shape[-1] // 2
-    return torch.cat([-t[..., h:], t[..., :h]], -1)
-
-
 class Engine:
     """Greedy Qwen3 decoding with every linear on the MI355X 12-bit path.
 
@@ -104,14 +95,12 @@ class Engine:
         self.head = wcomp.compact(wcomp.compress(ck.t(ck.head_name(), dev)))
         torch.cuda.empty_cache()
         f = lambda n: torch.zeros(BATCH, n, device=dev)
-        self.xb, self.hb, self.qkvb, self.attb, self.gub = f(self.D), f(self.D), f((H + 2 * KV) * HD), f(H * HD), f(
-            2 * self.FF)
+        self.xb, self.qkvb, self.attb, self.gub = f(self.D), f((H + 2 * KV) * HD), f(H * HD), f(2 * self.FF)
         self.pos = torch.zeros(1, dtype=torch.long, device=dev)
         self.tok = torch.zeros(BATCH, dtype=torch.long, device=dev)
         self.nxt = torch.zeros(BATCH, dtype=torch.long, device=dev)
         self.steps = torch.zeros(1, dtype=torch.long, device=dev)
         self.out = torch.zeros(maxt + 1, dtype=torch.long, device=dev)
-        self.ar = torch.arange(maxt, device=dev)
         self.attn = RopeAttn(H, KV, HD, maxt, kv_dtype, self.eps, dev)
         self.graph = None
         self.pgraph = None  # a full prefill chunk of BATCH tokens
@@ -120,41 +109,14 @@ class Engine:
     def _rope_attn(self, l, T, p0=None):
         """Rows 0..T-1 of qkv at positions pos..pos+T-1: q/k head RMSNorm,
         RoPE, K/V into the cache (rounded to its dtype), causal attention over
-        the cache (tkernels.py:82-150, 164-213).  One token: the HIP kernel;
-        a batch (prefill, first position p0 known on the host): torch."""
+        the cache (tkernels.py:82-150, 164-213), all on the device: the
+        one-token kernel, or the batch kernels for T > 1."""
+        s = self.small[l]
         if T == 1:
-            s = self.small[l]
             self.attn(self.qkvb[0], s["qn"], s["kn"], self.inv, self.pos, self.Kc[l], self.Vc[l], self.attb[0])
-            return
-        self._rope_attn_torch(l, T, p0)
-
-    def _rope_attn_torch(self, l, T, p0=None):
-        """Batched prefill attention in torch; with p0 given only the cache
-        positions [0, p0 + T) take part (the rest are masked anyway)."""
-        H, KV, HD = self.H, self.KV, self.HD
-        G = H // KV
-        qkv = self.qkvb[:T]
-        q = _rms(qkv[:, :H * HD].view(T, H, HD), self.small[l]["qn"], self.eps)
-        k = _rms(qkv[:, H * HD:(H + KV) * HD].view(T, KV, HD), self.small[l]["kn"], self.eps)
-        v = qkv[:, (H + KV) * HD:].view(T, KV, HD)
-        p = self.pos + self.ar[:T]
-        ang = p[:, None].float() * self.inv[None]
-        e = torch.cat([ang, ang], -1)
-        cos, sin = e.cos()[:, None], e.sin()[:, None]
-        q = q * cos + _rot(q) * sin
-        k = k * cos + _rot(k) * sin
-        Kc, Vc = self.Kc[l], self.Vc[l]
-        Kc.index_copy_(1, p, k.to(self.kv_dtype).transpose(0, 1))
-        Vc.index_copy_(1, p, v.to(self.kv_dtype).transpose(0, 1))
-        n = self.maxt if p0 is None else min(self.maxt, p0 + T)
-        Kf, Vf = Kc[:, :n].float(), Vc[:, :n].float()
-        qg = q.view(T, KV, G, HD).permute(1, 2, 0, 3).reshape(KV, G * T, HD)
-        sc = torch.bmm(Kf, qg.transpose(1, 2).contiguous()).transpose(1, 2)  # [KV, G*T, n]
-        sc = sc.reshape(KV, G, T, n) * HD ** -0.5
-        sc = sc.masked_fill(self.ar[None, None, None, :n] > p[None, None, :, None], float("-inf"))
-        a = torch.softmax(sc, -1).reshape(KV, G * T, n)
-        o = torch.bmm(a, Vf).view(KV, G, T, HD).permute(2, 0, 1, 3).reshape(T, H * HD)
-        self.attb[:T].copy_(o)
+        else:
+            self.attn.batch(self.qkvb[:T], s["qn"], s["kn"], self.inv, self.pos, self.Kc[l], self.Vc[l],
+                            self.attb[:T], T)
 
     def _gpu_layer(self, l, x, T, p0=None, W=None):
         """engine.py:329-341: one token with the RMS prologues fused, else the batched layer."""
@@ -169,16 +131,14 @@ class Engine:
         wcomp.gemvc1(self.gub[:1], W["down"], x, 2)
 
     def _batch_layer(self, l, x, T, p0=None, W=None):
-        """engine.py:344-356: T <= 16 tokens of one sequence (first position p0)."""
+        """engine.py:344-356: T <= 16 tokens of one sequence; the RMSNorms
+        (rmsg_k in the reference) are fused into the qkv and gu linears."""
         W = self.W[l] if W is None else W
         s = self.small[l]
-        h = self.hb[:T]
-        h.copy_(_rms(x, s["ln1"].float(), self.eps))
-        wcomp.gemvc_tc(h, W["qkv"], self.qkvb[:T], 0, T)
+        wcomp.gemvc_tc(x, W["qkv"], self.qkvb[:T], 0, T, lnw=s["ln1"], eps=self.eps)
         self._rope_attn(l, T, p0)
         wcomp.gemvc_tc(self.attb[:T], W["o"], x, 1, T)
-        h.copy_(_rms(x, s["ln2"].float(), self.eps))
-        wcomp.gemvc_tc(h, W["gu"], self.gub[:T], 0, T)
+        wcomp.gemvc_tc(x, W["gu"], self.gub[:T], 0, T, lnw=s["ln2"], eps=self.eps)
         wcomp.gemvc_tc(self.gub[:T], W["down"], x, 2, T)
 
     def _layers(self, x, T, p0=None):

@@ -391,8 +391,10 @@ def gemvc1(x, c, y, mode, BN=None, w=None, lnw=None, eps=1e-6):
     _linear(x, c, y, mode, 1, BN, w, S, lnw, eps, "gemvc1")
 
 
-def gemvc_tc(x, c, y, mode, T, BN=None, w=None, S=None):
-    """1 <= T <= 16 token rows: y[t] (=|+=) W x'[t] (wcomp.py:155-242)."""
+def gemvc_tc(x, c, y, mode, T, BN=None, w=None, S=None, lnw=None, eps=1e-6):
+    """1 <= T <= 16 token rows: y[t] (=|+=) W x'[t] (wcomp.py:155-242).  lnw
+    (an addition: bf16 [K]) fuses each row's RMSNorm into the prologue, as
+    gemvc1 does at one token, in place of a separate rmsg_k pass."""
     N, K = int(c["N"]), int(c["K"])
     if BN is None and int(T) > VECTOR_TOKENS:  # CFGT is tuned at 16 tokens, for the MFMA kernel
         cfg = CFGT.get((N, K, mode))
@@ -400,4 +402,4 @@ def gemvc_tc(x, c, y, mode, T, BN=None, w=None, S=None):
             BN, w, S = cfg
     if not 1 <= int(T) <= 16:
         raise ValueError("T must be in [1, 16]")
-    _linear(x, c, y, mode, int(T), BN, w, S, None, 1e-6, "gemvc_tc")
+    _linear(x, c, y, mode, int(T), BN, w, S, lnw, eps, "gemvc_tc")

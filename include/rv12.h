@@ -239,6 +239,23 @@ size_t rv12_attn_workspace_bytes(const rv12_attn* a);
 int rv12_rope_attn(const rv12_attn* a, const float* qkv, const float* qn, const float* kn, const float* inv,
                    const int64_t* pos, void* kc, void* vc, float* out, void* ws, size_t ws_bytes, void* stream);
 
+/* Attention of a batch of 1 <= t <= 16 tokens of one sequence at positions
+ * *pos .. *pos + t - 1 (read on the device): rows r of qkv (t rows of
+ * (n_heads + 2 n_kv) * head_dim floats) as in rv12_rope_attn; q and k get the
+ * head RMSNorm and RoPE at their position, k and v (rounded to the cache dtype)
+ * go into the caches, and token r attends over positions 0..*pos + r (causal)
+ * into out[r] (t rows of n_heads * head_dim floats).  Three passes (q/k/v
+ * prologue, attention over position splits of at most 80 positions with all
+ * the batch's rows of a kv head, the ordered combine), no atomics.  A batch
+ * outside [0, maxt) gives zeros and leaves the caches untouched.  ws:
+ * rv12_attn_batch_workspace_bytes(a, t) bytes (the q rows and the split
+ * partials), 16-byte aligned.  Replaces qk_rope_cache_k and attn_k,
+ * ramvi/engine/ramvi_engine/kernels/tkernels.py:82-150. */
+size_t rv12_attn_batch_workspace_bytes(const rv12_attn* a, int t);
+int rv12_rope_attn_batch(const rv12_attn* a, int t, const float* qkv, const float* qn, const float* kn,
+                         const float* inv, const int64_t* pos, void* kc, void* vc, float* out, void* ws,
+                         size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

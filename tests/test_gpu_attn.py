@@ -185,3 +185,131 @@ def test_graph_replays_advance_the_position():
         ref, _, _ = _torch_ref(qkv, ones, ones, inv, p, kc0, vc0, H, KV, HD, 1e-6, k_at_pos=kc[:, p].clone())
         assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), (r, float((out - ref).abs().max()))
         qkv.mul_(0.9)  # eager work between the replays
+
+
+def _torch_batch_ref(qkv, qn, kn, inv, p0, kc, vc, H, KV, HD, eps, k_new=None):
+    """T rows of qkv at positions p0..p0+T-1: the rounded k/v of all T
+    positions in the caches (k_new: the keys as the kernel stored them, one
+    bf16 rounding apart at most), then token t attends over 0..p0+t."""
+    T = qkv.shape[0]
+    G = H // KV
+    q = qkv[:, :H * HD].view(T, H, HD)
+    k = qkv[:, H * HD:(H + KV) * HD].view(T, KV, HD)
+    v = qkv[:, (H + KV) * HD:].view(T, KV, HD)
+    rms = lambda x, w: w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+    q, k = rms(q, qn), rms(k, kn)
+    pos = torch.arange(p0, p0 + T, device=inv.device, dtype=torch.float32)
+    ang = (pos[:, None] * inv[None]).double()
+    cos = torch.cat([ang, ang], -1).cos().float()[:, None]
+    sin = torch.cat([ang, ang], -1).sin().float()[:, None]
+    rot = lambda t: torch.cat([-t[..., HD // 2:], t[..., :HD // 2]], -1)
+    q, k = q * cos + rot(q) * sin, k * cos + rot(k) * sin
+    kr, vr = k.to(kc.dtype), v.to(vc.dtype)
+    K = kc.float().clone()
+    V = vc.float().clone()
+    K[:, p0:p0 + T] = (kr if k_new is None else k_new).float().transpose(0, 1)
+    V[:, p0:p0 + T] = vr.float().transpose(0, 1)
+    out = torch.empty(T, H * HD, device=qkv.device)
+    for t in range(T):
+        n = p0 + t + 1
+        s = torch.matmul(q[t].view(KV, G, HD).double(), K[:, :n].double().transpose(1, 2).contiguous()) * HD ** -0.5
+        a = torch.softmax(s, -1)
+        out[t] = torch.matmul(a, V[:, :n].double().contiguous()).reshape(H * HD).float()
+    return out, kr, vr
+
+
+@pytest.mark.parametrize("H,KV,HD", [(32, 8, 128), (16, 8, 128), (8, 4, 64), (64, 8, 128), (8, 8, 64)])
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16])
+def test_batch_attention_matches_torch(H, KV, HD, kv_dtype):
+    """rv12_rope_attn_batch (the batched companions qk_rope_cache_k + attn_k)
+    for T = 2, 5, 16 tokens at the start, the middle and the end of the cache,
+    one split and several: outputs within 1e-4 of the float64 restatement,
+    the T cache slots written (k within one bf16 ulp, v exact), the others
+    untouched."""
+    from ai_amd.attn import RopeAttn
+    dev = "cuda"
+    maxt = 300
+    g = torch.Generator(device=dev).manual_seed(H * 10 + HD + 7)
+    eps = 1e-6
+    inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+    qn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    kn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    for splits in (4, 19, 60):
+        att = RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev, splits=splits)
+        for T in (2, 5, 16):
+            for p0 in (0, 37, maxt - T):
+                print("case", H, KV, HD, kv_dtype, splits, T, p0, flush=True)
+                qkv = torch.randn(T, (H + 2 * KV) * HD, device=dev, generator=g) * 3
+                kc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+                vc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+                kc0, vc0 = kc.clone(), vc.clone()
+                out = torch.zeros(T, H * HD, device=dev)
+                att.batch(qkv, qn, kn, inv, torch.tensor([p0], device=dev), kc, vc, out, T)
+                torch.cuda.synchronize()
+                ref, kr, vr = _torch_batch_ref(qkv, qn, kn, inv, p0, kc0, vc0, H, KV, HD, eps,
+                                               k_new=kc[:, p0:p0 + T].transpose(0, 1).clone())
+                assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), float((out - ref).abs().max())
+                tol = 2.0 ** -7 if kv_dtype == torch.bfloat16 else 1e-5
+                assert torch.allclose(kc[:, p0:p0 + T].float(), kr.float().transpose(0, 1), rtol=tol, atol=1e-6)
+                assert torch.equal(vc[:, p0:p0 + T].float(), vr.float().transpose(0, 1))
+                keep = torch.ones(maxt, dtype=torch.bool)
+                keep[p0:p0 + T] = False
+                assert torch.equal(kc[:, keep], kc0[:, keep]) and torch.equal(vc[:, keep], vc0[:, keep])
+
+
+def test_batch_equals_single_steps_and_graph_replays():
+    """A batch of 8 equals 8 single-token steps from the same cache (each step
+    sees the keys the previous ones wrote), and a captured batch replayed with
+    the position advanced on the device gives the eager results; a batch
+    past the cache's end gives zeros and writes nothing."""
+    from ai_amd.attn import RopeAttn
+    dev = "cuda"
+    H, KV, HD, maxt, T = 32, 8, 128, 512, 8
+    g = torch.Generator(device=dev).manual_seed(5)
+    inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+    qn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    kn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    att = RopeAttn(H, KV, HD, maxt, torch.bfloat16, 1e-6, dev)
+    qkv = torch.randn(T, (H + 2 * KV) * HD, device=dev, generator=g)
+    kc = torch.randn(KV, maxt, HD, device=dev, generator=g).bfloat16()
+    vc = torch.randn(KV, maxt, HD, device=dev, generator=g).bfloat16()
+    kc1, vc1 = kc.clone(), vc.clone()
+    p0 = 200
+    out = torch.zeros(T, H * HD, device=dev)
+    att.batch(qkv, qn, kn, inv, torch.tensor([p0], device=dev), kc, vc, out, T)
+    one = torch.zeros(T, H * HD, device=dev)
+    for t in range(T):
+        att(qkv[t].contiguous(), qn, kn, inv, torch.tensor([p0 + t], device=dev), kc1, vc1, one[t])
+    torch.cuda.synchronize()
+    # the same keys up to one bf16 rounding (the two kernels may contract the
+    # RoPE products differently), the same values
+    assert torch.allclose(kc.float(), kc1.float(), rtol=2.0 ** -7, atol=1e-6) and torch.equal(vc, vc1)
+    assert torch.allclose(out, one, rtol=1e-4, atol=1e-5), float((out - one).abs().max())
+    # graph: replays at positions p0, p0 + T, p0 + 2T against eager calls
+    pos = torch.tensor([p0], device=dev)
+    kg, vg = kc.clone(), vc.clone()
+    og = torch.zeros(T, H * HD, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        att.batch(qkv, qn, kn, inv, pos, kg, vg, og, T)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        att.batch(qkv, qn, kn, inv, pos, kg, vg, og, T)
+        pos.add_(T)
+    ke, ve = kg.clone(), vg.clone()
+    pe = p0
+    for _ in range(3):
+        graph.replay()
+        oe = torch.zeros(T, H * HD, device=dev)
+        att.batch(qkv, qn, kn, inv, torch.tensor([pe], device=dev), ke, ve, oe, T)
+        pe += T
+        torch.cuda.synchronize()
+        assert torch.equal(og, oe) and torch.equal(kg, ke) and torch.equal(vg, ve)
+    # past the end: zeros, caches untouched
+    k0, v0 = kc.clone(), vc.clone()
+    bad = torch.full((T, H * HD), 7.0, device=dev)
+    att.batch(qkv, qn, kn, inv, torch.tensor([maxt - T + 1], device=dev), kc, vc, bad, T)
+    torch.cuda.synchronize()
+    assert torch.equal(bad, torch.zeros_like(bad)) and torch.equal(kc, k0) and torch.equal(vc, v0)
