@@ -21,6 +21,7 @@ OUT = os.path.join(HERE, "librv12.so")
 SOURCES = ["rv12_codec.hip", "rv12_gemv.hip", "rv12_gemm.hip", "rv12_attn.hip", "rv12_static.hip", "rv12_api.cpp"]
 HEADERS = ["rv12_device.h", "rv12_internal.h"]
 MANIFEST = OUT + ".build.json"
+PROBE_OUT = os.path.join(HERE, "librv12probe.so")  # bench.py's stream-ceiling probe (not the product)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CODEGEN = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -81,7 +82,18 @@ def build(verbose=False):
     with open(MANIFEST + ".tmp", "w") as f:
         json.dump(man, f, indent=1, sort_keys=True)
     os.replace(MANIFEST + ".tmp", MANIFEST)
+    build_probe()
     return OUT
+
+
+def build_probe():
+    """librv12probe.so: the pure-stream probe bench.py times beside the linear."""
+    tmp = PROBE_OUT + ".tmp"
+    r = subprocess.run([HIPCC] + FLAGS + [os.path.join(CSRC, "rv12_probe.hip"), "-o", tmp], capture_output=True,
+                       text=True)
+    if r.returncode:
+        raise RuntimeError(f"hipcc failed on the probe ({r.returncode}):\n{r.stdout}{r.stderr}")
+    os.replace(tmp, PROBE_OUT)
 
 
 if __name__ == "__main__":

@@ -313,10 +313,49 @@ def run_shape(name, reps, dev, min_bytes=1.2e9, outliers="rows"):
     cb = sum(comp_bytes(c) for c in cs) / ncopy
     ab = sum(alg_bytes(c, mode, False) for c in cs) / ncopy
     exc = sum(int(c["er"].numel()) for c in cs) / ncopy / (N * K)
+    r = {"shape": name, "N": N, "K": K, "copies": ncopy, "us": ms * 1e3, "comp_GBs": cb / ms / 1e6,
+         "alg_GBs": ab / ms / 1e6, "frac_peak": cb / ms / 1e6 / PEAK_HBM, "exception_frac": exc}
+    st = stream_ceiling(cs, N, K, reps)
+    if st:
+        r.update(st)
+        r["ceiling_frac"] = r["stream_us"] / r["us"]  # the linear's rate over the pure stream's
     del cs, graph
     torch.cuda.empty_cache()
-    return {"shape": name, "N": N, "K": K, "copies": ncopy, "us": ms * 1e3, "comp_GBs": cb / ms / 1e6,
-            "alg_GBs": ab / ms / 1e6, "frac_peak": cb / ms / 1e6 / PEAK_HBM, "exception_frac": exc}
+    return r
+
+
+def stream_ceiling(cs, N, K, reps):
+    """The pure weight stream of the same launch (ai_amd/csrc/rv12_probe.hip:
+    the vector linear's grid, waves, step order, loads and prefetch depth at
+    one token, without decode, activations, FMAs or exceptions) over the same
+    copies: what a launch of this shape can reach on its 12-bit bytes."""
+    import ctypes
+    from ai_amd import _lib, build
+    if not os.path.exists(build.PROBE_OUT):
+        return None
+    P = ctypes.CDLL(build.PROBE_OUT)
+    P.rv12_probe_stream.restype = ctypes.c_int
+    P.rv12_probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    c = _lib.Launch()
+    if _lib.lib().rv12_launch_shape(N, K, 1, None, ctypes.byref(c)) or c.kernel != 1 or c.splits != 1:
+        return None
+    nblk = (N + 15) // 16
+    out = torch.empty(((nblk + c.rb - 1) // c.rb) * c.waves * 64, dtype=torch.int32, device="cuda")
+    depth = 6  # the vector kernel's prefetch depth at one token without prologue
+
+    def fn():
+        for m in cs:
+            rc = P.rv12_probe_stream(ctypes.c_void_p(m["q16_tiles"].data_ptr()), N, K, c.rb, c.waves, depth,
+                                     ctypes.c_void_p(out.data_ptr()),
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            assert rc == 0, rc
+
+    graph = Graph(fn)
+    ms = time_graph(graph, reps) / len(cs)
+    tb = 1.5 * ((N + 15) // 16 * 16) * K
+    del graph
+    return {"stream_us": ms * 1e3, "stream_GBs": tb / ms / 1e6, "stream_frac_peak": tb / ms / 1e6 / PEAK_HBM}
 
 
 def run_skinny(name, reps, dev, min_bytes=1.2e9):
@@ -533,8 +572,9 @@ def main():
     if not args.no_sweep:
         for name in ("q_o", "k_v", "gate_up", "down", "lm_head", "qkv", "gu"):
             r = run_shape(name, args.reps, dev)
-            print(f"# {name}: {r['us']:.1f} us/launch, {r['comp_GBs']:.0f} GB/s ({r['frac_peak']:.1%})",
-                  file=sys.stderr, flush=True)
+            print(f"# {name}: {r['us']:.1f} us/launch, {r['comp_GBs']:.0f} GB/s ({r['frac_peak']:.1%}); pure "
+                  f"stream {r.get('stream_us', 0):.1f} us ({r.get('stream_frac_peak', 0):.1%}), linear at "
+                  f"{r.get('ceiling_frac', 0):.1%} of it", file=sys.stderr, flush=True)
             sweep.append({k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()})
         for name in ("q_o", "k_v", "gate_up", "down", "lm_head", "qkv", "gu"):
             r = run_shape(name, args.reps, dev, outliers="columns")
