@@ -532,6 +532,8 @@ def main():
     ap.add_argument("--no-32b", action="store_true", help="skip the Qwen3-32B end-to-end decode")
     ap.add_argument("--only-14b", action="store_true", help="run only the Qwen3-14B skinny-GEMM sweep (for profiling)")
     ap.add_argument("--only-attn", action="store_true", help="run only the Qwen3-8B decode attention (for profiling)")
+    ap.add_argument("--only-e2e", action="store_true",
+                    help="run only the Qwen3-8B end-to-end decode (2048-token prompt, 256 tokens; for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (scale factor of the HBM byte counters)")
     args = ap.parse_args()
@@ -556,6 +558,9 @@ def main():
         return
     if args.only_attn:
         print(json.dumps(run_attn(dev, args.reps)), flush=True)
+        return
+    if args.only_e2e:
+        print(json.dumps(run_e2e(dev)), flush=True)
         return
 
     tok = run_token_bench(args, dev)

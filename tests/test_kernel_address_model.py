@@ -1,0 +1,112 @@
+"""CPU model of the addresses the decode step's kernels form, at the real
+shapes of Qwen3-0.6B/8B/14B/32B and the launch shapes the library picks:
+every index a thread can compute stays inside its buffer, and every 32-bit
+byte offset or descriptor range stays below 2^32 (2^31 where the kernel
+treats it as signed).  The formulas are those of k_gemv (rv12_gemv.hip:
+steps 0-6), k_splitk_reduce, k_pick, k_rope_attn and k_attn_combine
+(rv12_attn.hip), written here from the kernels' own index expressions."""
+import ctypes
+
+import pytest
+
+from ai_amd import _lib
+
+MODELS = {  # D, H, KV, HD, FF, V
+    "0.6b": (1024, 16, 8, 128, 3072, 151936),
+    "8b": (4096, 32, 8, 128, 12288, 151936),
+    "14b": (5120, 40, 8, 128, 17408, 151936),
+    "32b": (5120, 64, 8, 128, 25600, 151936),
+}
+U32, I32 = 1 << 32, 1 << 31
+
+
+def _layer_linears(D, H, KV, HD, FF, V):
+    # (name, N, K, mode, rms)
+    return [("qkv", (H + 2 * KV) * HD, D, 0, True), ("o", D, H * HD, 1, False), ("gu", 2 * FF, D, 0, True),
+            ("down", D, FF, 2, False), ("head", V, D, 0, True)]
+
+
+def _shape(N, K, T):
+    c = _lib.Launch()
+    assert _lib.lib().rv12_launch_shape(N, K, T, None, ctypes.byref(c)) == 0
+    return c.kernel, c.rb, c.waves, c.splits
+
+
+@pytest.mark.parametrize("model", sorted(MODELS))
+@pytest.mark.parametrize("T", [1, 2])
+def test_vector_linear_addresses(model, T):
+    D, H, KV, HD, FF, V = MODELS[model]
+    for name, N, K, mode, rms in _layer_linears(D, H, KV, HD, FF, V):
+        kernel, RB, W, S = _shape(N, K, T)
+        if kernel != 1:
+            continue
+        nthr, nsteps = 64 * W, K // 32
+        nblk = (N + 15) // 16
+        grid = (nblk + RB - 1) // RB
+        npad = nblk * 16
+        xs = 2 * K if mode == 2 else K
+        n_exc = N * K // 64  # far above the densest Qwen3 matrix (0.1 % outlier rows give 0.08 %)
+        # step 0: the owner's row, clamped; old y at (min(tok, T-1), row)
+        for blk in (0, grid - 1):
+            n0 = blk * RB * 16
+            for orow in (0, RB * 16 - 1):
+                onc = min(n0 + orow, N - 1)
+                assert 0 <= onc < N and onc + 1 <= N  # rbase[onc], rp[onc], rp[onc + 1]
+                assert (T - 1) * N + onc < T * N
+            assert min(n0 + RB * 16, N) <= N  # rp[...] of the exception range
+        # step 1: activations of split sp, chunk offsets i < krange
+        for sp in (0, S - 1):
+            s_lo, s_hi = sp * nsteps // S, (sp + 1) * nsteps // S
+            assert (sp + 1) * nsteps < U32  # the split bounds are computed in 32 bits
+            k_lo, krange = s_lo * 32, (s_hi - s_lo) * 32
+            i_max = krange - 4
+            k = k_lo + i_max
+            assert k + 3 < K and (T - 1) * xs + (K if mode == 2 else 0) + k + 3 < T * xs
+            if rms:
+                assert k + 3 < K  # lnw (4 bf16 per chunk)
+        # step 2: weights through one descriptor per workgroup: its row blocks' bytes
+        blk_bytes = nsteps * 768
+        assert RB * blk_bytes < U32 and (RB - 1) * blk_bytes + 63 * 12 < I32  # voff is a signed int
+        assert (nsteps - 1) * 768 < I32  # soff
+        # step 3: the exception entries through descriptors of min(n_exc, 2^28) * 4 bytes
+        assert min(n_exc, 1 << 28) * 4 < U32 and (n_exc - 1) * 4 < 0xFFFFFFF0
+        # step 5/6: stores and partials
+        assert (T - 1) * N + N - 1 < T * N
+        if S > 1:
+            assert ((S - 1) * T + T - 1) * npad + npad - 1 < S * T * npad
+            assert (S + 16) * T * npad * 4 < I32  # the reduce's 32-bit byte offsets (host-checked)
+        # fused greedy pick: pairs [T][grid]
+        if name == "head":
+            assert (T - 1) * grid + grid - 1 < T * grid
+
+
+@pytest.mark.parametrize("model", sorted(MODELS))
+def test_decode_attention_addresses(model):
+    D, H, KV, HD, FF, V = MODELS[model]
+    from ai_amd.attn import SPAN, default_splits
+    G = H // KV
+    for maxt, eb in ((2304, 2), (4224, 2), (10240, 2), (2304, 4)):
+        S = default_splits(KV, maxt)
+        assert (maxt + S - 1) // S <= SPAN
+        for pos in (0, maxt // 2, maxt - 1):
+            n = pos + 1
+            assert S * n < U32 and (S + 1) * n < U32  # split bounds in 32 bits
+            for sp in (0, S - 1):
+                lo, hi = sp * n // S, (sp + 1) * n // S
+                assert hi - lo <= SPAN
+                cbytes = min(hi, n - 1) * HD * eb
+                assert cbytes < U32
+                # key quarter rows and value pairs of positions lo..lo+79 (past hi: zeros by the descriptor)
+                assert ((lo + SPAN - 1) * HD + HD - 1) * eb < I32
+            # the step's k/v slot and the caches' rows, 64-bit
+            row0 = (KV - 1) * maxt * HD
+            assert row0 + pos * HD + HD - 1 < KV * maxt * HD
+        # partials [n_kv][S][G][HD + 2] and the combine's ranges
+        part = KV * S * G * (HD + 2)
+        assert ((KV - 1) * S + S - 1) * G * (HD + 2) + G * (HD + 2) - 1 < part
+        stride = G * (HD + 2) * 4
+        assert (S - 1) * stride + (HD + 2) * 4 < U32
+        # batch: T <= 16 rows per token, R = 16 G rows per kv head
+        R = 16 * G
+        assert ((KV - 1) * S + S - 1) * R * (HD + 2) + R * (HD + 2) - 1 < KV * S * R * (HD + 2)
+        assert (S - 1) * R * (HD + 2) * 4 + (HD + 2) * 4 < U32
