@@ -18,7 +18,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "librv12.so")
-SOURCES = ["rv12_codec.hip", "rv12_gemv.hip", "rv12_gemm.hip", "rv12_attn.hip", "rv12_static.hip", "rv12_api.cpp"]
+SOURCES = ["rv12_codec.hip", "rv12_gemv.hip", "rv12_gemm.hip", "rv12_prefill.hip", "rv12_attn.hip", "rv12_static.hip",
+           "rv12_api.cpp"]
 HEADERS = ["rv12_device.h", "rv12_internal.h"]
 MANIFEST = OUT + ".build.json"
 PROBE_OUT = os.path.join(HERE, "librv12probe.so")  # bench.py's stream-ceiling probe (not the product)

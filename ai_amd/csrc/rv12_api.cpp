@@ -472,6 +472,26 @@ int rv12_head_argmax(const rv12_matrix* w, const float* x, int t, const uint16_t
     return launch_status();
 }
 
+size_t rv12_prefill_workspace_bytes(int k, int t) {
+    if (k < 32 || k % 32 || k > kMaxK || t < 1 || t > kMaxPrefillTokens) return 0;
+    return prefill_ws_bytes(k, t);
+}
+
+int rv12_prefill_linear(const rv12_matrix* w, const float* x, float* y, int t, int mode, void* ws, size_t ws_bytes,
+                        void* stream) {
+    int rc = check_matrix(w);
+    if (rc) return rc;
+    if (!x || !y) return RV12_E_NULL;
+    if (mode < 0 || mode > 2) return RV12_E_MODE;
+    if (t < 1 || t > kMaxPrefillTokens) return RV12_E_TOKENS;
+    if (!aligned16(x) || !aligned16(y)) return RV12_E_ALIGN;
+    const size_t need = prefill_ws_bytes(w->k, t);
+    if (!ws || ws_bytes < need) return RV12_E_WORKSPACE;
+    if (!aligned16(ws)) return RV12_E_ALIGN;
+    launch_prefill(*w, x, y, t, mode, ws, (hipStream_t)stream);
+    return launch_status();
+}
+
 int rv12_gemv(const rv12_matrix* w, const float* x, float* y, const uint16_t* lnw, float eps, int mode,
               const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream) {
     return rv12_gemm(w, x, y, 1, lnw, eps, mode, cfg, ws, ws_bytes, stream);

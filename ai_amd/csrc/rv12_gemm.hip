@@ -46,30 +46,8 @@
 
 namespace rv12 {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kGroupsPerThread = 4;  // B-operand groups a thread stages; host: steps <= 4 * waves
-
-__device__ __forceinline__ uint32_t bf16_bits(float v) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v);
-}
-__device__ __forceinline__ float bf16_value(uint32_t b) { return __uint_as_float(b << 16); }
-
-// split 8 values into three bf16x8 parts (as u32x4) with hi + mid + lo = v to 24 bits
-__device__ __forceinline__ void split3(const float (&v)[8], u32x4& hi, u32x4& mid, u32x4& lo) {
-    uint32_t h[8], m[8], l[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        h[e] = bf16_bits(v[e]);
-        const float r1 = v[e] - bf16_value(h[e]);
-        m[e] = bf16_bits(r1);
-        const float r2 = r1 - bf16_value(m[e]);
-        l[e] = bf16_bits(r2);
-    }
-    hi = u32x4{h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16};
-    mid = u32x4{m[0] | m[1] << 16, m[2] | m[3] << 16, m[4] | m[5] << 16, m[6] | m[7] << 16};
-    lo = u32x4{l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16};
-}
 
 template <int RBW>
 __device__ __forceinline__ void issue_rows(u32x3 (&dst)[RBW], __amdgpu_buffer_rsrc_t rv,
@@ -80,10 +58,6 @@ __device__ __forceinline__ void issue_rows(u32x3 (&dst)[RBW], __amdgpu_buffer_rs
     for (int b = 0; b < RBW; ++b) dst[b] = load_group(r, voff[b], soff);
 }
 
-__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-}
 
 // M2: silu(g) * u prologue (MODE 2); LN: RMSNorm weight.  Template arguments,
 // so that the activation loads of step 1 are straight-line code that waits for

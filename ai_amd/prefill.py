@@ -8,18 +8,17 @@ dense GEMM, instead of passes of 16 tokens through the fused decode-linear.
     matrix(x, c, y, add)                             prefill.py:66-78
     layer(eng, l, weights, x, start, kc, vc, gguf)   prefill.py:81-121 (same signature)
 
-MI355X form of `matrix`: the 12-bit matrix is decoded to its exact bf16 bits
-(rv12_decode_rows), and the fp32 activations are split into three bf16 parts
-x = hi + mid + lo (the reference's own split for bf16 matrix units,
-ramvi/engine/ramvi_engine/kernels/wcomp.py:130-140; the parts carry all 24
-significand bits of a normal fp32 value).  One hipBLASLt GEMM over the stacked
-parts [hi; mid; lo] (3T x K) with fp32 output runs on the bf16 MFMA units;
-every product w * part is exact in fp32 and the sums are fp32, and
-(hi + mid) + lo is added in fp32.  The reference computes the same sums with
-IEEE fp32 products (prefill_kernels.py:8-26, input_precision='ieee'); both
-are fp32 evaluations of the same closed form, held to the same error bound in
-the tests.  The decode of a matrix is bit-exact, so the weights are the
-reference's, not a re-quantisation.
+MI355X form of `matrix`: one fused kernel chain in librv12
+(rv12_prefill_linear): the fp32 activations of all prompt tokens are split
+once into three bf16 parts (24 significand bits, after an exact per-token
+power-of-two scale, the reference's own split for bf16 matrix units,
+ramvi/engine/ramvi_engine/kernels/wcomp.py:130-140), and a hand-written
+bf16 MFMA GEMM reads each weight once in its 12-bit packed form (the Q16
+tiles are the MFMA's A operand), accumulates in fp32 and adds the
+exceptions; no wider copy of W is ever written.  The reference computes the
+same sums with IEEE fp32 products after decoding W to fp32
+(prefill_kernels.py:8-26, 58-110); both are fp32 evaluations of the same
+closed form, held to the same error bound in the tests.
 
 Attention over the prompt (prefill_kernels.py:35-60, att_k) is the same causal
 softmax in fp32, computed in query blocks of ATT_BLOCK tokens with fp32 IEEE
@@ -46,29 +45,37 @@ def enabled(n=None):
     return mode == "blocked" and (n is None or n >= minimum)
 
 
-def split3(x):
-    """fp32 [T, K] -> bf16 [3T, K]: hi, mid, lo with hi + mid + lo = x."""
-    hi = x.bfloat16()
-    r = x - hi.float()
-    mid = r.bfloat16()
-    lo = (r - mid.float()).bfloat16()
-    return torch.cat([hi, mid, lo], 0)
+_WS = {}  # device -> workspace of the prefill linear (the split activations)
+
+
+def _linear(x, c, y, mode):
+    """y (=|+=) W x' over every token row of x (fp32 [T, K], [T, 2K] in mode 2)."""
+    import ctypes
+    from . import _lib
+    T = x.shape[0]
+    K, N = int(c["K"]), int(c["N"])
+    if x.dtype != torch.float32 or y.dtype != torch.float32 or not x.is_contiguous() or not y.is_contiguous():
+        raise ValueError("prefill: x and y must be contiguous float32")
+    if x.shape[1] != (2 * K if mode == 2 else K) or y.numel() < T * N:
+        raise ValueError("prefill: x or y has the wrong shape")
+    L = _lib.lib()
+    need = L.rv12_prefill_workspace_bytes(K, T)
+    if need == 0:
+        raise ValueError("prefill: too many tokens")
+    key = str(x.device)
+    if key not in _WS or _WS[key].numel() < need:
+        _WS[key] = torch.empty(need, dtype=torch.uint8, device=x.device)
+    ws = _WS[key]
+    rc = L.rv12_prefill_linear(ctypes.byref(wcomp._matrix(c)), ctypes.c_void_p(x.data_ptr()),
+                               ctypes.c_void_p(y.data_ptr()), T, int(mode), ctypes.c_void_p(ws.data_ptr()),
+                               ws.numel(), ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream))
+    _lib.check(rc, "prefill")
 
 
 def matrix(x, c, y, add=False):
-    """y (=|+=) x . W^T for every token row of x (fp32 [T, K]); W decoded
-    exactly from the 12-bit codec (prefill.py:66-78)."""
-    T = x.shape[0]
-    N = int(c["N"])
-    w = wcomp.decode_rows(c, 0, N, torch.bfloat16)  # exact bf16 bits of W
-    parts = torch.mm(split3(x), w.t(), out_dtype=torch.float32)  # [3T, N]
-    del w
-    v = parts[:T]
-    v.add_(parts[T:2 * T]).add_(parts[2 * T:])
-    if add:
-        y.add_(v)
-    else:
-        y.copy_(v)
+    """y (=|+=) x . W^T for every token row of x (fp32 [T, K]); W read once
+    in its 12-bit form (prefill.py:66-78)."""
+    _linear(x, c, y, 1 if add else 0)
 
 
 def _rms(x, w, eps):
@@ -146,7 +153,5 @@ def layer(eng, l, weights, x, start, kc, vc, gguf=False):
     gu = torch.empty(T, 2 * FF, device=x.device)
     matrix(norm, W["gu"], gu)
     del norm
-    g = gu[:, :FF]
-    mid = g / (1.0 + torch.exp(-g)) * gu[:, FF:]
+    _linear(gu, W["down"], x, 2)  # silu(g) * u fused into the linear's prologue
     del gu
-    matrix(mid, W["down"], x, add=True)

@@ -207,6 +207,21 @@ size_t rv12_head_workspace_bytes(int n, int k, int t, const rv12_launch* cfg);
 int rv12_gemm_static(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps,
                      int mode, const rv12_launch* cfg, void* stream);
 
+/* The prompt's linear, 1 <= t <= 65536 tokens at once:  y[r] (=|+=) W_dec . x'[r]
+ * for every token row r (x rows K floats apart, 2K in mode 2; y rows N apart),
+ * mode as rv12_gemv.  The 12-bit decode is fused into a bf16 MFMA GEMM:
+ * x' is split per token into three bf16 parts (24 significand bits, after an
+ * exact power-of-two scale), every weight is read once in its 12-bit form,
+ * products and sums are fp32, the exceptions are added in list order.  ws:
+ * rv12_prefill_workspace_bytes(k, t) bytes (6 bytes per column and padded
+ * token, the parts), 16-byte aligned.  Replaces the blocked prefill's
+ * matrix() (decode_rows + the fp32 GEMM mm_k),
+ * ramvi/engine/ramvi_engine/kernels/prefill.py:66-78,
+ * ramvi/engine/ramvi_engine/kernels/prefill_kernels.py:8-26, 58-110. */
+size_t rv12_prefill_workspace_bytes(int k, int t);
+int rv12_prefill_linear(const rv12_matrix* w, const float* x, float* y, int t, int mode, void* ws, size_t ws_bytes,
+                        void* stream);
+
 /* Bit-exact decode of rows [first, last) to bf16 bits (out_f32 == 0, out is
  * uint16[last-first, K]) or to float32 (out_f32 != 0, out is float[last-first, K]).
  * Replaces decode_rows / dequant_k TYPE 0 + exceptions_k,

@@ -1,9 +1,11 @@
-"""GPU parity of the blocked prefill's GEMM (ai_amd.prefill.matrix: exact
-bf16 decode of the 12-bit matrix, three-part bf16 split of the fp32
-activations, one hipBLASLt GEMM with fp32 output) against the oracle's float64
-closed form: 1e-3 abs + 1e-2 rel and 4x the fp32 forward-error bound, for
-store and residual add, on the golden matrices and on a matrix with
-exceptions in many rows."""
+"""GPU parity of the blocked prefill's linear (ai_amd.prefill.matrix ->
+rv12_prefill_linear: the 12-bit decode fused into a bf16x3 MFMA GEMM over all
+tokens) against the oracle's float64 closed form: 1e-3 abs + 1e-2 rel and 4x
+the fp32 forward-error bound, for store, residual add and the silu(g) * u
+prologue, ragged token counts and row counts, on the golden matrices, a
+matrix with exceptions in many rows, activations of very different scales,
+and (at the Qwen3-8B gu shape over 2048 tokens, beyond what the float64
+oracle finishes in seconds) sampled rows against the decode kernels."""
 import numpy as np
 import pytest
 import torch
@@ -14,26 +16,36 @@ from oracle import codec, linear
 pytestmark = pytest.mark.gpu
 
 
-def _check(cnp, T, seed, add):
+def _check(cnp, T, seed, add, mode=None, scales=None):
     from ai_amd import prefill, wcomp
     rng = np.random.default_rng(seed)
     N, K = cnp["N"], cnp["K"]
-    X = (rng.standard_normal((T, K)) * 2).astype(np.float32)
+    mode = (1 if add else 0) if mode is None else mode
+    X = rng.standard_normal((T, 2 * K if mode == 2 else K)) * 2
+    if scales is not None:  # MODE 2: g and u each by the square root, so that x' ~ the scale
+        sc = np.asarray(scales, np.float64)[:T, None]
+        X *= np.sqrt(sc) if mode == 2 else sc
+    X = X.astype(np.float32)
     Y0 = rng.standard_normal((T, N)).astype(np.float32)
     W = codec.decode_f32(cnp).astype(np.float64)
-    ref = linear.linear(cnp, X, 1 if add else 0, Y0 if add else None, W=W)
-    bound = linear.error_bound(cnp, X, 0, W=W)
+    ref = linear.linear(cnp, X, mode, Y0 if mode else None, W=W)
+    bound = linear.error_bound(cnp, X, mode, W=W)
     c = wcomp.prepare({k: (torch.from_numpy(np.ascontiguousarray(v)) if isinstance(v, np.ndarray) else v)
                        for k, v in cnp.items()})
     y = torch.from_numpy(Y0.copy()).cuda()
-    prefill.matrix(torch.from_numpy(X).cuda(), c, y, add=add)
+    if mode == 2:
+        prefill._linear(torch.from_numpy(X).cuda(), c, y, 2)
+    else:
+        prefill.matrix(torch.from_numpy(X).cuda(), c, y, add=add)
     torch.cuda.synchronize()
     got = y.cpu().numpy().astype(np.float64)
     fin = np.isfinite(ref)
     assert np.array_equal(np.isnan(got), np.isnan(ref))
     err = np.abs(got[fin] - ref[fin])
     assert np.all(err <= 1e-3 + 1e-2 * np.abs(ref[fin])), float(err.max())
-    assert np.all(err <= 4 * bound[fin] + 1e-30), float((err - 4 * bound[fin]).max())
+    # plus the rounding of the final add into y (2^-23 |y|) where y is accumulated
+    tight = 4 * bound[fin] + (2.0 ** -23 * np.abs(ref[fin]) if mode else 0.0) + 1e-30
+    assert np.all(err <= tight), float((err - tight).max())
 
 
 @pytest.mark.parametrize("case", ["prefill_seed7", "outliers_rows_cols", "chunk128", "subnormal_heavy"])
@@ -53,3 +65,62 @@ def test_matrix_with_exceptions_in_many_rows():
     cnp = codec.compress(codec.f32_to_bf16_rne(w))
     assert cnp["er"].size > 100
     _check(cnp, 513, 2, True)
+
+
+@pytest.mark.parametrize("T", [1, 17, 128, 129, 300])
+def test_ragged_tokens_rows_and_modes(T):
+    """Token counts around the 128-token tile, a row count that is not a
+    multiple of the 256-row tile, every mode."""
+    rng = np.random.default_rng(T)
+    w = (rng.standard_normal((300, 512)) * 0.02).astype(np.float32)
+    w[rng.choice(300, 2)] *= 20
+    cnp = codec.compress(codec.f32_to_bf16_rne(w))
+    for mode in (0, 1, 2):
+        print("T", T, "mode", mode, flush=True)
+        _check(cnp, T, T + mode, mode != 0, mode=mode)
+
+
+def test_token_scales():
+    """Tokens scaled by 2^-60 .. 2^60 (and one of zeros) in one prompt: each
+    token's exact power-of-two scale keeps the fp32 bound."""
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((200, 1024)) * 0.02).astype(np.float32)
+    cnp = codec.compress(codec.f32_to_bf16_rne(w))
+    T = 40
+    scales = [2.0 ** e for e in np.linspace(-60, 60, T)]
+    scales[7] = 0.0
+    for mode in (0, 2):
+        _check(cnp, T, 11 + mode, False, mode=mode, scales=scales)
+
+
+def test_qwen3_8b_gu_2048_tokens_against_the_decode_kernels():
+    """The 24576 x 4096 gu matrix over 2048 tokens: sampled token rows equal
+    the MFMA decode-linear's (rv12_gemm at 16 tokens) within the tolerance,
+    and a 64-token slice of rows equals the float64 closed form."""
+    from ai_amd import prefill, wcomp
+    g = torch.Generator(device="cuda").manual_seed(8)
+    N, K, T = 24576, 4096, 2048
+    w = (torch.randn(N, K, device="cuda", generator=g) * 0.02)
+    w[torch.randperm(N, device="cuda", generator=g)[:24]] *= 20
+    w = w.bfloat16()
+    c = wcomp.compress(w)
+    x = torch.randn(T, K, device="cuda", generator=g)
+    y = torch.zeros(T, N, device="cuda")
+    prefill.matrix(x, c, y)
+    pick = torch.tensor([0, 1, 127, 128, 1000, 1777, 2046, 2047, 5, 6, 7, 8, 9, 10, 11, 12], device="cuda")
+    xs = x[pick].contiguous()
+    ys = torch.zeros(16, N, device="cuda")
+    wcomp.gemvc_tc(xs, c, ys, 0, 16)
+    torch.cuda.synchronize()
+    ref = ys.cpu().numpy().astype(np.float64)
+    got = y[pick].cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 1e-3 + 1e-2 * np.abs(ref)), float(np.abs(got - ref).max())
+    # 64 rows against float64
+    rows = slice(4096, 4160)
+    W64 = w[rows].float().cpu().numpy().astype(np.float64)
+    want = x[:64].cpu().numpy().astype(np.float64) @ W64.T
+    mag = np.abs(x[:64].cpu().numpy().astype(np.float64)) @ np.abs(W64).T
+    err = np.abs(y[:64, rows].cpu().numpy() - want)
+    assert np.all(err <= 4 * (K + 8) * 2.0 ** -24 * mag + 1e-30), float(err.max())
+    del c, w, x, y
+    torch.cuda.empty_cache()
