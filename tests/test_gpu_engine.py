@@ -111,6 +111,42 @@ def test_qwen3_8b_2048_prompt_64_tokens_bf16_cache():
            oracle_device="cuda")
 
 
+def test_qwen3_8b_architecture_4_layers_2048_prompt_bf16_cache():
+    """Qwen3-8B dimensions (every matrix at its full 8B shape, the 151936 x
+    4096 head) with 4 of its 36 layers, random init: 2048-token random prompt
+    through the blocked prefill, bf16 KV cache, context as the benchmark's
+    (2304 positions), the first 64 greedy ids equal to the fp32 oracle's,
+    which runs on the CPU."""
+    from ai_amd.model import QWEN3, RandomCkpt
+    print("qwen3-8b architecture, 4 layers", flush=True)
+    ck = RandomCkpt(dict(QWEN3["8b"], num_hidden_layers=4), seed=0)
+    prompt = [int(t) for t in np.random.default_rng(0).integers(0, ck.V, 2048)]
+    _check(ck, prompt, 64, kv_dtype=torch.bfloat16, maxt=2048 + 256, prefill="blocked", prefill_min=256)
+
+
+def test_qwen3_32b_architecture_2_layers_4096_prompt_and_8_token_pass():
+    """Qwen3-32B dimensions with 2 of its 64 layers, random init: 4096-token
+    random prompt, bf16 KV cache, the first 16 greedy ids equal to the fp32
+    oracle's (on the CPU); then the reference's batch of 8 (one _batch_layer
+    pass of 8 tokens of the sequence, as speculative verification runs it)
+    picks the same ids as 8 single-token steps."""
+    from ai_amd.model import QWEN3, RandomCkpt
+    print("qwen3-32b architecture, 2 layers", flush=True)
+    ck = RandomCkpt(dict(QWEN3["32b"], num_hidden_layers=2), seed=0)
+    P = 4096
+    prompt = [int(t) for t in np.random.default_rng(0).integers(0, ck.V, P)]
+    ids, eng = _check(ck, prompt, 16, kv_dtype=torch.bfloat16, maxt=P + 128 + 8, prefill="blocked",
+                      prefill_min=256, keep=True)
+    eng.reset()
+    first = eng.prefill(prompt).tolist()
+    assert first == ids[:1]
+    got = eng.process(ids[:8], P)
+    print("8-token pass", got, "single steps", ids[1:9], flush=True)
+    assert got == ids[1:9]
+    del eng
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.skip(reason=OFF_GPU)
 def test_qwen3_32b_4096_prompt_and_8_token_pass():
     """Qwen3-32B architecture, random init, held in HBM: 4096-token random
