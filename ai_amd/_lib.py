@@ -25,9 +25,10 @@ EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_pack_p
            "rv12_codec_to_bf16", "rv12_encode_stats", "rv12_encode", "rv12_encode_exc", "rv12_launch_shape",
            "rv12_workspace_bytes", "rv12_launch_workspace_bytes", "rv12_head_argmax", "rv12_head_workspace_bytes",
            "rv12_gemv", "rv12_gemm", "rv12_gemm_static", "rv12_decode_rows", "rv12_attn_workspace_bytes", "rv12_rope_attn",
-           "rv12_attn_batch_workspace_bytes", "rv12_rope_attn_batch", "rv12_prefill_workspace_bytes",
+           "rv12_attn_batch_workspace_bytes", "rv12_rope_attn_batch", "rv12_prefill_attn_workspace_bytes",
+           "rv12_prefill_rope_attn", "rv12_prefill_workspace_bytes",
            "rv12_prefill_linear")
-ABI_VERSION = 4
+ABI_VERSION = 5
 STATIC_SCRATCH_BYTES = 8 << 20  # RV12_STATIC_SCRATCH_BYTES
 
 
@@ -126,6 +127,10 @@ def lib():
         L.rv12_attn_batch_workspace_bytes.argtypes = [ctypes.POINTER(Attn), I]
         L.rv12_rope_attn_batch.restype = I
         L.rv12_rope_attn_batch.argtypes = [ctypes.POINTER(Attn), I, P, P, P, P, P, P, P, P, P, SZ, P]
+        L.rv12_prefill_attn_workspace_bytes.restype = SZ
+        L.rv12_prefill_attn_workspace_bytes.argtypes = [ctypes.POINTER(Attn), I]
+        L.rv12_prefill_rope_attn.restype = I
+        L.rv12_prefill_rope_attn.argtypes = [ctypes.POINTER(Attn), I, P, P, P, P, P, P, P, P, P, SZ, P]
         v = L.rv12_abi_version()
         if v != ABI_VERSION:
             raise RuntimeError(f"librv12.so ABI version {v}, expected {ABI_VERSION}")

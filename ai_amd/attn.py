@@ -3,7 +3,10 @@ device-side position, K/V into the cache, grouped-query attention.  One token
 (rv12_rope_attn: the reference's rope_attn_k,
 ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213) or a batch of up to 16
 tokens of one sequence, each attending causally (rv12_rope_attn_batch: the
-reference's qk_rope_cache_k + attn_k, tkernels.py:82-150)."""
+reference's qk_rope_cache_k + attn_k, tkernels.py:82-150), or a whole prompt
+block (rv12_prefill_rope_attn: qk_rope_cache_k + att_k of the blocked prefill,
+ramvi/engine/ramvi_engine/kernels/prefill.py:100-103,
+prefill_kernels.py:29-54)."""
 import ctypes
 
 import torch
@@ -64,3 +67,26 @@ class RopeAttn:
                                         p(vc), p(out), p(self.wsb), self.wsb.numel(),
                                         ctypes.c_void_p(torch.cuda.current_stream(qkv.device).cuda_stream))
         check(rc, "rope_attn_batch")
+
+    def prefill(self, qkv, qn, kn, inv, pos, kc, vc, out, T):
+        """A prompt block of T tokens at positions pos .. pos + T - 1 (pos a
+        device int64): rows of qkv in, rows of out written; K/V of the T
+        positions into the caches.  The q rows live in a workspace kept for
+        the largest T seen."""
+        for t in (qkv, qn, kn, inv, out):
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                raise ValueError("qkv, qn, kn, inv and out must be contiguous float32")
+        if pos.dtype != torch.int64:
+            raise ValueError("pos must be int64")
+        L = lib()
+        need = L.rv12_prefill_attn_workspace_bytes(ctypes.byref(self.a), int(T))
+        if need == 0:
+            raise ValueError("prefill attention: unsupported block (tokens, context or head size)")
+        ws = getattr(self, "wsp", None)
+        if ws is None or ws.numel() < need:
+            ws = self.wsp = torch.empty(need, dtype=torch.uint8, device=qkv.device)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())
+        rc = L.rv12_prefill_rope_attn(ctypes.byref(self.a), int(T), p(qkv), p(qn), p(kn), p(inv), p(pos), p(kc),
+                                      p(vc), p(out), p(ws), ws.numel(),
+                                      ctypes.c_void_p(torch.cuda.current_stream(qkv.device).cuda_stream))
+        check(rc, "prefill_rope_attn")

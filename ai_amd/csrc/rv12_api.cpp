@@ -599,4 +599,58 @@ int rv12_rope_attn_batch(const rv12_attn* a, int t, const float* qkv, const floa
     return launch_status();
 }
 
+
+// the prompt attention ignores splits: its workgroups cover 16 tokens, not a
+// position range; every 32-bit byte offset of its loads stays below 2^31
+static int check_prefill_attn(const rv12_attn* a, int t) {
+    if (!a) return RV12_E_NULL;
+    if (a->head_dim != 64 && a->head_dim != 128) return RV12_E_SHAPE;
+    if (a->n_kv < 1 || a->n_heads < a->n_kv || a->n_heads % a->n_kv) return RV12_E_SHAPE;
+    const int g = a->n_heads / a->n_kv;
+    if (g != 1 && g != 2 && g != 4 && g != 8) return RV12_E_SHAPE;
+    if (a->maxt < 1 || (int64_t)a->maxt * a->head_dim * (a->kv_bf16 ? 2 : 4) >= ((int64_t)1 << 31))
+        return RV12_E_SHAPE;
+    if (t < 1 || t > kMaxPrefillAttnTokens || (int64_t)(t + 15) * a->n_heads * a->head_dim * 4 >= ((int64_t)1 << 31))
+        return RV12_E_TOKENS;
+    return RV12_OK;
+}
+
+size_t rv12_prefill_attn_workspace_bytes(const rv12_attn* a, int t) {
+    if (check_prefill_attn(a, t)) return 0;
+    return (size_t)t * a->n_heads * a->head_dim * 4;
+}
+
+int rv12_prefill_rope_attn(const rv12_attn* a, int t, const float* qkv, const float* qn, const float* kn,
+                           const float* inv, const int64_t* pos, void* kc, void* vc, float* out, void* ws,
+                           size_t ws_bytes, void* stream) {
+    int rc = check_prefill_attn(a, t);
+    if (rc) return rc;
+    if (!qkv || !qn || !kn || !inv || !pos || !kc || !vc || !out) return RV12_E_NULL;
+    if (!aligned16(qkv) || !aligned16(kc) || !aligned16(vc) || !aligned16(out)) return RV12_E_ALIGN;
+    const size_t need = rv12_prefill_attn_workspace_bytes(a, t);
+    if (!ws || ws_bytes < need) return RV12_E_WORKSPACE;
+    if (!aligned16(ws)) return RV12_E_ALIGN;
+    AttnParams p;
+    p.qkv = qkv;
+    p.qn = qn;
+    p.kn = kn;
+    p.inv = inv;
+    p.pos = pos;
+    p.kc = kc;
+    p.vc = vc;
+    p.out = out;
+    p.qo = (float*)ws;
+    p.part = nullptr;
+    p.n_heads = a->n_heads;
+    p.n_kv = a->n_kv;
+    p.head_dim = a->head_dim;
+    p.maxt = a->maxt;
+    p.kv_bf16 = a->kv_bf16 ? 1 : 0;
+    p.eps = a->eps;
+    p.scale = a->scale;
+    p.T = t;
+    if (launch_prefill_attn(p, (hipStream_t)stream)) return RV12_E_CONFIG;
+    return launch_status();
+}
+
 }  // extern "C"

@@ -622,6 +622,197 @@ static void launch_batch_t(const AttnParams& p, int S, hipStream_t st) {
                        dim3(kAttnThreads), lds, st, p);
 }
 
+// ---------------------------------------------------------------------------
+// Prompt attention (the blocked prefill's att_k,
+// ramvi/engine/ramvi_engine/kernels/prefill_kernels.py:29-54): token r of a
+// block of T at positions p0 .. p0 + T - 1 attends over positions
+// 0 .. p0 + r with float32 products (the reference's input_precision='ieee')
+// on the float32 matrix cores, v_mfma_f32_16x16x4_f32 (lane l: A row l%16,
+// B column l%16, k = l/16; result rows 4(l/16) + 0..3, column l%16).
+//
+// Grid (token tiles of 16, kv heads), the last tile first (it has the most
+// positions); workgroup = the G query heads of kv head g, one wave per head,
+// all reading the same cache rows.  Per block of 16 positions a wave computes
+// the scores transposed, S^T = K . Q^T (rows = positions, columns = its 16
+// tokens), so each lane holds 4 positions of one token: the online softmax
+// (running max m, rescale exp(m_old - m_new), running sum) needs two lane
+// exchanges per block and no LDS.  The sums over dims and positions run in
+// an order of our choosing, the same for both operands:
+//   scores  MFMA t = 8a + b, k slot q: dim 32a + 8q + b, so lane l loads the
+//           8 consecutive dims 32a + 8(l/16) .. +7 of its position l%16 (and
+//           of its token's q) with one 16-byte (32-byte for float32) load;
+//   values  O^T = V^T . P^T over output dim tiles dt: tile row r is dim
+//           DT r + dt (DT = HD / 16), k slot q of MFMA j is position 4q + j,
+//           so lane l loads the DT consecutive dims DT (l%16) .. of position
+//           4(l/16) + j, and P^T's operand is the lane's own probability j.
+// The caches are read through descriptors ending at position p0 + T, the q
+// rows through one ending at row T: tokens and positions past the block
+// read zeros, are masked (-inf scores) and never stored.
+template <int HD, bool BF16>
+__global__ __launch_bounds__(512) void k_prefill_attn(AttnParams p) {
+    constexpr int EB = BF16 ? 2 : 4;    // cache bytes per value
+    constexpr int NA = HD / 32;         // 8-dim score chunks per lane
+    constexpr int DT = HD / 16;         // output dim tiles = value dims per lane
+    constexpr int KWD = 8 * EB / 4;     // words of one 8-dim key chunk
+    constexpr int VWD = DT * EB / 4;    // words of one lane's value dims
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int q4 = lane >> 4, c16 = lane & 15;
+    const int H = p.n_heads, KV = p.n_kv, G = H / KV;
+    const int g = blockIdx.y, h = g * G + wv;
+    const int T = p.T;
+    const int ntile = (T + 15) >> 4;
+    const int t0 = (ntile - 1 - (int)blockIdx.x) * 16;
+    const int tq = t0 + c16;  // this lane's token
+    const int64_t p0 = *p.pos;
+    float* orow = p.out + (int64_t)min(tq, T - 1) * H * HD + h * HD;
+    if (p0 < 0 || p0 + T > p.maxt) {  // a block outside the cache: zeros, as the prologue writes nothing
+        if (tq < T && q4 == 0)
+            for (int d = 0; d < HD; ++d) orow[d] = 0.0f;
+        return;
+    }
+    const int n = (int)p0 + T;  // positions in the cache after the block
+    const uint32_t head_bytes = (uint32_t)n * HD * EB;
+    const char* kbase = reinterpret_cast<const char*>(p.kc) + (int64_t)g * p.maxt * HD * EB;
+    const char* vbase = reinterpret_cast<const char*>(p.vc) + (int64_t)g * p.maxt * HD * EB;
+    const __amdgpu_buffer_rsrc_t rk = attn_rsrc(kbase, head_bytes), rv = attn_rsrc(vbase, head_bytes);
+    const __amdgpu_buffer_rsrc_t rq = attn_rsrc(p.qo, (uint32_t)T * H * HD * 4);
+
+    // q of (tq, h): the B operand of the score MFMAs
+    float qv[NA][8];
+    {
+        const int qoff = ((tq * H + h) * HD + 8 * q4) * 4;
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + a * 128 + c * 16, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qv[a][4 * c + e] = __uint_as_float(v[e]);
+            }
+        }
+    }
+    const int last = min((int)p0 + t0 + 15, n - 1);  // last position any token of the tile sees
+    const int nkb = last / 16 + 1;
+
+    uint32_t kw[NA][KWD], vw[4][VWD];
+    auto load_block = [&](int kb) {
+        const int koff = ((kb * 16 + c16) * HD + 8 * q4) * EB;
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+#pragma unroll
+            for (int c = 0; c < KWD / 4; ++c) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + a * 32 * EB + c * 16, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kw[a][4 * c + e] = v[e];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int voff = ((kb * 16 + 4 * q4 + j) * HD + DT * c16) * EB;
+            if constexpr (VWD == 2) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, 0, 0);
+                vw[j][0] = v[0];
+                vw[j][1] = v[1];
+            } else {
+#pragma unroll
+                for (int c = 0; c < VWD / 4; ++c) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rv, voff + c * 16, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) vw[j][4 * c + e] = v[e];
+                }
+            }
+        }
+    };
+    auto word_f = [](const uint32_t* w, int i) -> float {
+        if constexpr (BF16) return __uint_as_float((i & 1) ? (w[i >> 1] & 0xFFFF0000u) : (w[i >> 1] << 16));
+        else return __uint_as_float(w[i]);
+    };
+
+    f32x4 o[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    const int qpos = (int)p0 + tq;  // the last position this lane's token sees
+    load_block(0);
+    for (int kb = 0; kb < nkb; ++kb) {
+        uint32_t kcur[NA][KWD], vcur[4][VWD];
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int i = 0; i < KWD; ++i) kcur[a][i] = kw[a][i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < VWD; ++i) vcur[j][i] = vw[j][i];
+        if (kb + 1 < nkb) load_block(kb + 1);
+        // scores of positions kb 16 + 4 q4 + r for token tq
+        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int b = 0; b < 8; ++b) s = __builtin_amdgcn_mfma_f32_16x16x4f32(word_f(kcur[a], b), qv[a][b], s, 0, 0, 0);
+        float sc[4], pr[4];
+        float mb = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int pos = kb * 16 + 4 * q4 + r;
+            sc[r] = (pos <= qpos && pos < n) ? s[r] * p.scale : -INFINITY;
+            mb = fmaxf(mb, sc[r]);
+        }
+        mb = fmaxf(mb, __shfl_xor(mb, 16));
+        mb = fmaxf(mb, __shfl_xor(mb, 32));
+        const float mn = fmaxf(m, mb);  // finite from block 0 on: position 0 is seen by every token
+        const float alpha = expf(m - mn);
+        float ls = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pr[r] = expf(sc[r] - mn);
+            ls += pr[r];
+        }
+        l = l * alpha + ls;
+        m = mn;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+            o[d] *= alpha;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(word_f(vcur[j], d), pr[j], o[d], 0, 0, 0);
+        }
+    }
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (tq < T) {
+        // lane l holds dims DT (4 q4 + r) + dt of its token
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float* dst = orow + DT * (4 * q4 + r);
+#pragma unroll
+            for (int d4 = 0; d4 < DT; d4 += 4)
+                *reinterpret_cast<f32x4*>(dst + d4) =
+                    f32x4{o[d4][r] / l, o[d4 + 1][r] / l, o[d4 + 2][r] / l, o[d4 + 3][r] / l};
+        }
+    }
+}
+
+template <int HD, bool BF16>
+static void launch_prefill_t(const AttnParams& p, hipStream_t st) {
+    hipLaunchKernelGGL((k_qk_rope_cache<HD, BF16>), dim3(p.n_heads + 2 * p.n_kv, p.T), dim3(64), 0, st, p);
+    hipLaunchKernelGGL((k_prefill_attn<HD, BF16>), dim3((p.T + 15) / 16, p.n_kv),
+                       dim3(64 * (p.n_heads / p.n_kv)), 0, st, p);
+}
+
+int launch_prefill_attn(const AttnParams& p, hipStream_t st) {
+    if (p.head_dim == 128) {
+        if (p.kv_bf16) launch_prefill_t<128, true>(p, st);
+        else launch_prefill_t<128, false>(p, st);
+    } else if (p.head_dim == 64) {
+        if (p.kv_bf16) launch_prefill_t<64, true>(p, st);
+        else launch_prefill_t<64, false>(p, st);
+    } else {
+        return -1;
+    }
+    return 0;
+}
+
 int launch_attn_batch(const AttnParams& p, int S, hipStream_t st) {
     if (p.head_dim == 128) {
         if (p.kv_bf16) launch_batch_t<128, true>(p, S, st);

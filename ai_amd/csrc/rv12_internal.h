@@ -121,6 +121,10 @@ inline size_t attn_batch_lds_bytes(int hd) {
                 2 * kAttnRows + pg * kAttnRows * hd);
 }
 int launch_attn_batch(const AttnParams& p, int splits, hipStream_t st);
+// prompt block of T tokens: the q/k/v prologue, then causal attention on the
+// float32 matrix cores (one wave per head and 16 tokens)
+constexpr int kMaxPrefillAttnTokens = 1 << 15;  // the prologue grid's second dimension stays below 65536
+int launch_prefill_attn(const AttnParams& p, hipStream_t st);
 
 int launch_gemv(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st);
 int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st);

@@ -20,17 +20,17 @@ same sums with IEEE fp32 products after decoding W to fp32
 (prefill_kernels.py:8-26, 58-110); both are fp32 evaluations of the same
 closed form, held to the same error bound in the tests.
 
-Attention over the prompt (prefill_kernels.py:35-60, att_k) is the same causal
-softmax in fp32, computed in query blocks of ATT_BLOCK tokens with fp32 IEEE
-batched products over the whole cache prefix.
+The q/k head norms, RoPE, the cache writes and the attention over the prompt
+(qk_rope_cache_k, tkernels.py:82-150, and att_k, prefill_kernels.py:29-54)
+are one library call, rv12_prefill_rope_attn: the same causal softmax with
+float32 products, on the float32 matrix cores.
 """
 import os
 
 import torch
 
 from . import wcomp
-
-ATT_BLOCK = 256  # query tokens per attention block
+from .attn import RopeAttn
 
 
 def enabled(n=None):
@@ -82,36 +82,22 @@ def _rms(x, w, eps):
     return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
 
 
-def _rot(t):
-    h = t.shape[-1] // 2
-    return torch.cat([-t[..., h:], t[..., :h]], -1)
+_ATT = {}  # (dimensions, cache, device) -> RopeAttn launch parameters and workspace
+_POS = {}  # device -> the block's first position (int64 on the device)
 
 
-def attention(eng, q, start, kc, vc):
-    """Causal grouped-query attention of the T prompt rows q (fp32 [T, H, HD],
-    positions start..start+T-1) over positions 0..start+T-1 of the caches
-    kc / vc [KV, maxt, HD], in query blocks (prefill_kernels.py:35-60)."""
-    T = q.shape[0]
-    H, KV, HD = eng.H, eng.KV, eng.HD
-    G = H // KV
-    n = start + T
-    Kf = kc[:, :n].float()                             # [KV, n, HD]
-    Kt = Kf.transpose(1, 2).contiguous()               # [KV, HD, n]
-    Vf = vc[:, :n].float().contiguous()                # [KV, n, HD]
-    del Kf
-    out = torch.empty(T, H * HD, device=q.device)
-    cols = torch.arange(n, device=q.device)
-    for b0 in range(0, T, ATT_BLOCK):
-        b1 = min(T, b0 + ATT_BLOCK)
-        tb = b1 - b0
-        qg = q[b0:b1].view(tb, KV, G, HD).permute(1, 2, 0, 3).reshape(KV, G * tb, HD)
-        sc = torch.bmm(qg, Kt).view(KV, G, tb, n) * HD ** -0.5
-        rows = start + torch.arange(b0, b1, device=q.device)
-        sc.masked_fill_(cols[None, None, None, :] > rows[None, None, :, None], float("-inf"))
-        a = torch.softmax(sc, -1).view(KV, G * tb, n)
-        o = torch.bmm(a, Vf).view(KV, G, tb, HD).permute(2, 0, 1, 3).reshape(tb, H * HD)
-        out[b0:b1].copy_(o)
-    return out
+def _attn(eng, kc):
+    key = (eng.H, eng.KV, eng.HD, kc.shape[1], kc.dtype, float(eng.eps), str(kc.device))
+    if key not in _ATT:
+        _ATT[key] = RopeAttn(eng.H, eng.KV, eng.HD, kc.shape[1], kc.dtype, eng.eps, kc.device)
+    return _ATT[key]
+
+
+def _pos(device, start):
+    key = str(device)
+    if key not in _POS:
+        _POS[key] = torch.zeros(1, dtype=torch.int64, device=device)
+    return _POS[key].fill_(start)
 
 
 def layer(eng, l, weights, x, start, kc, vc, gguf=False):
@@ -133,20 +119,11 @@ def layer(eng, l, weights, x, start, kc, vc, gguf=False):
     norm = _rms(x, s["ln1"].float(), eps)
     qkv = torch.empty(T, (H + 2 * KV) * HD, device=x.device)
     matrix(norm, W["qkv"], qkv)
-    q = _rms(qkv[:, :H * HD].view(T, H, HD), s["qn"], eps)
-    k = _rms(qkv[:, H * HD:(H + KV) * HD].view(T, KV, HD), s["kn"], eps)
-    v = qkv[:, (H + KV) * HD:].view(T, KV, HD)
-    p = start + torch.arange(T, device=x.device)
-    ang = p[:, None].float() * eng.inv[None]
-    e = torch.cat([ang, ang], -1)
-    cos, sin = e.cos()[:, None], e.sin()[:, None]
-    q = q * cos + _rot(q) * sin
-    k = k * cos + _rot(k) * sin
-    kc.index_copy_(1, p, k.to(kc.dtype).transpose(0, 1))
-    vc.index_copy_(1, p, v.to(vc.dtype).transpose(0, 1))
-    del qkv, k, v
-    att = attention(eng, q, start, kc, vc)
-    del q
+    del norm
+    f32 = lambda t: t.float().contiguous()
+    att = torch.empty(T, H * HD, device=x.device)
+    _attn(eng, kc).prefill(qkv, f32(s["qn"]), f32(s["kn"]), f32(eng.inv), _pos(x.device, start), kc, vc, att, T)
+    del qkv
     matrix(att, W["o"], x, add=True)
     del att
     norm = _rms(x, s["ln2"].float(), eps)

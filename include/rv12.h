@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define RV12_ABI_VERSION 4
+#define RV12_ABI_VERSION 5
 
 enum rv12_status {
     RV12_OK = 0,
@@ -270,6 +270,25 @@ size_t rv12_attn_batch_workspace_bytes(const rv12_attn* a, int t);
 int rv12_rope_attn_batch(const rv12_attn* a, int t, const float* qkv, const float* qn, const float* kn,
                          const float* inv, const int64_t* pos, void* kc, void* vc, float* out, void* ws,
                          size_t ws_bytes, void* stream);
+
+/* Attention of a prompt block of 1 <= t <= 32768 tokens at positions *pos ..
+ * *pos + t - 1 (read on the device), the blocked prefill's: the q/k/v
+ * prologue of rv12_rope_attn_batch (head RMSNorm, RoPE, k and v rounded into
+ * the caches), then token r attends over positions 0..*pos + r with float32
+ * products and an online softmax into out[r] (t rows of n_heads * head_dim
+ * floats): one wave per (head, 16 tokens) on the float32 matrix cores, the
+ * G heads of a kv head in one workgroup.  a->splits is not used.  A block
+ * outside [0, maxt) gives zeros and leaves the caches untouched.  ws:
+ * rv12_prefill_attn_workspace_bytes(a, t) bytes (the q rows), 16-byte
+ * aligned; 0 there means the shape is not supported (maxt * head_dim * cache
+ * bytes and t * n_heads * head_dim * 4 must stay below 2^31).  Replaces
+ * qk_rope_cache_k + attention / att_k of the blocked prefill,
+ * ramvi/engine/ramvi_engine/kernels/prefill.py:100-103 and
+ * prefill_kernels.py:29-54. */
+size_t rv12_prefill_attn_workspace_bytes(const rv12_attn* a, int t);
+int rv12_prefill_rope_attn(const rv12_attn* a, int t, const float* qkv, const float* qn, const float* kn,
+                           const float* inv, const int64_t* pos, void* kc, void* vc, float* out, void* ws,
+                           size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

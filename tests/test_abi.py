@@ -31,7 +31,7 @@ def test_library_exports_every_symbol():
 def test_abi_version_and_strerror():
     from ai_amd import _lib
     L = _lib.lib()
-    assert L.rv12_abi_version() == 4
+    assert L.rv12_abi_version() == 5
     for s in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -20):
         assert _lib.strerror(s) and _lib.strerror(s) != "unknown rv12 status"
     assert _lib.strerror(-99) == "unknown rv12 status"
@@ -277,6 +277,37 @@ def test_attention_argument_errors():
     assert call(A(maxt=10241, splits=128)) == _lib.RV12_E_CONFIG  # 81 positions per split
     assert call(A(), out=None) == _lib.RV12_E_NULL
     assert call(A(), pos=None) == _lib.RV12_E_NULL
+    assert call(A(), ws=0) == _lib.RV12_E_WORKSPACE
+    assert call(A(), ws_bytes=1000) == _lib.RV12_E_WORKSPACE
+
+
+def test_prefill_attention_argument_errors():
+    """The prompt attention's faults are statuses before any device work; its
+    workspace holds the q rows (t * n_heads * head_dim floats); the splits
+    of the decode attention do not apply, its 32-bit offset limits do."""
+    from ai_amd import _lib
+    L = _lib.lib()
+    A = lambda **kw: _lib.Attn(*[kw.get(k, d) for k, d in (("n_heads", 32), ("n_kv", 8), ("head_dim", 128),
+                                                              ("maxt", 2304), ("kv_bf16", 1), ("splits", 36),
+                                                              ("eps", 1e-6), ("scale", 128 ** -0.5))])
+    ws = lambda a, t: L.rv12_prefill_attn_workspace_bytes(ctypes.byref(a), t)
+    assert ws(A(), 2048) == 2048 * 32 * 128 * 4
+    assert ws(A(splits=0, maxt=20000), 2048) == 2048 * 32 * 128 * 4  # no split rule
+    assert ws(A(), 0) == 0 and ws(A(), (1 << 15) + 1) == 0 and ws(A(n_heads=8), 1 << 15) > 0
+    assert ws(A(n_heads=128, n_kv=16), 1 << 15) == 0                 # q rows past 2^31 bytes
+    assert ws(A(maxt=1 << 22, kv_bf16=0), 16) == 0                   # cache offsets past 2^31
+    assert ws(A(head_dim=96), 16) == 0 and ws(A(n_heads=24), 16) == 0
+    p = ctypes.c_void_p(0x1000)
+
+    def call(a, t=16, ws=0x100000, ws_bytes=1 << 30, **null):
+        args = {k: (None if k in null else p) for k in ("qkv", "qn", "kn", "inv", "pos", "kc", "vc", "out")}
+        return L.rv12_prefill_rope_attn(ctypes.byref(a), t, *args.values(), ctypes.c_void_p(ws),
+                                        ctypes.c_size_t(ws_bytes), None)
+
+    assert call(A(head_dim=96)) == _lib.RV12_E_SHAPE
+    assert call(A(n_heads=24)) == _lib.RV12_E_SHAPE
+    assert call(A(), t=0) == _lib.RV12_E_TOKENS
+    assert call(A(), kc=None) == _lib.RV12_E_NULL
     assert call(A(), ws=0) == _lib.RV12_E_WORKSPACE
     assert call(A(), ws_bytes=1000) == _lib.RV12_E_WORKSPACE
 

@@ -313,3 +313,112 @@ def test_batch_equals_single_steps_and_graph_replays():
     att.batch(qkv, qn, kn, inv, torch.tensor([maxt - T + 1], device=dev), kc, vc, bad, T)
     torch.cuda.synchronize()
     assert torch.equal(bad, torch.zeros_like(bad)) and torch.equal(kc, k0) and torch.equal(vc, v0)
+
+
+def _prefill_ref(q, kc, vc, p0, T, H, KV, HD):
+    """Causal attention of T roped q rows [T, H, HD] at positions p0.. over
+    the caches' positions 0..p0 + t, in float64 (the softmax of masked
+    scores; prefill_kernels.py:29-51 in exact arithmetic)."""
+    G = H // KV
+    n = p0 + T
+    K = kc[:, :n].double()
+    V = vc[:, :n].double()
+    qh = q.double().view(T, KV, G, HD).permute(1, 2, 0, 3).reshape(KV, G * T, HD)
+    s = torch.matmul(qh, K.transpose(1, 2).contiguous()).view(KV, G, T, n) * HD ** -0.5
+    cols = torch.arange(n, device=q.device)
+    rows = p0 + torch.arange(T, device=q.device)
+    s.masked_fill_(cols[None, None, None, :] > rows[None, None, :, None], float("-inf"))
+    a = torch.softmax(s, -1).view(KV, G * T, n)
+    o = torch.matmul(a, V.contiguous()).view(KV, G, T, HD).permute(2, 0, 1, 3).reshape(T, H * HD)
+    return o.float()
+
+
+@pytest.mark.parametrize("H,KV,HD", [(32, 8, 128), (16, 8, 128), (8, 4, 64), (64, 8, 128), (8, 8, 64)])
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16])
+def test_prefill_attention_matches_float64(H, KV, HD, kv_dtype):
+    """rv12_prefill_rope_attn (the blocked prefill's qk_rope_cache_k + att_k)
+    for T = 1, 17, 300 prompt tokens at positions 0.. and 45.. of the cache:
+    the q/k/v prologue as in the batch kernel (k within one bf16 ulp, v
+    exact, other slots untouched), outputs within 1e-4 of the float64 causal
+    attention over the keys the kernel stored."""
+    from ai_amd.attn import RopeAttn
+    dev = "cuda"
+    maxt = 400
+    g = torch.Generator(device=dev).manual_seed(H * 7 + HD + 3)
+    eps = 1e-6
+    inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+    qn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    kn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    att = RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev)
+    for T in (1, 17, 300):
+        for p0 in (0, 45):
+            print("case", H, KV, HD, kv_dtype, T, p0, flush=True)
+            qkv = torch.randn(T, (H + 2 * KV) * HD, device=dev, generator=g) * 3
+            kc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+            vc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+            kc0, vc0 = kc.clone(), vc.clone()
+            out = torch.full((T, H * HD), 7.0, device=dev)
+            att.prefill(qkv, qn, kn, inv, torch.tensor([p0], device=dev), kc, vc, out, T)
+            torch.cuda.synchronize()
+            # the prologue: the batch reference's q rows, k/v slots
+            _, kr, vr = _torch_batch_ref(qkv[:1], qn, kn, inv, p0, kc0, vc0, H, KV, HD, eps)
+            q = qkv[:, :H * HD].view(T, H, HD)
+            k = qkv[:, H * HD:(H + KV) * HD].view(T, KV, HD)
+            rms = lambda x, w: w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+            q, k = rms(q, qn), rms(k, kn)
+            pos = torch.arange(p0, p0 + T, device=dev, dtype=torch.float32)
+            ang = (pos[:, None] * inv[None]).double()
+            cos = torch.cat([ang, ang], -1).cos().float()[:, None]
+            sin = torch.cat([ang, ang], -1).sin().float()[:, None]
+            rot = lambda t: torch.cat([-t[..., HD // 2:], t[..., :HD // 2]], -1)
+            q, k = q * cos + rot(q) * sin, k * cos + rot(k) * sin
+            v = qkv[:, (H + KV) * HD:].view(T, KV, HD)
+            tol = 2.0 ** -7 if kv_dtype == torch.bfloat16 else 1e-5
+            assert torch.allclose(kc[:, p0:p0 + T].float(), k.to(kv_dtype).float().transpose(0, 1), rtol=tol, atol=1e-6)
+            assert torch.equal(vc[:, p0:p0 + T].float(), v.to(kv_dtype).float().transpose(0, 1))
+            keep = torch.ones(maxt, dtype=torch.bool)
+            keep[p0:p0 + T] = False
+            assert torch.equal(kc[:, keep], kc0[:, keep]) and torch.equal(vc[:, keep], vc0[:, keep])
+            ref = _prefill_ref(q, kc, vc, p0, T, H, KV, HD)
+            assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), float((out - ref).abs().max())
+
+
+def test_prefill_attention_equals_batch_and_rejects_bad_blocks():
+    """A prompt block of 16 equals the batch kernel's 16 tokens from the same
+    cache (both within 1e-4 of each other); a block past the cache's end
+    gives zeros and writes nothing; unsupported blocks are refused before
+    any launch."""
+    import ctypes
+    from ai_amd import _lib
+    from ai_amd.attn import RopeAttn
+    dev = "cuda"
+    H, KV, HD, maxt, T = 32, 8, 128, 512, 16
+    g = torch.Generator(device=dev).manual_seed(9)
+    inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+    qn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    kn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    att = RopeAttn(H, KV, HD, maxt, torch.bfloat16, 1e-6, dev)
+    qkv = torch.randn(T, (H + 2 * KV) * HD, device=dev, generator=g)
+    kc = torch.randn(KV, maxt, HD, device=dev, generator=g).bfloat16()
+    vc = torch.randn(KV, maxt, HD, device=dev, generator=g).bfloat16()
+    kb, vb = kc.clone(), vc.clone()
+    p0 = 300
+    out = torch.zeros(T, H * HD, device=dev)
+    att.prefill(qkv, qn, kn, inv, torch.tensor([p0], device=dev), kc, vc, out, T)
+    ob = torch.zeros(T, H * HD, device=dev)
+    att.batch(qkv, qn, kn, inv, torch.tensor([p0], device=dev), kb, vb, ob, T)
+    torch.cuda.synchronize()
+    assert torch.equal(kc, kb) and torch.equal(vc, vb)
+    assert torch.allclose(out, ob, rtol=1e-4, atol=1e-5), float((out - ob).abs().max())
+    k0, v0 = kc.clone(), vc.clone()
+    bad = torch.full((T, H * HD), 7.0, device=dev)
+    att.prefill(qkv, qn, kn, inv, torch.tensor([maxt - T + 1], device=dev), kc, vc, bad, T)
+    torch.cuda.synchronize()
+    assert torch.equal(bad, torch.zeros_like(bad)) and torch.equal(kc, k0) and torch.equal(vc, v0)
+    L = _lib.lib()
+    a = att.a
+    assert L.rv12_prefill_attn_workspace_bytes(ctypes.byref(a), 0) == 0
+    assert L.rv12_prefill_attn_workspace_bytes(ctypes.byref(a), (1 << 15) + 1) == 0
+    assert L.rv12_prefill_attn_workspace_bytes(ctypes.byref(a), T) == T * H * HD * 4
+    rc = L.rv12_prefill_rope_attn(ctypes.byref(a), T, None, None, None, None, None, None, None, None, None, 0, None)
+    assert rc == _lib.RV12_E_NULL
