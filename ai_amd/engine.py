@@ -32,9 +32,12 @@ prefill, engine.py:471-480), or, in the reference's opt-in blocked mode
 ramvi/engine/ramvi_engine/kernels/prefill.py), all prompt tokens at once with
 each matrix decoded once and multiplied in one GEMM (ai_amd.prefill).
 
-Every layer stays resident in HBM (the reference's "gpu" placement): at about
-1.5 bytes per weight the largest model here, Qwen3-32B, needs 48 GB of the
-MI355X's 288 GB.
+Every layer stays resident in HBM by default (the reference's "gpu"
+placement): at about 1.5 bytes per weight the largest model here, Qwen3-32B,
+needs 48 GB of the MI355X's 288 GB.  With stream_layers = n the last n layers
+are kept as byte images in pinned host memory instead and copied into HBM
+slots during every pass (the reference's "stream" placement, ai_amd.stream),
+the copies ordered by events inside the same graph.
 """
 import os
 
@@ -43,6 +46,7 @@ import torch
 from . import prefill as blocked_prefill
 from . import wcomp
 from .attn import RopeAttn
+from .stream import LayerImage, Streamer
 
 MATS = ("qkv", "o", "gu", "down")
 BATCH = 16  # largest batch of one pass, as the reference's graph buckets (engine.py:31)
@@ -59,10 +63,12 @@ class Engine:
               None reads RAMVI_PREFILL as the reference does
     prefill_min  fewest prompt tokens for the blocked prefill (None:
               RAMVI_PREFILL_MIN_TOKENS, 256)
+    stream_layers  the last n layers live in pinned host memory and are
+              streamed through `slots` HBM slots every pass (ai_amd.stream)
     """
 
     def __init__(self, ck, maxt=2048, kv_dtype=torch.float32, device="cuda", log=None, prefill=None,
-                 prefill_min=None):
+                 prefill_min=None, stream_layers=0, slots=2):
         if prefill is None:
             blocked_prefill.enabled()  # validates RAMVI_PREFILL
             prefill = os.environ.get("RAMVI_PREFILL", "legacy")
@@ -80,16 +86,23 @@ class Engine:
         H, KV, HD = self.H, self.KV, self.HD
         self.inv = (1.0 / (ck.theta ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)  # engine.py:204
         self.emb = ck.t("model.embed_tokens.weight", dev)
-        self.W, self.small, self.Kc, self.Vc = [], [], [], []
+        if not 0 <= stream_layers <= self.L:
+            raise ValueError("stream_layers must be in 0..layers")
+        self.first_streamed = self.L - int(stream_layers)
+        self.W, self.small, self.Kc, self.Vc, images = [], [], [], [], []
         for i in range(self.L):
             w = ck.layer(i, dev)
             self.small.append({k: w[k] for k in ("ln1", "ln2")} | {k: w[k].float() for k in ("qn", "kn")})
             self.W.append({n: wcomp.compact(wcomp.compress(w[n])) for n in MATS})
+            if i >= self.first_streamed:  # to pinned host memory; HBM keeps only the slots
+                images.append(LayerImage(self.W[i]))
+                self.W[i] = None
             self.Kc.append(torch.zeros(KV, maxt, HD, dtype=kv_dtype, device=dev))
             self.Vc.append(torch.zeros_like(self.Kc[-1]))
             del w
             if log:
                 log(f"layer {i + 1}/{self.L} compressed")
+        self.streamer = Streamer(images, dev, slots) if images else None
         self.norm = ck.t("model.norm.weight", dev)
         self.normf = self.norm.float()
         self.head = wcomp.compact(wcomp.compress(ck.t(ck.head_name(), dev)))
@@ -141,9 +154,22 @@ class Engine:
         wcomp.gemvc_tc(x, W["gu"], self.gub[:T], 0, T, lnw=s["ln2"], eps=self.eps)
         wcomp.gemvc_tc(self.gub[:T], W["down"], x, 2, T)
 
-    def _layers(self, x, T, p0=None):
+    def _layers(self, x, T, p0=None, fn=None):
+        """Every layer in order (fn(l, W) in place of _gpu_layer); the streamed
+        layers take their matrices from the streamer's slots."""
+        fn = fn or (lambda l, W: self._gpu_layer(l, x, T, p0, W))
+        st = self.streamer
+        if st:
+            st.begin()
         for l in range(self.L):
-            self._gpu_layer(l, x, T, p0)
+            if l < self.first_streamed:
+                fn(l, self.W[l])
+            else:
+                i = l - self.first_streamed
+                fn(l, st.acquire(i))
+                st.release(i)
+        if st:
+            st.end()
 
     def _head_row(self, x1):
         """Greedy id of one row into self.nxt[0]: the final norm fused into the
@@ -236,8 +262,7 @@ class Engine:
         (ai_amd.prefill.layer), then the greedy id after the last one."""
         P = t.numel()
         x = self.emb.index_select(0, t).float()
-        for l in range(self.L):
-            blocked_prefill.layer(self, l, self.W[l], x, 0, self.Kc[l], self.Vc[l])
+        self._layers(x, P, fn=lambda l, W: blocked_prefill.layer(self, l, W, x, 0, self.Kc[l], self.Vc[l]))
         self._head_row(x[P - 1:P].contiguous())
         self.pos.fill_(P)
         return self.nxt[:1]

@@ -225,7 +225,7 @@ def measure_hbm(dev, reps=10):
             "method": "torch copy_, sum and bf16 mv over 2 GiB; read_GBs = the faster read; HIP events, 10 launches"}
 
 
-def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefill="blocked"):
+def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefill="blocked", stream_layers=0):
     """Greedy decode of a random-init Qwen3 (8b: a 2048-token random-id
     prompt, 256 new tokens; 32b: 4096 and
     128; bf16 KV cache): decode-only tok/s from the graph replays after the
@@ -237,7 +237,8 @@ def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefil
     from ai_amd.model import QWEN3, RandomCkpt
     ck = RandomCkpt(QWEN3[size], seed=seed)
     t0 = time.time()
-    eng = Engine(ck, maxt=prompt_len + new + (batch or 0), kv_dtype=torch.bfloat16, prefill=prefill)
+    eng = Engine(ck, maxt=prompt_len + new + (batch or 0), kv_dtype=torch.bfloat16, prefill=prefill,
+                 stream_layers=stream_layers)
     load_s = time.time() - t0
     prompt = [int(t) for t in np.random.default_rng(seed).integers(0, ck.V, prompt_len)]
     eng.generate(prompt[:64], 8)  # capture + warm
@@ -249,6 +250,10 @@ def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefil
            "tok_s": round(1e3 / per_tok, 2), "ms_per_token": round(per_tok, 4), "prefill_ms": round(prefill_ms, 1),
            "prefill": prefill if prefill != "blocked" or prompt_len >= eng.prefill_min else "legacy (below the blocked minimum)",
            "load_s": round(load_s, 1), "first_ids": ids[:8]}
+    if stream_layers:
+        gb = eng.streamer.bytes_per_pass / 1e9
+        out["streamed"] = {"layers": stream_layers, "of_layers": eng.L, "slots": eng.streamer.S,
+                           "GB_per_token": round(gb, 4), "h2d_GBs_per_token_time": round(gb / per_tok * 1e3, 1)}
     if new <= 64:
         out["ids"] = ids
     if batch:
@@ -259,6 +264,25 @@ def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefil
     del eng
     torch.cuda.empty_cache()
     return out
+
+
+def measure_h2d(dev, nbytes=1 << 30, reps=5):
+    """Pinned host -> HBM copy rate (one 1 GiB hipMemcpyAsync, HIP events):
+    the ceiling of the streamed placement."""
+    host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    d = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    d.copy_(host, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        d.copy_(host, non_blocking=True)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del host, d
+    torch.cuda.empty_cache()
+    return round(nbytes / ms / 1e6, 1)
 
 
 def run_attn(dev, reps=20, layers=36, positions=(100, 1000, 2100)):
@@ -609,6 +633,16 @@ def main():
         print(f"# qwen3-0.6b decode: {e2e06['tok_s']} tok/s ({e2e06['ms_per_token']} ms/token), prefill "
               f"{e2e06['prefill_ms']} ms for {e2e06['prompt']} tokens", file=sys.stderr, flush=True)
 
+    e2e_st = None
+    if not args.no_e2e:
+        # the reference's "stream" placement: 12 of the 36 layers in pinned host
+        # memory, copied into two HBM slots every token
+        e2e_st = run_e2e(dev, "8b", prompt_len=512, new=64, stream_layers=12)
+        e2e_st["h2d_measured_GBs"] = measure_h2d(dev)
+        print(f"# qwen3-8b, 12 layers streamed: {e2e_st['tok_s']} tok/s, {e2e_st['streamed']['GB_per_token']} GB "
+              f"per token over PCIe ({e2e_st['streamed']['h2d_GBs_per_token_time']} GB/s of token time; pinned "
+              f"copy {e2e_st['h2d_measured_GBs']} GB/s)", file=sys.stderr, flush=True)
+
     e2e32 = None
     if not args.no_e2e and not args.no_32b:
         e2e32 = run_e2e(dev, "32b", prompt_len=4096, new=128, batch=8)
@@ -653,6 +687,7 @@ def main():
         "e2e_decode": e2e,
         "e2e_decode_0_6b": e2e06,
         "e2e_decode_32b": e2e32,
+        "e2e_decode_8b_streamed": e2e_st,
         "cpu_baseline": cpu,
         "sweep_m1": sweep,
         "sweep_m1_input_column_outliers": sweep_cols,
