@@ -12,7 +12,7 @@ and a token runs them exactly as the reference's `_gpu_layer` does
     gemvc1(gu,  W.down, x,   2)               silu(g) * u prologue, accumulate
 
 and 2..16 tokens of one sequence as `_batch_layer` does (engine.py:344-356),
-RMSNorm separately and `gemvc_tc` for the four matrices.  The lm_head runs
+`gemvc_tc` for the four matrices with the RMSNorms fused into the prologue.  The lm_head runs
 through the same 12-bit linear with the final norm fused (new: the reference
 picks greedy tokens with an int8 bound pass and exact CPU rows,
 ramvi/engine/ramvi_engine/generation/head.py:29-88), followed by argmax, the
@@ -23,8 +23,8 @@ engine.py:432-444): the embedding row of the current token, all layers, the
 head, argmax, and the bookkeeping (next token becomes the input, position and
 output counter advance) run on the device, so the host only replays the graph.
 The step's attention (head norms, RoPE, KV write, grouped-query attention)
-is one HIP kernel per layer (ai_amd.attn); the batched prefill passes use the
-same math in torch.
+is one HIP kernel per layer (ai_amd.attn); passes of 2..16 tokens use the
+batch kernels of the same library, the blocked prefill its prompt kernels.
 
 A prompt goes through passes of up to 16 tokens (the reference's legacy
 prefill, engine.py:471-480), or, in the reference's opt-in blocked mode
