@@ -40,10 +40,11 @@ bool shape_fits(int K, int T, const Shape& c) {
 //     CUs, and wherever the activations would not fit in registers;
 //   MFMA kernel: the shape with the least time in a model of its rounds of
 //     workgroups (mfma_model_us);
-// The MFMA kernel is the built-in choice from 3 tokens on (at 3-4 tokens the
-// vector kernel's 8 FMAs per weight and token make it ALU-bound), and at 2
-// tokens where the vector kernel would have to split K to hold its activations
-// in registers (Qwen3-14B down: 35 vs 37.5 us).
+// The MFMA kernel is the built-in choice from 3 tokens on, except at 3-4
+// tokens on small matrices (up to 512 row blocks, K <= 6144), where the
+// vector kernel's FMAs still hide behind its weight stream; and at 2 tokens
+// where the vector kernel would have to split K to hold its activations in
+// registers (Qwen3-14B down: 35 vs 37.5 us).
 Shape vector_shape(int N, int K, int T) {
     const int64_t nblk = nblocks(N);
     Shape c;
@@ -145,6 +146,15 @@ Shape default_shape(int N, int K, int T) {
     const int nsteps = K / 32;
     bool vec = T <= kVectorDefaultTokens;
     if (T == 2 && !gemv_prefetch_all(K, T, vector_shape(N, K, T).waves, 1)) vec = false;
+    // 3-4 tokens on up to 512 row blocks of K <= 6144: the vector kernel,
+    // unsplit unless below 128 row blocks, beats the MFMA kernel's staging
+    // and split-K reduce (MI355X: Qwen3-8B qkv 14.8 -> 12.1 us and o 10.9 ->
+    // 9.6 at 3 tokens, 14.4 -> 13.0 and 10.7 -> 10.4 at 4; 14B k/v 9.1 ->
+    // 7.8 / 9.2 -> 8.2, qkv 16.2 -> 15.9 / 16.3 -> 16.0, o 14.6 -> 13.7 at 3
+    // tokens); larger or longer matrices keep the MFMA kernel (14B down
+    // 32.5 against 43.5, gate/up 29.9 against 34.7)
+    const bool vec34 = (T == 3 || T == 4) && K <= 6144 && nblocks(N) <= 512;
+    vec = vec || vec34;
     Shape c = vec ? vector_shape(N, K, T) : mfma_shape(N, K, T);
     while (c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
     // at one token the vector kernel's waves want at least 8 K steps each
@@ -153,7 +163,8 @@ Shape default_shape(int N, int K, int T) {
     while (c.splits < kMaxSplits && c.splits < nsteps && !shape_fits(K, T, c)) ++c.splits;
     // the vector kernel streams best with all activations loaded before the weights
     const int s_fit = c.splits;
-    while (c.kernel == 1 && c.splits < kMaxSplits && c.splits < nsteps && !gemv_prefetch_all(K, T, c.waves, c.splits))
+    while (c.kernel == 1 && !vec34 && c.splits < kMaxSplits && c.splits < nsteps &&
+           !gemv_prefetch_all(K, T, c.waves, c.splits))
         ++c.splits;
     if (c.splits > s_fit) {
         // once K is split anyway, up to two more splits may fill the last

@@ -34,7 +34,7 @@ from ._lib import KERNEL_MFMA, KERNEL_VECTOR, Codec, Launch, Matrix, check, lib
 
 CFG1 = {}  # (N, K, MODE) -> (BN, waves) or (BN, waves, S); filled by ai_amd.tune
 CFGT = {}  # (N, K, MODE) -> (BN, waves, S); filled by ai_amd.tune
-VECTOR_TOKENS = 2  # the library's built-in kernel: vector FMA up to 2 tokens, bf16 MFMA above
+VECTOR_TOKENS = 2  # a given BN names the vector kernel up to 2 tokens, the bf16 MFMA kernel above
 _SK = {}   # (N, device) -> workspace tensor (split-K partial sums)
 
 
@@ -260,8 +260,9 @@ def _launch(BN, w, S, T):
     """Launch struct for the reference's tuning triple.  BN = rows per
     workgroup: row blocks of 16 per workgroup in the vector kernel (T <= 2),
     row blocks per wave times waves in the MFMA kernel (T > 2).  A given BN
-    names its kernel; without one the library picks (the vector kernel up to
-    2 tokens, except where it would have to split K at 2 tokens)."""
+    names its kernel; without one the library picks (rv12_launch_shape: the
+    vector kernel up to 2 tokens, except where it would have to split K at 2
+    tokens, and at 3-4 tokens on small matrices)."""
     rb = kernel = 0
     if BN:
         vec = T <= VECTOR_TOKENS

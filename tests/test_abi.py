@@ -85,6 +85,13 @@ def test_launch_shapes():
     assert shape(5120, 17408, 2)[0] == 2                  # Qwen3-14B down at 2 tokens: MFMA
     assert shape(7168, 5120, 2) == (1, 2, 8, 1)           # 14B qkv at 2 tokens: vector, unsplit, 2 row blocks
     assert shape(5120, 8192, 2) == (1, 1, 16, 1)          # 32B o at 2 tokens: K > 6144 keeps one row block
+    # 3-4 tokens on up to 512 row blocks of K <= 6144: the vector kernel
+    assert shape(6144, 4096, 3) == (1, 2, 8, 1)           # 8B qkv: two row blocks, unsplit
+    assert shape(4096, 4096, 4) == (1, 1, 8, 1)           # 8B o
+    assert shape(1024, 5120, 3) == (1, 1, 8, 4)           # 14B k/v: split below 128 row blocks
+    assert shape(5120, 17408, 3)[0] == 2                  # 14B down: MFMA
+    assert shape(17408, 5120, 4)[0] == 2                  # 14B gate/up: MFMA (1088 row blocks)
+    assert shape(4096, 4096, 5)[0] == 2                   # 5 tokens: MFMA
     # the MFMA kernel's time model picks the shapes the MI355X sweeps found best
     assert shape(5120, 17408, 16)[:3] == (2, 4, 8)        # 14B down: four row blocks per wave
     assert shape(1024, 5120, 16)[:3] == (2, 1, 4)         # 14B k/v: 64 row blocks

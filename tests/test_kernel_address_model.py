@@ -33,7 +33,7 @@ def _shape(N, K, T):
 
 
 @pytest.mark.parametrize("model", sorted(MODELS))
-@pytest.mark.parametrize("T", [1, 2])
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
 def test_vector_linear_addresses(model, T):
     D, H, KV, HD, FF, V = MODELS[model]
     for name, N, K, mode, rms in _layer_linears(D, H, KV, HD, FF, V):
