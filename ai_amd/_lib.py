@@ -28,7 +28,7 @@ EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_pack_p
            "rv12_attn_batch_workspace_bytes", "rv12_rope_attn_batch", "rv12_prefill_attn_workspace_bytes",
            "rv12_prefill_rope_attn", "rv12_prefill_workspace_bytes",
            "rv12_prefill_linear")
-ABI_VERSION = 5
+ABI_VERSION = 6
 STATIC_SCRATCH_BYTES = 8 << 20  # RV12_STATIC_SCRATCH_BYTES
 
 
@@ -122,7 +122,7 @@ def lib():
         L.rv12_prefill_workspace_bytes.restype = SZ
         L.rv12_prefill_workspace_bytes.argtypes = [I, I]
         L.rv12_prefill_linear.restype = I
-        L.rv12_prefill_linear.argtypes = [ctypes.POINTER(Matrix), P, P, I, I, P, SZ, P]
+        L.rv12_prefill_linear.argtypes = [ctypes.POINTER(Matrix), P, P, I, P, F, I, P, SZ, P]
         L.rv12_attn_batch_workspace_bytes.restype = SZ
         L.rv12_attn_batch_workspace_bytes.argtypes = [ctypes.POINTER(Attn), I]
         L.rv12_rope_attn_batch.restype = I

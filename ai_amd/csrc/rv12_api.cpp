@@ -488,18 +488,20 @@ size_t rv12_prefill_workspace_bytes(int k, int t) {
     return prefill_ws_bytes(k, t);
 }
 
-int rv12_prefill_linear(const rv12_matrix* w, const float* x, float* y, int t, int mode, void* ws, size_t ws_bytes,
-                        void* stream) {
+int rv12_prefill_linear(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps,
+                        int mode, void* ws, size_t ws_bytes, void* stream) {
     int rc = check_matrix(w);
     if (rc) return rc;
     if (!x || !y) return RV12_E_NULL;
     if (mode < 0 || mode > 2) return RV12_E_MODE;
+    if (lnw && mode == 2) return RV12_E_MODE;  // the RMS prologue belongs to the plain linear
+    if (lnw && (uintptr_t)lnw % 16) return RV12_E_ALIGN;
     if (t < 1 || t > kMaxPrefillTokens) return RV12_E_TOKENS;
     if (!aligned16(x) || !aligned16(y)) return RV12_E_ALIGN;
     const size_t need = prefill_ws_bytes(w->k, t);
     if (!ws || ws_bytes < need) return RV12_E_WORKSPACE;
     if (!aligned16(ws)) return RV12_E_ALIGN;
-    launch_prefill(*w, x, y, t, mode, ws, (hipStream_t)stream);
+    launch_prefill(*w, x, y, t, mode, lnw, eps, ws, (hipStream_t)stream);
     return launch_status();
 }
 

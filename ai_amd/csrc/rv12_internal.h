@@ -146,7 +146,8 @@ void launch_pick(const float* v, const int32_t* ix, int64_t n, int64_t stride, i
 // --- prefill linear (k_prefill_x + k_prefill_mm), any T
 constexpr int kMaxPrefillTokens = 1 << 16;
 size_t prefill_ws_bytes(int K, int T);
-void launch_prefill(const rv12_matrix& w, const float* x, float* y, int T, int mode, void* ws, hipStream_t st);
+void launch_prefill(const rv12_matrix& w, const float* x, float* y, int T, int mode, const uint16_t* lnw, float eps,
+                    void* ws, hipStream_t st);
 void launch_codec_to_bf16(const rv12_codec& c, uint16_t* w, hipStream_t st);
 void launch_pack_plan(const uint16_t* w, int N, int K, int32_t* rbase, int32_t* row_exc, hipStream_t st);
 void launch_pack(const uint16_t* w, int N, int K, const int32_t* rbase, const int32_t* rp, uint32_t* tiles,

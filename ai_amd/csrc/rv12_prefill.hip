@@ -5,10 +5,13 @@
 // in its 12-bit form, never written back in a wider format.
 //
 // y[t] (=|+=) W_dec . x'[t], t < T, with the MODE prologue (2: x' =
-// silu(x[0:K]) * x[K:2K]).  Two passes:
+// silu(x[0:K]) * x[K:2K]) or the RMSNorm prologue of mode 0 (x' = lnw x,
+// the token's rs = 1 / sqrt(mean x^2 + eps) applied to its outputs, as the
+// decode kernels apply it).  Two passes:
 //   1. k_prefill_x: one workgroup per 16 tokens: each token's exponent scale
 //      P_t (64 when its largest |x'| lies in [2^-40, 2^63), else 100 minus
-//      the exponent of the largest), then x' 2^P_t split into bf16 parts
+//      the exponent of the largest) and, with RMS, its rs (sum of squares of
+//      x 2^-32), then x' 2^P_t split into bf16 parts
 //      hi + mid + lo (24 significand bits, as the reference's _x3 split,
 //      wcomp.py:130-140) in B-operand lane order: for token block tb, step
 //      s (32 columns) and part, 64 lanes x 8 bf16 (lane l: token l%16,
@@ -23,8 +26,8 @@
 //      fp32 accumulators.  Epilogue: v = acc 2^(sc_row - P_t) (exact); the
 //      packed form's exception entries of the wave's rows (weights outside a
 //      row's window, zeros in the tiles) add ev * x'[t][col] in list order,
-//      x' gathered from x in fp32; then y is stored or added; rows past N and
-//      tokens past T are skipped.
+//      x' gathered from x in fp32; with RMS v is scaled by rs_t; then y is
+//      stored or added; rows past N and tokens past T are skipped.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -38,11 +41,22 @@ constexpr int kPfTokBlocks = 8;   // token blocks (of 16 tokens) per workgroup
 constexpr int kPfThreads = 512;
 constexpr int kPfDepth = 2;       // weight steps in flight per wave beyond the current one
 
-// x' of token row xr at columns k..k+7 (MODE 2: silu(g) * u)
-__device__ __forceinline__ void prefill_xprime(const float* xr, int K, int k, bool m2, float (&v)[8]) {
+// x' of token row xr at columns k..k+7 (MODE 2: silu(g) * u; lnw: the RMS
+// weight times x)
+__device__ __forceinline__ void prefill_xprime(const float* xr, int K, int k, bool m2, const uint16_t* lnw,
+                                               float (&v)[8]) {
     const f32x4 a = *reinterpret_cast<const f32x4*>(xr + k);
     const f32x4 b = *reinterpret_cast<const f32x4*>(xr + k + 4);
     v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    if (lnw) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(lnw + k);
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] *= __uint_as_float(ww[i] << 16);
+            v[2 * i + 1] *= __uint_as_float(ww[i] & 0xFFFF0000u);
+        }
+    }
     if (m2) {
         const f32x4 c = *reinterpret_cast<const f32x4*>(xr + K + k);
         const f32x4 d = *reinterpret_cast<const f32x4*>(xr + K + k + 4);
@@ -54,28 +68,49 @@ __device__ __forceinline__ void prefill_xprime(const float* xr, int K, int k, bo
 
 // 1. grid (token blocks of the padded T), 256 threads
 __global__ __launch_bounds__(256) void k_prefill_x(const float* __restrict__ x, int T, int K, int xs, int m2,
-                                                   u32x4* __restrict__ xb, int* __restrict__ P) {
+                                                   const uint16_t* __restrict__ lnw, float eps,
+                                                   u32x4* __restrict__ xb, int* __restrict__ P,
+                                                   float* __restrict__ R) {
     __shared__ int emax[4][16];
+    __shared__ float ssq[4][16];
     __shared__ int ps[16];
     const int tb = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nsteps = K >> 5;
-    // (a) the largest exponent of |x'| per token: thread (tok, sub) over columns 8 sub + 128 i
+    // (a) the largest exponent of |x'| per token and, with RMS, the sum of
+    // squares of x 2^-32: thread (tok, sub) over columns 8 sub + 128 i
     {
         const int tok = tid & 15, sub = tid >> 4;
         const int t = tb * 16 + tok;
         int e = -1000;
+        float sq = 0.0f;
         if (t < T) {
             const float* xr = x + (int64_t)t * xs;
             for (int k = sub * 8; k < K; k += 128) {
                 float v[8];
-                prefill_xprime(xr, K, k, m2 != 0, v);
+                prefill_xprime(xr, K, k, m2 != 0, nullptr, v);
+                if (lnw) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) sq += (v[i] * kSsqScale) * (v[i] * kSsqScale);
+                    const u32x4 w = *reinterpret_cast<const u32x4*>(lnw + k);
+                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        v[2 * i] *= __uint_as_float(ww[i] << 16);
+                        v[2 * i + 1] *= __uint_as_float(ww[i] & 0xFFFF0000u);
+                    }
+                }
 #pragma unroll
                 for (int i = 0; i < 8; ++i) e = max(e, exp_or_min(v[i]));
             }
         }
         e = max(e, __shfl_xor(e, 16));
         e = max(e, __shfl_xor(e, 32));
-        if (lane < 16) emax[wave][lane] = e;
+        sq += __shfl_xor(sq, 16);
+        sq += __shfl_xor(sq, 32);
+        if (lane < 16) {
+            emax[wave][lane] = e;
+            ssq[wave][lane] = sq;
+        }
     }
     __syncthreads();
     if (tid < 16) {
@@ -83,6 +118,7 @@ __global__ __launch_bounds__(256) void k_prefill_x(const float* __restrict__ x, 
         const int p = (e >= -39 && e <= kXRangeHi) ? kXScaleExp : slow_scale_exp(e);
         ps[tid] = p;
         P[tb * 16 + tid] = p;
+        if (lnw) R[tb * 16 + tid] = rms_scale((ssq[0][tid] + ssq[1][tid]) + (ssq[2][tid] + ssq[3][tid]), K, eps);
     }
     __syncthreads();
     // (b) the parts: thread (tok, k8, ss) writes step s0 + ss, lane 16 k8 + tok
@@ -94,7 +130,7 @@ __global__ __launch_bounds__(256) void k_prefill_x(const float* __restrict__ x, 
         u32x4 hi = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
         if (t < T) {
             float v[8];
-            prefill_xprime(xr, K, s * 32 + k8 * 8, m2 != 0, v);
+            prefill_xprime(xr, K, s * 32 + k8 * 8, m2 != 0, lnw, v);
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = ldexpf(v[i], p);
             split3(v, hi, mid, lo);
@@ -106,7 +142,10 @@ __global__ __launch_bounds__(256) void k_prefill_x(const float* __restrict__ x, 
     }
 }
 
-// 2. grid (row tiles of 256 rows, token tiles of 128), 512 threads
+// 2. grid (row tiles of 256 rows, token tiles of 128), 512 threads.  M2 / LN
+// (the silu(g) * u and RMS prologues) are template arguments, so that the
+// exception gathers of the epilogue are straight-line loads per variant.
+template <bool M2, bool LN>
 __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __restrict__ tiles,
                                                            const int32_t* __restrict__ rbase,
                                                            const u32x4* __restrict__ xb, const int* __restrict__ P,
@@ -114,8 +153,9 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
                                                            const int32_t* __restrict__ er,
                                                            const int32_t* __restrict__ ec,
                                                            const float* __restrict__ ev, const float* __restrict__ x,
-                                                           float* __restrict__ y, int N, int K, int T, int xs,
-                                                           int m2, int add) {
+                                                           const uint16_t* __restrict__ lnw,
+                                                           const float* __restrict__ R, float* __restrict__ y, int N,
+                                                           int K, int T, int xs, int m2, int add) {
     __shared__ u32x4 bs[2][kPfTokBlocks * 3 * 64];  // 2 x 24 KB
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -237,11 +277,14 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
                 rr[j] = (int)(er[e] - rlo);
                 evv[j] = e0 + j < e_hi ? ev[e] : 0.0f;
                 const int col = ec[e];
+                float wl = 1.0f;
+                if constexpr (LN) wl = __uint_as_float((uint32_t)lnw[col] << 16);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const float* xr = x + (int64_t)min(tok[c], T - 1) * xs;
                     const float g = xr[col];
-                    xv[j][c] = m2 ? silu_mul(g, xr[K + col]) : g;
+                    if constexpr (M2) xv[j][c] = silu_mul(g, xr[K + col]);
+                    else xv[j][c] = LN ? g * wl : g;
                 }
             }
 #pragma unroll
@@ -258,10 +301,18 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
             }
         }
     }
-    // (c) store or add; rows past N and tokens past T are skipped
+    // (c) with RMS the token's rs; store or add; rows past N and tokens past
+    // T are skipped
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         if (tok[c] >= T) continue;
+        if constexpr (LN) {
+            const float rs = R[tok[c]];
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[b][c][i] *= rs;
+        }
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const int64_t n = (blk0 + b) * 16 + q * 4;
@@ -279,21 +330,24 @@ int prefill_tokens_padded(int T) { return (T + kPfTokBlocks * 16 - 1) / (kPfTokB
 
 size_t prefill_ws_bytes(int K, int T) {
     const size_t tp = (size_t)prefill_tokens_padded(T);
-    return tp * (size_t)K * 6 + tp * 4;
+    return tp * (size_t)K * 6 + tp * 8;
 }
 
-void launch_prefill(const rv12_matrix& w, const float* x, float* y, int T, int mode, void* ws, hipStream_t st) {
+void launch_prefill(const rv12_matrix& w, const float* x, float* y, int T, int mode, const uint16_t* lnw, float eps,
+                    void* ws, hipStream_t st) {
     const int K = w.k, N = w.n;
     const int tp = prefill_tokens_padded(T);
     u32x4* xb = reinterpret_cast<u32x4*>(ws);
     int* P = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + (size_t)tp * K * 6);
+    float* R = reinterpret_cast<float*>(P + tp);
     const int xs = mode == 2 ? 2 * K : K;
-    hipLaunchKernelGGL(k_prefill_x, dim3(tp / 16), dim3(256), 0, st, x, T, K, xs, mode == 2 ? 1 : 0, xb, P);
+    hipLaunchKernelGGL(k_prefill_x, dim3(tp / 16), dim3(256), 0, st, x, T, K, xs, mode == 2 ? 1 : 0, lnw, eps, xb, P,
+                       R);
     const int64_t nblk = ((int64_t)N + 15) / 16;
     const dim3 grid((unsigned)((nblk + kPfRowBlocks - 1) / kPfRowBlocks), (unsigned)(tp / (kPfTokBlocks * 16)));
-    hipLaunchKernelGGL(k_prefill_mm, grid, dim3(kPfThreads), 0, st, reinterpret_cast<const uint32_t*>(w.tiles),
-                       w.rbase, xb, P, w.rp, w.er, w.ec, w.ev, x, y, N, K, T, xs, mode == 2 ? 1 : 0,
-                       mode != 0 ? 1 : 0);
+    const auto kern = mode == 2 ? k_prefill_mm<true, false> : (lnw ? k_prefill_mm<false, true> : k_prefill_mm<false, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(kPfThreads), 0, st, reinterpret_cast<const uint32_t*>(w.tiles), w.rbase, xb,
+                       P, w.rp, w.er, w.ec, w.ev, x, lnw, R, y, N, K, T, xs, mode == 2 ? 1 : 0, mode != 0 ? 1 : 0);
 }
 
 }  // namespace rv12

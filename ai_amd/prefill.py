@@ -48,8 +48,9 @@ def enabled(n=None):
 _WS = {}  # device -> workspace of the prefill linear (the split activations)
 
 
-def _linear(x, c, y, mode):
-    """y (=|+=) W x' over every token row of x (fp32 [T, K], [T, 2K] in mode 2)."""
+def _linear(x, c, y, mode, lnw=None, eps=1e-6):
+    """y (=|+=) W x' over every token row of x (fp32 [T, K], [T, 2K] in mode
+    2); lnw (bf16 [K]) fuses the row's RMSNorm, as gemvc1 does."""
     import ctypes
     from . import _lib
     T = x.shape[0]
@@ -58,6 +59,8 @@ def _linear(x, c, y, mode):
         raise ValueError("prefill: x and y must be contiguous float32")
     if x.shape[1] != (2 * K if mode == 2 else K) or y.numel() < T * N:
         raise ValueError("prefill: x or y has the wrong shape")
+    if lnw is not None and (lnw.dtype != torch.bfloat16 or not lnw.is_contiguous() or lnw.numel() < K):
+        raise ValueError("prefill: lnw must be a contiguous bf16 vector of K entries")
     L = _lib.lib()
     need = L.rv12_prefill_workspace_bytes(K, T)
     if need == 0:
@@ -67,19 +70,18 @@ def _linear(x, c, y, mode):
         _WS[key] = torch.empty(need, dtype=torch.uint8, device=x.device)
     ws = _WS[key]
     rc = L.rv12_prefill_linear(ctypes.byref(wcomp._matrix(c)), ctypes.c_void_p(x.data_ptr()),
-                               ctypes.c_void_p(y.data_ptr()), T, int(mode), ctypes.c_void_p(ws.data_ptr()),
-                               ws.numel(), ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream))
+                               ctypes.c_void_p(y.data_ptr()), T,
+                               None if lnw is None else ctypes.c_void_p(lnw.data_ptr()), float(eps), int(mode),
+                               ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                               ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream))
     _lib.check(rc, "prefill")
 
 
-def matrix(x, c, y, add=False):
+def matrix(x, c, y, add=False, lnw=None, eps=1e-6):
     """y (=|+=) x . W^T for every token row of x (fp32 [T, K]); W read once
-    in its 12-bit form (prefill.py:66-78)."""
-    _linear(x, c, y, 1 if add else 0)
-
-
-def _rms(x, w, eps):
-    return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+    in its 12-bit form (prefill.py:66-78).  lnw: the rows' RMSNorm (rmsg_k,
+    prefill.py:94) fused into the linear."""
+    _linear(x, c, y, 1 if add else 0, lnw, eps)
 
 
 _ATT = {}  # (dimensions, cache, device) -> RopeAttn launch parameters and workspace
@@ -102,10 +104,10 @@ def _pos(device, start):
 
 def layer(eng, l, weights, x, start, kc, vc, gguf=False):
     """One layer over all prompt rows x (fp32 [T, D], updated in place) at
-    positions start.. (prefill.py:81-121, same signature): RMSNorm, qkv, q/k
-    head norms, RoPE, K/V into the caches kc / vc (rounded to their dtype),
-    causal attention, o (residual add), RMSNorm, gate/up, silu(g) * u, down
-    (residual add).  weights: the layer's fused 12-bit matrices qkv, o, gu,
+    positions start.. (prefill.py:81-121, same signature): RMSNorm fused into
+    qkv, q/k head norms, RoPE, K/V into the caches kc / vc (rounded to their
+    dtype), causal attention, o (residual add), RMSNorm fused into gate/up,
+    silu(g) * u fused into down (residual add): five library calls.  weights: the layer's fused 12-bit matrices qkv, o, gu,
     down; eng supplies the dimensions, eng.small[l] the norm weights and
     eng.inv the RoPE frequencies.  gguf=True (separate q/k/v and gate/up GGUF
     matrices) belongs to the reference's GGUF engine, which is not on this
@@ -116,19 +118,16 @@ def layer(eng, l, weights, x, start, kc, vc, gguf=False):
     H, KV, HD, FF, eps = eng.H, eng.KV, eng.HD, eng.FF, eng.eps
     W = weights
     s = eng.small[l]
-    norm = _rms(x, s["ln1"].float(), eps)
+    bf = lambda t: t.to(torch.bfloat16).contiguous()
     qkv = torch.empty(T, (H + 2 * KV) * HD, device=x.device)
-    matrix(norm, W["qkv"], qkv)
-    del norm
+    matrix(x, W["qkv"], qkv, lnw=bf(s["ln1"]), eps=eps)
     f32 = lambda t: t.float().contiguous()
     att = torch.empty(T, H * HD, device=x.device)
     _attn(eng, kc).prefill(qkv, f32(s["qn"]), f32(s["kn"]), f32(eng.inv), _pos(x.device, start), kc, vc, att, T)
     del qkv
     matrix(att, W["o"], x, add=True)
     del att
-    norm = _rms(x, s["ln2"].float(), eps)
     gu = torch.empty(T, 2 * FF, device=x.device)
-    matrix(norm, W["gu"], gu)
-    del norm
+    matrix(x, W["gu"], gu, lnw=bf(s["ln2"]), eps=eps)
     _linear(gu, W["down"], x, 2)  # silu(g) * u fused into the linear's prologue
     del gu

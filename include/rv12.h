@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define RV12_ABI_VERSION 5
+#define RV12_ABI_VERSION 6
 
 enum rv12_status {
     RV12_OK = 0,
@@ -210,18 +210,19 @@ int rv12_gemm_static(const rv12_matrix* w, const float* x, float* y, int t, cons
 
 /* The prompt's linear, 1 <= t <= 65536 tokens at once:  y[r] (=|+=) W_dec . x'[r]
  * for every token row r (x rows K floats apart, 2K in mode 2; y rows N apart),
- * mode as rv12_gemv.  The 12-bit decode is fused into a bf16 MFMA GEMM:
+ * mode and lnw / eps (the RMSNorm prologue, modes 0 and 1; 16-byte aligned)
+ * as rv12_gemv.  The 12-bit decode is fused into a bf16 MFMA GEMM:
  * x' is split per token into three bf16 parts (24 significand bits, after an
  * exact power-of-two scale), every weight is read once in its 12-bit form,
  * products and sums are fp32, the exceptions are added in list order.  ws:
  * rv12_prefill_workspace_bytes(k, t) bytes (6 bytes per column and padded
- * token, the parts), 16-byte aligned.  Replaces the blocked prefill's
- * matrix() (decode_rows + the fp32 GEMM mm_k),
- * ramvi/engine/ramvi_engine/kernels/prefill.py:66-78,
+ * token, the parts, and 8 per padded token), 16-byte aligned.  Replaces the
+ * blocked prefill's rmsg_k + matrix() (decode_rows + the fp32 GEMM mm_k),
+ * ramvi/engine/ramvi_engine/kernels/prefill.py:66-78, 94-99,
  * ramvi/engine/ramvi_engine/kernels/prefill_kernels.py:8-26, 58-110. */
 size_t rv12_prefill_workspace_bytes(int k, int t);
-int rv12_prefill_linear(const rv12_matrix* w, const float* x, float* y, int t, int mode, void* ws, size_t ws_bytes,
-                        void* stream);
+int rv12_prefill_linear(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps,
+                        int mode, void* ws, size_t ws_bytes, void* stream);
 
 /* Bit-exact decode of rows [first, last) to bf16 bits (out_f32 == 0, out is
  * uint16[last-first, K]) or to float32 (out_f32 != 0, out is float[last-first, K]).

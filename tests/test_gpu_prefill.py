@@ -16,7 +16,7 @@ from oracle import codec, linear
 pytestmark = pytest.mark.gpu
 
 
-def _check(cnp, T, seed, add, mode=None, scales=None):
+def _check(cnp, T, seed, add, mode=None, scales=None, rms=False):
     from ai_amd import prefill, wcomp
     rng = np.random.default_rng(seed)
     N, K = cnp["N"], cnp["K"]
@@ -27,16 +27,21 @@ def _check(cnp, T, seed, add, mode=None, scales=None):
         X *= np.sqrt(sc) if mode == 2 else sc
     X = X.astype(np.float32)
     Y0 = rng.standard_normal((T, N)).astype(np.float32)
+    lnw = lw = ln = None
+    if rms:  # the RMSNorm prologue (rmsg_k fused): a bf16 weight of K entries
+        lnw = codec.f32_to_bf16_rne((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+        lw = codec.bf16_to_f32(lnw)
+        ln = torch.from_numpy(lnw.view(np.int16).copy()).view(torch.bfloat16).cuda()
     W = codec.decode_f32(cnp).astype(np.float64)
-    ref = linear.linear(cnp, X, mode, Y0 if mode else None, W=W)
-    bound = linear.error_bound(cnp, X, mode, W=W)
+    ref = linear.linear(cnp, X, mode, Y0 if mode else None, lnw=lw, W=W)
+    bound = linear.error_bound(cnp, X, mode, lnw=lw, W=W)
     c = wcomp.prepare({k: (torch.from_numpy(np.ascontiguousarray(v)) if isinstance(v, np.ndarray) else v)
                        for k, v in cnp.items()})
     y = torch.from_numpy(Y0.copy()).cuda()
     if mode == 2:
         prefill._linear(torch.from_numpy(X).cuda(), c, y, 2)
     else:
-        prefill.matrix(torch.from_numpy(X).cuda(), c, y, add=add)
+        prefill.matrix(torch.from_numpy(X).cuda(), c, y, add=add, lnw=ln)
     torch.cuda.synchronize()
     got = y.cpu().numpy().astype(np.float64)
     fin = np.isfinite(ref)
@@ -70,7 +75,8 @@ def test_matrix_with_exceptions_in_many_rows():
 @pytest.mark.parametrize("T", [1, 17, 128, 129, 300])
 def test_ragged_tokens_rows_and_modes(T):
     """Token counts around the 128-token tile, a row count that is not a
-    multiple of the 256-row tile, every mode."""
+    multiple of the 256-row tile, every mode, and the RMSNorm prologue
+    (store and accumulate)."""
     rng = np.random.default_rng(T)
     w = (rng.standard_normal((300, 512)) * 0.02).astype(np.float32)
     w[rng.choice(300, 2)] *= 20
@@ -78,6 +84,41 @@ def test_ragged_tokens_rows_and_modes(T):
     for mode in (0, 1, 2):
         print("T", T, "mode", mode, flush=True)
         _check(cnp, T, T + mode, mode != 0, mode=mode)
+    for mode in (0, 1):
+        print("T", T, "mode", mode, "rms", flush=True)
+        _check(cnp, T, T + 7 + mode, mode != 0, mode=mode, rms=True)
+
+
+def test_rms_prologue_on_golden_dicts_and_scales(golden):
+    """The fused RMSNorm (rs per token over its full row, lnw x staged) on
+    the golden matrices, and over tokens scaled by 2^-60 .. 2^60: the sum of
+    squares runs over (x 2^-32)^2, so no token overflows or vanishes."""
+    for case in ("prefill_seed7", "outliers_rows_cols"):
+        _check(ref_dict(golden[case]), 300, 5, False, rms=True)
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((200, 1024)) * 0.02).astype(np.float32)
+    cnp = codec.compress(codec.f32_to_bf16_rne(w))
+    T = 40
+    scales = [2.0 ** e for e in np.linspace(-60, 60, T)]
+    _check(cnp, T, 13, False, mode=0, scales=scales, rms=True)
+
+
+def test_rms_prologue_rejected_in_mode_2():
+    import ctypes
+    from ai_amd import _lib, wcomp
+    rng = np.random.default_rng(1)
+    cnp = codec.compress(codec.f32_to_bf16_rne((rng.standard_normal((32, 256)) * 0.02).astype(np.float32)))
+    c = wcomp.prepare({k: (torch.from_numpy(np.ascontiguousarray(v)) if isinstance(v, np.ndarray) else v)
+                       for k, v in cnp.items()})
+    x = torch.zeros(4, 512, device="cuda")
+    y = torch.zeros(4, 32, device="cuda")
+    ln = torch.ones(256, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    L = _lib.lib()
+    rc = L.rv12_prefill_linear(ctypes.byref(wcomp._matrix(c)), ctypes.c_void_p(x.data_ptr()),
+                               ctypes.c_void_p(y.data_ptr()), 4, ctypes.c_void_p(ln.data_ptr()), 1e-6, 2,
+                               ctypes.c_void_p(ws.data_ptr()), ws.numel(), None)
+    assert rc == _lib.RV12_E_MODE
 
 
 def test_token_scales():

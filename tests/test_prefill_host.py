@@ -23,10 +23,11 @@ def test_enabled_follows_the_reference_variables(monkeypatch):
 
 def test_prefill_workspace_bytes():
     """Six bytes per column and token (three bf16 parts), tokens padded to
-    128, plus one scale exponent per padded token; 0 for bad arguments."""
+    128, plus a scale exponent and an RMS factor per padded token; 0 for bad
+    arguments."""
     from ai_amd import _lib
     L = _lib.lib()
-    assert L.rv12_prefill_workspace_bytes(4096, 2048) == 2048 * 4096 * 6 + 2048 * 4
-    assert L.rv12_prefill_workspace_bytes(1024, 300) == 384 * 1024 * 6 + 384 * 4
+    assert L.rv12_prefill_workspace_bytes(4096, 2048) == 2048 * 4096 * 6 + 2048 * 8
+    assert L.rv12_prefill_workspace_bytes(1024, 300) == 384 * 1024 * 6 + 384 * 8
     assert L.rv12_prefill_workspace_bytes(1000, 5) == 0 and L.rv12_prefill_workspace_bytes(1024, 0) == 0
     assert L.rv12_prefill_workspace_bytes(1024, (1 << 16) + 1) == 0
