@@ -20,7 +20,7 @@
 //      64 tokens.  Per 32-column step each wave reads its 4 row blocks' Q16
 //      tiles straight from memory, three steps ahead (they are the A operand
 //      of v_mfma_f32_16x16x32_bf16, the h values w 2^-sc); the step's B parts
-//      of the workgroup's 8 token blocks are loaded two steps ahead into
+//      of the workgroup's 8 token blocks are loaded three steps ahead into
 //      registers and pass through LDS (double-buffered, one barrier per
 //      step); 4 x 4 tiles x 3 parts = 48 MFMAs accumulate in 16 independent
 //      fp32 accumulators.  Epilogue: v = acc 2^(sc_row - P_t) (exact); the
@@ -40,6 +40,7 @@ constexpr int kPfRowBlocks = 16;  // row blocks (of 16 rows) per workgroup
 constexpr int kPfTokBlocks = 8;   // token blocks (of 16 tokens) per workgroup
 constexpr int kPfThreads = 512;
 constexpr int kPfDepth = 2;       // weight steps in flight per wave beyond the current one
+static_assert((kPfDepth + 1) % 3 == 0, "the B register ring (3 sets) is indexed by the unrolled step");
 
 // x' of token row xr at columns k..k+7 (MODE 2: silu(g) * u; lnw: the RMS
 // weight times x)
@@ -178,15 +179,25 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
 #pragma unroll
         for (int b = 0; b < 4; ++b) dst[b] = load_group(r, voff[b], soff);
     };
-    // the B parts of step s for the workgroup's token blocks: 3 groups per thread
+    // the B parts of step s for the workgroup's token blocks: 3 groups per
+    // thread, through a descriptor over the workgroup's parts (a step past the
+    // end reads zeros through a 0-byte one), so no load sits behind a branch
+    // and every wait counts only the loads it needs
     const u32x4* xbw = xb + (int64_t)tb0 * nsteps * 192;
-    auto load_b = [&](u32x4 (&dst)[3], int s) {
+    const __amdgpu_buffer_rsrc_t rbx = make_rsrc(xbw, (uint32_t)kPfTokBlocks * nsteps * 192 * 16);
+    const __amdgpu_buffer_rsrc_t rbnull = make_rsrc(xbw, 0u);
+    int boff[3];
 #pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int idx = tid + j * kPfThreads;  // (token block, part, lane) of the step
-            const int tbl = idx / 192, rem = idx % 192;
-            dst[j] = xbw[((int64_t)tbl * nsteps + s) * 192 + rem];
-        }
+    for (int j = 0; j < 3; ++j) {
+        const int idx = tid + j * kPfThreads;  // (token block, part, lane) of the step
+        boff[j] = ((idx / 192) * nsteps * 192 + idx % 192) * 16;
+    }
+    auto load_b = [&](u32x4 (&dst)[3], int s) {
+        const __amdgpu_buffer_rsrc_t r = s < nsteps ? rbx : rbnull;
+        const int soff = (s < nsteps ? s : 0) * 192 * 16;
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            dst[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, boff[j], soff, 0));
     };
     auto store_b = [&](const u32x4 (&src)[3], int buf) {
 #pragma unroll
@@ -201,21 +212,28 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     u32x3 ring[kPfDepth + 1][4];
 #pragma unroll
     for (int u = 0; u <= kPfDepth; ++u) issue_a(ring[u], u);
-    // B parts: loaded two steps ahead into a ring of three register sets,
-    // stored to LDS one step ahead (double buffer), so a store waits for a
-    // load issued a step earlier while the later loads stay in flight
+    // B parts: loaded three steps ahead into a ring of three register sets
+    // (the set of step s + 3 is the one step s's parts left, stored to LDS at
+    // the end of step s - 1), stored to LDS one step ahead (double buffer), so
+    // a store waits for a load issued two steps earlier while the later loads
+    // stay in flight
+    // The loop runs the steps in whole rounds of the unroll: steps past
+    // nsteps read zeros (A and B), add nothing, and keep the loop body free of
+    // branches around loads.
     u32x4 breg[3][3];
     load_b(breg[0], 0);
-    if (nsteps > 1) load_b(breg[1], 1);
+    load_b(breg[1], 1);
+    load_b(breg[2], 2);
     store_b(breg[0], 0);
     __syncthreads();
 
-    for (int s0 = 0; s0 < nsteps; s0 += kPfDepth + 1) {
+    const int nround = (nsteps + kPfDepth) / (kPfDepth + 1) * (kPfDepth + 1);
+    for (int s0 = 0; s0 < nround; s0 += kPfDepth + 1) {
 #pragma unroll
         for (int u = 0; u <= kPfDepth; ++u) {
             const int s = s0 + u;
-            if (s < nsteps) {
-                if (s + 2 < nsteps) load_b(breg[(u + 2) % 3], s + 2);
+            {
+                load_b(breg[u % 3], s + 3);  // u % 3 == s % 3: step s's set, already in LDS
                 // this wave's B fragments: 4 token blocks x 3 parts
                 u32x4 bf[4][3];
                 const u32x4* src = bs[s & 1] + (wc * 4) * 192 + lane;
@@ -231,13 +249,16 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
                     a[b] = u32x4{pr[0], pr[1], pr[2], pr[3]};
                 }
                 issue_a(ring[u], s + kPfDepth + 1);
+                // every fragment read is issued before the first MFMA, so the
+                // LDS latency is paid once per step, not between MFMAs
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int q = 0; q < 3; ++q)
 #pragma unroll
                     for (int b = 0; b < 4; ++b)
 #pragma unroll
                         for (int c = 0; c < 4; ++c) acc[b][c] = mfma(a[b], bf[c][q], acc[b][c]);
-                if (s + 1 < nsteps) store_b(breg[(u + 1) % 3], (s + 1) & 1);
+                store_b(breg[(u + 1) % 3], (s + 1) & 1);  // past the end: zeros nobody reads
                 __syncthreads();
             }
         }
