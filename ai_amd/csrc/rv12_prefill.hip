@@ -67,18 +67,21 @@ __device__ __forceinline__ void prefill_xprime(const float* xr, int K, int k, bo
     }
 }
 
-// 1. grid (token blocks of the padded T), 256 threads
-__global__ __launch_bounds__(256) void k_prefill_x(const float* __restrict__ x, int T, int K, int xs, int m2,
+// 1. grid (token blocks of the padded T), kPxThreads threads: 16 waves per
+// 16 tokens, so the few workgroups of a prompt keep enough loads in flight
+constexpr int kPxThreads = 1024;
+constexpr int kPxWaves = kPxThreads / 64;
+__global__ __launch_bounds__(kPxThreads) void k_prefill_x(const float* __restrict__ x, int T, int K, int xs, int m2,
                                                    const uint16_t* __restrict__ lnw, float eps,
                                                    u32x4* __restrict__ xb, int* __restrict__ P,
                                                    float* __restrict__ R) {
-    __shared__ int emax[4][16];
-    __shared__ float ssq[4][16];
+    __shared__ int emax[kPxWaves][16];
+    __shared__ float ssq[kPxWaves][16];
     __shared__ int ps[16];
     const int tb = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nsteps = K >> 5;
     // (a) the largest exponent of |x'| per token and, with RMS, the sum of
-    // squares of x 2^-32: thread (tok, sub) over columns 8 sub + 128 i
+    // squares of x 2^-32: thread (tok, sub) over columns 8 sub + 8 kPxThreads / 16 i
     {
         const int tok = tid & 15, sub = tid >> 4;
         const int t = tb * 16 + tok;
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(256) void k_prefill_x(const float* __restrict__ x, 
         float sq = 0.0f;
         if (t < T) {
             const float* xr = x + (int64_t)t * xs;
-            for (int k = sub * 8; k < K; k += 128) {
+            for (int k = sub * 8; k < K; k += kPxThreads / 2) {
                 float v[8];
                 prefill_xprime(xr, K, k, m2 != 0, nullptr, v);
                 if (lnw) {
@@ -115,19 +118,24 @@ __global__ __launch_bounds__(256) void k_prefill_x(const float* __restrict__ x, 
     }
     __syncthreads();
     if (tid < 16) {
-        const int e = max(max(emax[0][tid], emax[1][tid]), max(emax[2][tid], emax[3][tid]));
+        int e = emax[0][tid];
+        float q = ssq[0][tid];
+        for (int w = 1; w < kPxWaves; ++w) {  // a fixed order
+            e = max(e, emax[w][tid]);
+            q += ssq[w][tid];
+        }
         const int p = (e >= -39 && e <= kXRangeHi) ? kXScaleExp : slow_scale_exp(e);
         ps[tid] = p;
         P[tb * 16 + tid] = p;
-        if (lnw) R[tb * 16 + tid] = rms_scale((ssq[0][tid] + ssq[1][tid]) + (ssq[2][tid] + ssq[3][tid]), K, eps);
+        if (lnw) R[tb * 16 + tid] = rms_scale(q, K, eps);
     }
     __syncthreads();
-    // (b) the parts: thread (tok, k8, ss) writes step s0 + ss, lane 16 k8 + tok
+    // (b) the parts: thread (tok, k8, ss) writes steps ss + kPxWaves i, lane 16 k8 + tok
     const int tok = tid & 15, k8 = (tid >> 4) & 3, ss = tid >> 6;
     const int t = tb * 16 + tok;
     const int p = ps[tok];
     const float* xr = x + (int64_t)min(t, T - 1) * xs;
-    for (int s = ss; s < nsteps; s += 4) {
+    for (int s = ss; s < nsteps; s += kPxWaves) {
         u32x4 hi = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
         if (t < T) {
             float v[8];
@@ -362,7 +370,7 @@ void launch_prefill(const rv12_matrix& w, const float* x, float* y, int T, int m
     int* P = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + (size_t)tp * K * 6);
     float* R = reinterpret_cast<float*>(P + tp);
     const int xs = mode == 2 ? 2 * K : K;
-    hipLaunchKernelGGL(k_prefill_x, dim3(tp / 16), dim3(256), 0, st, x, T, K, xs, mode == 2 ? 1 : 0, lnw, eps, xb, P,
+    hipLaunchKernelGGL(k_prefill_x, dim3(tp / 16), dim3(kPxThreads), 0, st, x, T, K, xs, mode == 2 ? 1 : 0, lnw, eps, xb, P,
                        R);
     const int64_t nblk = ((int64_t)N + 15) / 16;
     const dim3 grid((unsigned)((nblk + kPfRowBlocks - 1) / kPfRowBlocks), (unsigned)(tp / (kPfTokBlocks * 16)));

@@ -266,6 +266,32 @@ def run_e2e(dev, size="8b", prompt_len=2048, new=256, seed=0, batch=None, prefil
     return out
 
 
+def run_prefill(dev, size="8b", prompt_len=2048, reps=3, seed=0):
+    """The blocked prefill alone (every layer's fused linears and prompt
+    attention over the whole prompt, then the head's pick), `reps` times
+    after a warm pass: ms per prompt."""
+    from ai_amd.engine import Engine
+    from ai_amd.model import QWEN3, RandomCkpt
+    ck = RandomCkpt(QWEN3[size], seed=seed)
+    eng = Engine(ck, maxt=prompt_len + 8, kv_dtype=torch.bfloat16, prefill="blocked")
+    prompt = [int(t) for t in np.random.default_rng(seed).integers(0, ck.V, prompt_len)]
+    eng.prefill(prompt)
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(reps):
+        eng.reset()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        eng.prefill(prompt)
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+        print(f"# prefill {prompt_len} tokens: {ms[-1]:.1f} ms", file=sys.stderr, flush=True)
+    del eng
+    torch.cuda.empty_cache()
+    return {"model": f"qwen3-{size} random init", "prompt": prompt_len, "kv_cache": "bf16", "prefill_ms": ms}
+
+
 def measure_h2d(dev, nbytes=1 << 30, reps=5):
     """Pinned host -> HBM copy rate (one 1 GiB hipMemcpyAsync, HIP events):
     the ceiling of the streamed placement."""
@@ -558,6 +584,8 @@ def main():
     ap.add_argument("--only-attn", action="store_true", help="run only the Qwen3-8B decode attention (for profiling)")
     ap.add_argument("--only-e2e", action="store_true",
                     help="run only the Qwen3-8B end-to-end decode (2048-token prompt, 256 tokens; for profiling)")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="run only the Qwen3-8B blocked prefill of a 2048-token prompt, 3 times (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (scale factor of the HBM byte counters)")
     args = ap.parse_args()
@@ -585,6 +613,9 @@ def main():
         return
     if args.only_e2e:
         print(json.dumps(run_e2e(dev)), flush=True)
+        return
+    if args.only_prefill:
+        print(json.dumps(run_prefill(dev)), flush=True)
         return
 
     tok = run_token_bench(args, dev)
