@@ -40,7 +40,7 @@ bool shape_fits(int K, int T, const Shape& c) {
 //     CUs, and wherever the activations would not fit in registers;
 //   MFMA kernel: the shape with the least time in a model of its rounds of
 //     workgroups (mfma_model_us);
-// The MFMA kernel is the built-in choice from 3 tokens on, except at 3-4
+// The MFMA kernel is the built-in choice from 3 tokens on, except at 3
 // tokens on small matrices (up to 512 row blocks, K <= 6144), where the
 // vector kernel's FMAs still hide behind its weight stream; and at 2 tokens
 // where the vector kernel would have to split K to hold its activations in
@@ -75,37 +75,40 @@ Shape vector_shape(int N, int K, int T) {
     return c;
 }
 
-// Time model of the MFMA kernel, in us (constants from register timestamps
-// and launch-shape sweeps on MI355X).  A workgroup stages x' for its K split
-// in LDS before streaming, so the launch runs in rounds: one workgroup per CU
-// at 8 waves (registers allow two waves per SIMD), two at 4 waves where the
-// LDS holds both.  Each round costs a fixed prologue (kernel arguments, x'
-// staging, barrier: ~5 us at 16 tokens) plus its weight bytes at the smaller
-// of the HBM rate and 45 GB/s per active CU (the bytes one CU keeps in
-// flight over the memory latency); a K split adds the reduce pass.  The model
-// ranks the measured 8B/14B/32B shapes at 8-16 tokens as the sweeps do (e.g.
-// 32B o 5120x8192: 2 row blocks per wave, 160 workgroups, 20 us; 4 row blocks,
-// 90 workgroups, 30 us).
-constexpr double kModelPrologueUs = 5.0;
-constexpr double kModelHbmGBs = 6500.0;
-constexpr double kModelCuGBs = 45.0;
-constexpr double kModelLaunchUs = 1.6;
+// Time model of the MFMA kernel, in us.  A workgroup stages x' for its K
+// split in LDS before streaming, so the launch runs in rounds of one
+// workgroup per CU.  Each round costs a fixed part plus the staging of its
+// split (per K step) plus its weight bytes at the smaller of the HBM rate and
+// a per-CU rate (the bytes one CU keeps in flight over the memory latency); a
+// K split adds the reduce pass, a launch plus a cost per MB of partials.  The
+// constants are fitted to a sweep of every launch shape of the kernel on 16
+// Qwen3-8B/14B/32B shapes at 4, 8 and 16 tokens on MI355X: the model's pick
+// lies within 0.5 % of the measured best on average and 6.6 % at worst
+// (4 % at worst for a shape left out of the fit), where the earlier model
+// (a 5 us prologue per round whatever the split) lost 5.2 % on average and
+// 19 % at worst (Qwen3-8B o 4096x4096 at 16 tokens: 13.4 against 11.3 us).
+constexpr double kModelRoundUs = 1.0;
+constexpr double kModelStepUs = 0.1;
+constexpr double kModelHbmGBs = 7500.0;
+constexpr double kModelCuGBs = 30.0;
+constexpr double kModelReduceUs = 1.0;
+constexpr double kModelReduceUsPerMB = 2.0;
 constexpr int kModelCUs = 256;
 constexpr double kModelStepBytes = 768.0;  // one (row block, step) tile
 
 double mfma_model_us(int64_t nblk, int N, int K, int T, int rb, int waves, int splits) {
     const int64_t per_wg = (int64_t)rb * waves;
     const int64_t wgs = (nblk + per_wg - 1) / per_wg * splits;
-    const int per_cu = (waves <= 4 && 2 * gemm_lds_bytes(K, rb, waves, splits) <= kMaxLds) ? 2 : 1;
-    const double wg_bytes = (double)per_wg * split_steps(K, splits) * kModelStepBytes;
+    const int steps = split_steps(K, splits);
+    const double wg_bytes = (double)per_wg * steps * kModelStepBytes;
     double t = 0.0;
     for (int64_t left = wgs; left > 0;) {
-        const int64_t n = std::min<int64_t>(left, (int64_t)kModelCUs * per_cu);
-        const double active = (double)std::min<int64_t>(n, kModelCUs);
-        t += kModelPrologueUs + (double)n * wg_bytes / (std::min(kModelHbmGBs, active * kModelCuGBs) * 1e3);
+        const int64_t n = std::min<int64_t>(left, (int64_t)kModelCUs);
+        t += kModelRoundUs + kModelStepUs * steps +
+             (double)n * wg_bytes / (std::min(kModelHbmGBs, (double)n * kModelCuGBs) * 1e3);
         left -= n;
     }
-    if (splits > 1) t += kModelLaunchUs + (double)(splits + 1) * T * N * 4 / (kModelHbmGBs * 1e3);
+    if (splits > 1) t += kModelReduceUs + kModelReduceUsPerMB * (double)(splits + 1) * T * N * 4 / 1e6;
     return t;
 }
 
@@ -146,15 +149,15 @@ Shape default_shape(int N, int K, int T) {
     const int nsteps = K / 32;
     bool vec = T <= kVectorDefaultTokens;
     if (T == 2 && !gemv_prefetch_all(K, T, vector_shape(N, K, T).waves, 1)) vec = false;
-    // 3-4 tokens on up to 512 row blocks of K <= 6144: the vector kernel,
-    // unsplit unless below 128 row blocks, beats the MFMA kernel's staging
-    // and split-K reduce (MI355X: Qwen3-8B qkv 14.8 -> 12.1 us and o 10.9 ->
-    // 9.6 at 3 tokens, 14.4 -> 13.0 and 10.7 -> 10.4 at 4; 14B k/v 9.1 ->
-    // 7.8 / 9.2 -> 8.2, qkv 16.2 -> 15.9 / 16.3 -> 16.0, o 14.6 -> 13.7 at 3
-    // tokens); larger or longer matrices keep the MFMA kernel (14B down
-    // 32.5 against 43.5, gate/up 29.9 against 34.7)
-    const bool vec34 = (T == 3 || T == 4) && K <= 6144 && nblocks(N) <= 512;
-    vec = vec || vec34;
+    // 3 tokens on up to 512 row blocks of K <= 6144: the vector kernel,
+    // unsplit unless below 128 row blocks, matches or beats the MFMA kernel's
+    // best shape (MI355X: Qwen3-8B qkv 12.1 against 12.8 us, o 9.6 against
+    // 10.6; Qwen3-14B o, qkv, k/v within 1 %); at 4 tokens the MFMA kernel
+    // wins (14B o 13.6 against 14.8 us, k/v 7.9 against 8.2), and larger or
+    // longer matrices keep it (14B down 32.5 against 43.5, gate/up 29.9
+    // against 34.7 at 3 tokens)
+    const bool vec3 = T == 3 && K <= 6144 && nblocks(N) <= 512;
+    vec = vec || vec3;
     Shape c = vec ? vector_shape(N, K, T) : mfma_shape(N, K, T);
     while (c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
     // at one token the vector kernel's waves want at least 8 K steps each
@@ -163,7 +166,7 @@ Shape default_shape(int N, int K, int T) {
     while (c.splits < kMaxSplits && c.splits < nsteps && !shape_fits(K, T, c)) ++c.splits;
     // the vector kernel streams best with all activations loaded before the weights
     const int s_fit = c.splits;
-    while (c.kernel == 1 && !vec34 && c.splits < kMaxSplits && c.splits < nsteps &&
+    while (c.kernel == 1 && !vec3 && c.splits < kMaxSplits && c.splits < nsteps &&
            !gemv_prefetch_all(K, T, c.waves, c.splits))
         ++c.splits;
     if (c.splits > s_fit) {

@@ -85,19 +85,19 @@ def test_launch_shapes():
     assert shape(5120, 17408, 2)[0] == 2                  # Qwen3-14B down at 2 tokens: MFMA
     assert shape(7168, 5120, 2) == (1, 2, 8, 1)           # 14B qkv at 2 tokens: vector, unsplit, 2 row blocks
     assert shape(5120, 8192, 2) == (1, 1, 16, 1)          # 32B o at 2 tokens: K > 6144 keeps one row block
-    # 3-4 tokens on up to 512 row blocks of K <= 6144: the vector kernel
+    # 3 tokens on up to 512 row blocks of K <= 6144: the vector kernel
     assert shape(6144, 4096, 3) == (1, 2, 8, 1)           # 8B qkv: two row blocks, unsplit
-    assert shape(4096, 4096, 4) == (1, 1, 8, 1)           # 8B o
     assert shape(1024, 5120, 3) == (1, 1, 8, 4)           # 14B k/v: split below 128 row blocks
     assert shape(5120, 17408, 3)[0] == 2                  # 14B down: MFMA
-    assert shape(17408, 5120, 4)[0] == 2                  # 14B gate/up: MFMA (1088 row blocks)
-    assert shape(4096, 4096, 5)[0] == 2                   # 5 tokens: MFMA
+    assert shape(4096, 4096, 4)[0] == 2                   # 4 tokens: MFMA
     # the MFMA kernel's time model picks the shapes the MI355X sweeps found best
+    assert shape(4096, 4096, 8) == (2, 1, 8, 8)           # 8B o: 256 workgroups of 16 K steps
+    assert shape(6144, 4096, 4) == (2, 2, 8, 10)          # 8B qkv: 240 workgroups
+    assert shape(1024, 5120, 16) == (2, 1, 4, 16)         # 14B k/v: 64 row blocks, 16 splits of 10 steps
+    assert shape(5120, 5120, 4) == (2, 2, 8, 12)          # 14B o: 240 workgroups of 14 K steps
     assert shape(5120, 17408, 16)[:3] == (2, 4, 8)        # 14B down: four row blocks per wave
-    assert shape(1024, 5120, 16)[:3] == (2, 1, 4)         # 14B k/v: 64 row blocks
-    assert shape(5120, 5120, 8) == (2, 1, 8, 5)           # 14B o: one row block per wave, 200 workgroups
-    assert shape(5120, 8192, 16)[:3] == (2, 2, 8)         # 32B o: two (four would leave 90 workgroups)
-    assert shape(5120, 25600, 8)[:3] == (2, 2, 8)         # 32B down
+    assert shape(5120, 8192, 16) == (2, 2, 8, 12)         # 32B o
+    assert shape(5120, 25600, 8) == (2, 2, 8, 25)         # 32B down
     # 4 waves of the MFMA kernel stage at most 16 steps: K = 5120 is split 10 ways
     assert shape(5120, 5120, 16, _lib.Launch(2, 2, 4, 0)) == (2, 2, 4, 10)
     assert shape(5120, 5120, 1, _lib.Launch(1, 1, 4, 3)) == (1, 1, 4, 3)
