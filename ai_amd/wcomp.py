@@ -262,7 +262,7 @@ def _launch(BN, w, S, T):
     row blocks per wave times waves in the MFMA kernel (T > 2).  A given BN
     names its kernel; without one the library picks (rv12_launch_shape: the
     vector kernel up to 2 tokens, except where it would have to split K at 2
-    tokens, and at 3-4 tokens on small matrices)."""
+    tokens, and at 3 tokens on small matrices)."""
     rb = kernel = 0
     if BN:
         vec = T <= VECTOR_TOKENS

@@ -90,7 +90,7 @@ typedef struct rv12_launch {
 /* The launch shape a linear of n rows, k columns and t tokens runs with for
  * cfg (NULL or all-zero: the built-in choice — the vector kernel up to 2
  * tokens, at 2 only while its activations fit in registers without splitting
- * K, and at 3-4 tokens on matrices of up to 512 row blocks and k <= 6144;
+ * K, and at 3 tokens on matrices of up to 512 row blocks and k <= 6144;
  * the MFMA kernel otherwise, with waves, row blocks and splits from
  * launch-shape sweeps on MI355X; zero fields of a partial cfg are filled in,
  * with K split further where the given fields need it).  Fills *out and
