@@ -7,27 +7,33 @@
 // y[t] (=|+=) W_dec . x'[t], t < T, with the MODE prologue (2: x' =
 // silu(x[0:K]) * x[K:2K]) or the RMSNorm prologue of mode 0 (x' = lnw x,
 // the token's rs = 1 / sqrt(mean x^2 + eps) applied to its outputs, as the
-// decode kernels apply it).  Two passes:
-//   1. k_prefill_x: one workgroup per 16 tokens: each token's exponent scale
+// decode kernels apply it).  Three launches:
+//   1. k_prefill_stats (one wave per token): each token's exponent scale
 //      P_t (64 when its largest |x'| lies in [2^-40, 2^63), else 100 minus
 //      the exponent of the largest) and, with RMS, its rs (sum of squares of
-//      x 2^-32), then x' 2^P_t split into bf16 parts
+//      x 2^-32); k_prefill_parts (32 tokens x 64 columns per workgroup):
+//      x' 2^P_t split into bf16 parts
 //      hi + mid + lo (24 significand bits, as the reference's _x3 split,
 //      wcomp.py:130-140) in B-operand lane order: for token block tb, step
 //      s (32 columns) and part, 64 lanes x 8 bf16 (lane l: token l%16,
-//      k = 8(l/16) + 0..7).  Token rows past T are zeros.
+//      k = 8(l/16) + 0..7), and x' itself in fp32, transposed (column-major
+//      over the padded tokens).  Token rows past T are zeros.
 //   2. k_prefill_mm: workgroup = 256 rows x 128 tokens, 8 waves of 64 rows x
-//      64 tokens.  Per 32-column step each wave reads its 4 row blocks' Q16
-//      tiles straight from memory, three steps ahead (they are the A operand
-//      of v_mfma_f32_16x16x32_bf16, the h values w 2^-sc); the step's B parts
-//      of the workgroup's 8 token blocks are loaded three steps ahead into
-//      registers and pass through LDS (double-buffered, one barrier per
-//      step); 4 x 4 tiles x 3 parts = 48 MFMAs accumulate in 16 independent
-//      fp32 accumulators.  Epilogue: v = acc 2^(sc_row - P_t) (exact); the
-//      packed form's exception entries of the wave's rows (weights outside a
-//      row's window, zeros in the tiles) add ev * x'[t][col] in list order,
-//      x' gathered from x in fp32; with RMS v is scaled by rs_t; then y is
-//      stored or added; rows past N and tokens past T are skipped.
+//      64 tokens.  Per 32-column step the workgroup's 16 row blocks' Q16
+//      tiles (the A operand of v_mfma_f32_16x16x32_bf16, the h values
+//      w 2^-sc) and the B parts of its 8 token blocks go from memory straight
+//      into a ring of four LDS slots (buffer loads with the LDS destination;
+//      no register holds them on the way, every wait is explicit), three
+//      steps ahead; one wait + barrier per step; each wave reads the next
+//      step's fragments while its 48 MFMAs of the current step run; the MFMAs
+//      accumulate in 16 independent fp32 accumulators.  Epilogue:
+//      v = acc 2^(sc_row - P_t) (exact); the packed form's exception entries
+//      of the wave's rows (weights outside a row's window, zeros in the
+//      tiles) add ev * x'[t][col] in list order, x' read from the transposed
+//      copy (one column of the wave's 64 tokens is 256 contiguous bytes,
+//      where the rows of x would take a cache line per token); with RMS v is
+//      scaled by rs_t; then y is stored or added; rows past N and tokens past
+//      T are skipped.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -39,8 +45,24 @@ namespace rv12 {
 constexpr int kPfRowBlocks = 16;  // row blocks (of 16 rows) per workgroup
 constexpr int kPfTokBlocks = 8;   // token blocks (of 16 tokens) per workgroup
 constexpr int kPfThreads = 512;
-constexpr int kPfDepth = 2;       // weight steps in flight per wave beyond the current one
-static_assert((kPfDepth + 1) % 3 == 0, "the B register ring (3 sets) is indexed by the unrolled step");
+constexpr int kPfRing = 4;  // LDS slots: the A tiles and B parts of steps s .. s + 3
+// slot layout (u32x4 units): 16 A tiles of 1 KB (a 12-byte-per-lane load with
+// the LDS destination writes lane l at 16 l: 768 B of each KB), then the B
+// parts (8 token blocks x 3 parts x 64 lanes)
+constexpr int kPfSlotA = kPfRowBlocks * 64;
+constexpr int kPfSlot = kPfSlotA + kPfTokBlocks * 3 * 64;  // 40 KB
+constexpr size_t kPfLds = (size_t)kPfRing * kPfSlot * 16;   // 160 KB
+static_assert(kPfLds <= 160 * 1024, "gfx950 LDS per workgroup");
+// loads a wave issues per step: 2 A tiles and 3 B chunks, all into LDS
+constexpr int kPfOpsPerStep = kPfRowBlocks / (kPfThreads / 64) + 3;
+// at the top of step s, the wave's loads of step s + 1 (issued at step
+// s + 1 - kPfRing) are followed by those of the kPfRing - 2 steps between
+constexpr int kPfWait = kPfOpsPerStep * (kPfRing - 2);
+static_assert(kPfWait < 64, "vmcnt holds 6 bits");
+// s_waitcnt immediates (gfx9 encoding): vmcnt(n) and lgkmcnt(0), expcnt not
+// waited for; vmcnt(n) alone
+constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
+constexpr int waitcnt_vm(int n) { return waitcnt_vm_lgkm0(n) | (15 << 8); }
 
 // x' of token row xr at columns k..k+7 (MODE 2: silu(g) * u; lnw: the RMS
 // weight times x)
@@ -67,130 +89,146 @@ __device__ __forceinline__ void prefill_xprime(const float* xr, int K, int k, bo
     }
 }
 
-// 1. grid (token blocks of the padded T), kPxThreads threads: 16 waves per
-// 16 tokens, so the few workgroups of a prompt keep enough loads in flight
-constexpr int kPxThreads = 1024;
-constexpr int kPxWaves = kPxThreads / 64;
-__global__ __launch_bounds__(kPxThreads) void k_prefill_x(const float* __restrict__ x, int T, int K, int xs, int m2,
-                                                   const uint16_t* __restrict__ lnw, float eps,
-                                                   u32x4* __restrict__ xb, int* __restrict__ P,
-                                                   float* __restrict__ R) {
-    __shared__ int emax[kPxWaves][16];
-    __shared__ float ssq[kPxWaves][16];
-    __shared__ int ps[16];
-    const int tb = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nsteps = K >> 5;
-    // (a) the largest exponent of |x'| per token and, with RMS, the sum of
-    // squares of x 2^-32: thread (tok, sub) over columns 8 sub + 8 kPxThreads / 16 i
-    {
-        const int tok = tid & 15, sub = tid >> 4;
-        const int t = tb * 16 + tok;
-        int e = -1000;
-        float sq = 0.0f;
-        if (t < T) {
-            const float* xr = x + (int64_t)t * xs;
-            for (int k = sub * 8; k < K; k += kPxThreads / 2) {
-                float v[8];
-                prefill_xprime(xr, K, k, m2 != 0, nullptr, v);
-                if (lnw) {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) sq += (v[i] * kSsqScale) * (v[i] * kSsqScale);
-                    const u32x4 w = *reinterpret_cast<const u32x4*>(lnw + k);
-                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        v[2 * i] *= __uint_as_float(ww[i] << 16);
-                        v[2 * i + 1] *= __uint_as_float(ww[i] & 0xFFFF0000u);
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < 8; ++i) e = max(e, exp_or_min(v[i]));
-            }
-        }
-        e = max(e, __shfl_xor(e, 16));
-        e = max(e, __shfl_xor(e, 32));
-        sq += __shfl_xor(sq, 16);
-        sq += __shfl_xor(sq, 32);
-        if (lane < 16) {
-            emax[wave][lane] = e;
-            ssq[wave][lane] = sq;
-        }
-    }
-    __syncthreads();
-    if (tid < 16) {
-        int e = emax[0][tid];
-        float q = ssq[0][tid];
-        for (int w = 1; w < kPxWaves; ++w) {  // a fixed order
-            e = max(e, emax[w][tid]);
-            q += ssq[w][tid];
-        }
-        const int p = (e >= -39 && e <= kXRangeHi) ? kXScaleExp : slow_scale_exp(e);
-        ps[tid] = p;
-        P[tb * 16 + tid] = p;
-        if (lnw) R[tb * 16 + tid] = rms_scale(q, K, eps);
-    }
-    __syncthreads();
-    // (b) the parts: thread (tok, k8, ss) writes steps ss + kPxWaves i, lane 16 k8 + tok
-    const int tok = tid & 15, k8 = (tid >> 4) & 3, ss = tid >> 6;
-    const int t = tb * 16 + tok;
-    const int p = ps[tok];
-    const float* xr = x + (int64_t)min(t, T - 1) * xs;
-    for (int s = ss; s < nsteps; s += kPxWaves) {
-        u32x4 hi = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
-        if (t < T) {
+// 1a. k_prefill_stats: one wave per token (4 per workgroup, a grid over the
+// padded tokens): the largest exponent of |x'| and, with RMS, the sum of
+// squares of x 2^-32, lane l over columns 8 l + 512 i, reduced across the
+// wave in a fixed order; writes the token's scale exponent P_t and rs_t.
+constexpr int kPsThreads = 256;
+__global__ __launch_bounds__(kPsThreads) void k_prefill_stats(const float* __restrict__ x, int T, int K, int xs,
+                                                              int m2, const uint16_t* __restrict__ lnw, float eps,
+                                                              int* __restrict__ P, float* __restrict__ R) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * (kPsThreads / 64) + (threadIdx.x >> 6);
+    int e = -1000;
+    float sq = 0.0f;
+    if (t < T) {
+        const float* xr = x + (int64_t)t * xs;
+        for (int k = lane * 8; k < K; k += 512) {
             float v[8];
-            prefill_xprime(xr, K, s * 32 + k8 * 8, m2 != 0, lnw, v);
+            prefill_xprime(xr, K, k, m2 != 0, nullptr, v);
+            if (lnw) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = ldexpf(v[i], p);
-            split3(v, hi, mid, lo);
+                for (int i = 0; i < 8; ++i) sq += (v[i] * kSsqScale) * (v[i] * kSsqScale);
+                const u32x4 w = *reinterpret_cast<const u32x4*>(lnw + k);
+                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[2 * i] *= __uint_as_float(ww[i] << 16);
+                    v[2 * i + 1] *= __uint_as_float(ww[i] & 0xFFFF0000u);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) e = max(e, exp_or_min(v[i]));
         }
-        u32x4* d = xb + ((int64_t)tb * nsteps + s) * 192 + k8 * 16 + tok;
-        d[0] = hi;
-        d[64] = mid;
-        d[128] = lo;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        e = max(e, __shfl_xor(e, o));
+        sq += __shfl_xor(sq, o);
+    }
+    if (lane == 0) {
+        P[t] = (e >= -39 && e <= kXRangeHi) ? kXScaleExp : slow_scale_exp(e);
+        if (lnw) R[t] = rms_scale(sq, K, eps);
     }
 }
 
-// 2. grid (row tiles of 256 rows, token tiles of 128), 512 threads.  M2 / LN
-// (the silu(g) * u and RMS prologues) are template arguments, so that the
-// exception gathers of the epilogue are straight-line loads per variant.
-template <bool M2, bool LN>
+// 1b. k_prefill_parts: grid (32-token blocks, 64-column chunks), 256 threads,
+// thread (token tok, 8-column group k8): x' (prologue applied) of token t at
+// columns kc .. kc + 7 written transposed (per column, 32 consecutive tokens:
+// full 128-byte lines), then x' 2^P_t split into the bf16 parts in B-operand
+// lane order.  Tokens past T are zeros.
+constexpr int kPpThreads = 256;
+__global__ __launch_bounds__(kPpThreads) void k_prefill_parts(const float* __restrict__ x, int T, int K, int xs,
+                                                              int m2, const uint16_t* __restrict__ lnw,
+                                                              const int* __restrict__ P, u32x4* __restrict__ xb,
+                                                              float* __restrict__ xt, int tp) {
+    const int tok = threadIdx.x & 31, k8 = threadIdx.x >> 5;
+    const int t = blockIdx.x * 32 + tok;
+    const int kc = blockIdx.y * 64 + k8 * 8;
+    if (kc >= K) return;
+    const int nsteps = K >> 5;
+    float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (t < T) prefill_xprime(x + (int64_t)t * xs, K, kc, m2 != 0, lnw, v);
+    float* xc = xt + (int64_t)kc * tp + t;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xc[(int64_t)i * tp] = v[i];
+    u32x4 hi = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
+    if (t < T) {
+        const int p = P[t];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = ldexpf(v[i], p);
+        split3(v, hi, mid, lo);
+    }
+    const int s = kc >> 5, g = (kc & 31) >> 3;  // step, 8-column group in the step
+    u32x4* d = xb + ((int64_t)(t >> 4) * nsteps + s) * 192 + g * 16 + (t & 15);
+    d[0] = hi;
+    d[64] = mid;
+    d[128] = lo;
+}
+
+// Workgroup i -> (row tile, token tile).  Workgroups are dispatched in order,
+// round-robin over the 8 XCDs (each with its own L2): i runs on XCD i % 8 as
+// its (i / 8)-th.  The virtual index v gives each XCD a contiguous range of
+// G / 8 tiles (the remainder past 8 (G / 8) keeps v = i), and v runs over
+// groups of kPfGroupRows row tiles x all token tiles, row tile fastest, so the
+// ~32 workgroups an XCD holds at once cover 8 row tiles x 4 token tiles: per
+// step their L2 misses are 8 A tiles (12 KB each) and 4 B sets (24 KB each),
+// 192 KB, where 2 row tiles x 16 token tiles (the Qwen3-8B o and down in
+// launch order) would miss 408 KB.  A bijection of [0, G).
+constexpr int kPfGroupRows = 8;
+__device__ __forceinline__ void prefill_tile(int i, int G, int nx, int ny, int& rt, int& tt) {
+    const int g8 = G / 8;
+    const int v = i < g8 * 8 ? (i % 8) * g8 + i / 8 : i;
+    const int per = kPfGroupRows * ny;
+    const int g = v / per, r0 = g * kPfGroupRows;
+    const int gr = min(kPfGroupRows, nx - r0);
+    const int w = v - g * per;
+    tt = w / gr;
+    rt = r0 + w % gr;
+}
+
+// 2. grid (row tiles of 256 rows x token tiles of 128, in the order above),
+// 512 threads.  LN (the RMS prologue: each token's rs applied to its outputs)
+// is a template argument; the prologues themselves were applied in the
+// pre-pass, to the parts and to the transposed x' (xt, row stride tp).
+template <bool LN>
 __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __restrict__ tiles,
                                                            const int32_t* __restrict__ rbase,
                                                            const u32x4* __restrict__ xb, const int* __restrict__ P,
                                                            const int32_t* __restrict__ rp,
                                                            const int32_t* __restrict__ er,
                                                            const int32_t* __restrict__ ec,
-                                                           const float* __restrict__ ev, const float* __restrict__ x,
-                                                           const uint16_t* __restrict__ lnw,
-                                                           const float* __restrict__ R, float* __restrict__ y, int N,
-                                                           int K, int T, int xs, int m2, int add) {
-    __shared__ u32x4 bs[2][kPfTokBlocks * 3 * 64];  // 2 x 24 KB
+                                                           const float* __restrict__ ev, const float* __restrict__ xt,
+                                                           int tp, const float* __restrict__ R, float* __restrict__ y,
+                                                           int N, int K, int T, int add) {
+    extern __shared__ u32x4 bs[];  // [kPfRing][kPfSlot]: A tiles and B parts of steps s .. s + 3
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wr = wave & 3, wc = wave >> 2;
     const int nsteps = K >> 5;
     const int64_t nblk = (N + 15) / 16;
-    const int64_t blk0 = (int64_t)blockIdx.x * kPfRowBlocks + wr * 4;  // this wave's first row block
-    const int tb0 = blockIdx.y * kPfTokBlocks;                            // the workgroup's first token block
-    const int nvalid = (int)max((int64_t)0, min((int64_t)4, nblk - blk0));
+    const int nx = (int)((nblk + kPfRowBlocks - 1) / kPfRowBlocks);
+    int rt, tt;
+    prefill_tile(blockIdx.x, gridDim.x, nx, gridDim.x / nx, rt, tt);
+    const int64_t blk0 = (int64_t)rt * kPfRowBlocks + wr * 4;  // this wave's first row block
+    const int tb0 = tt * kPfTokBlocks;                          // the workgroup's first token block
     const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
-    const char* wbase = reinterpret_cast<const char*>(tiles) + blk0 * (int64_t)blk_bytes;
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, (uint32_t)nvalid * blk_bytes);
-    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(wbase, 0u);
-    int voff[4];
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    // the workgroup's A tiles: wave w loads row blocks 2w and 2w + 1 of the
+    // workgroup through a descriptor over its valid row blocks (a row block
+    // past N, or a step past the end through the 0-byte descriptor, reads
+    // zeros)
+    const int64_t wblk0 = (int64_t)rt * kPfRowBlocks;
+    const int nvalid_wg = (int)max((int64_t)0, min((int64_t)kPfRowBlocks, nblk - wblk0));
+    const char* wgbase = reinterpret_cast<const char*>(tiles) + wblk0 * (int64_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(wgbase, (uint32_t)nvalid_wg * blk_bytes);
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(wgbase, 0u);
+    constexpr int kAPerWave = kPfRowBlocks / (kPfThreads / 64);
+    int aoff[kAPerWave];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) voff[b] = (int)(b * blk_bytes) + lane * 12;
-    auto issue_a = [&](u32x3 (&dst)[4], int s) {
-        const __amdgpu_buffer_rsrc_t r = s < nsteps ? rv : rnull;
-        const int soff = (s < nsteps ? s : 0) * kStepBytes;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) dst[b] = load_group(r, voff[b], soff);
-    };
-    // the B parts of step s for the workgroup's token blocks: 3 groups per
-    // thread, through a descriptor over the workgroup's parts (a step past the
-    // end reads zeros through a 0-byte one), so no load sits behind a branch
-    // and every wait counts only the loads it needs
+    for (int i = 0; i < kAPerWave; ++i) aoff[i] = (int)((wave * kAPerWave + i) * blk_bytes) + lane * 12;
+    // the B parts of the workgroup's token blocks: 3 chunks of 64 lanes x
+    // 16 B per wave, through a descriptor over the workgroup's parts
     const u32x4* xbw = xb + (int64_t)tb0 * nsteps * 192;
     const __amdgpu_buffer_rsrc_t rbx = make_rsrc(xbw, (uint32_t)kPfTokBlocks * nsteps * 192 * 16);
     const __amdgpu_buffer_rsrc_t rbnull = make_rsrc(xbw, 0u);
@@ -200,16 +238,38 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
         const int idx = tid + j * kPfThreads;  // (token block, part, lane) of the step
         boff[j] = ((idx / 192) * nsteps * 192 + idx % 192) * 16;
     }
-    auto load_b = [&](u32x4 (&dst)[3], int s) {
-        const __amdgpu_buffer_rsrc_t r = s < nsteps ? rbx : rbnull;
-        const int soff = (s < nsteps ? s : 0) * 192 * 16;
+    // step s's A tiles and B parts into LDS slot `slot`; a step past the end
+    // goes through the 0-byte descriptors, which write zeros, so the loop has
+    // no branch around a load
+    auto load_step = [&](int slot, int s) {
+        const bool in = s < nsteps;
+        const __amdgpu_buffer_rsrc_t ra = in ? rv : rnull, rb = in ? rbx : rbnull;
+        const int sa = (in ? s : 0) * kStepBytes, sb = (in ? s : 0) * 192 * 16;
+        u32x4* d = bs + slot * kPfSlot;
+#pragma unroll
+        for (int i = 0; i < kAPerWave; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)(d + (wave * kAPerWave + i) * 64), 12, aoff[i], sa,
+                                                     0, 0);
 #pragma unroll
         for (int j = 0; j < 3; ++j)
-            dst[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, boff[j], soff, 0));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr)(d + kPfSlotA + wave * 64 + j * kPfThreads), 16,
+                                                     boff[j], sb, 0, 0);
     };
-    auto store_b = [&](const u32x4 (&src)[3], int buf) {
+    // this wave's fragments of the step in slot `slot`: its 4 row blocks' A
+    // groups (12 bytes per lane) and 3 parts x 4 token blocks of B,
+    // part-major so the first part's MFMAs wait only for its own reads
+    auto read_frags = [&](u32x3 (&ra)[4], u32x4 (&rb)[3][4], int slot) {
+        const u32x4* d = bs + slot * kPfSlot;
 #pragma unroll
-        for (int j = 0; j < 3; ++j) bs[buf][tid + j * kPfThreads] = src[j];
+        for (int b = 0; b < 4; ++b) {
+            const u32x4 v = d[(wr * 4 + b) * 64 + lane];
+            ra[b] = u32x3{v.x, v.y, v.z};
+        }
+        const u32x4* src = d + kPfSlotA + (wc * 4) * 192 + lane;
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) rb[q][c] = src[c * 192 + q * 64];
     };
 
     f32x4 acc[4][4];
@@ -217,60 +277,59 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[b][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    u32x3 ring[kPfDepth + 1][4];
+    // prologue: steps 0-3 into slots 0-3, all landed; step 0's fragments read
 #pragma unroll
-    for (int u = 0; u <= kPfDepth; ++u) issue_a(ring[u], u);
-    // B parts: loaded three steps ahead into a ring of three register sets
-    // (the set of step s + 3 is the one step s's parts left, stored to LDS at
-    // the end of step s - 1), stored to LDS one step ahead (double buffer), so
-    // a store waits for a load issued two steps earlier while the later loads
-    // stay in flight
-    // The loop runs the steps in whole rounds of the unroll: steps past
-    // nsteps read zeros (A and B), add nothing, and keep the loop body free of
-    // branches around loads.
-    u32x4 breg[3][3];
-    load_b(breg[0], 0);
-    load_b(breg[1], 1);
-    load_b(breg[2], 2);
-    store_b(breg[0], 0);
-    __syncthreads();
+    for (int i = 0; i < kPfRing; ++i) load_step(i, i);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    u32x3 fa[2][4];
+    u32x4 fb[2][3][4];
+    read_frags(fa[0], fb[0], 0);
 
-    const int nround = (nsteps + kPfDepth) / (kPfDepth + 1) * (kPfDepth + 1);
-    for (int s0 = 0; s0 < nround; s0 += kPfDepth + 1) {
+    // Step s, software-pipelined: wait for this wave's loads of step s + 1
+    // and for its fragment reads of step s; barrier (every wave's loads of
+    // step s + 1 have landed, and every wave is done reading slot s % 4);
+    // step s + 4 into that slot; the fragments of step s + 1 read while the
+    // A groups of step s are unpacked and its 48 MFMAs run.  The loop runs
+    // whole rounds of the unroll: steps past nsteps read zeros (A and B) and
+    // add nothing.
+    const int nround = (nsteps + kPfRing - 1) / kPfRing * kPfRing;
+    for (int s0 = 0; s0 < nround; s0 += kPfRing) {
 #pragma unroll
-        for (int u = 0; u <= kPfDepth; ++u) {
+        for (int u = 0; u < kPfRing; ++u) {
             const int s = s0 + u;
-            {
-                load_b(breg[u % 3], s + 3);  // u % 3 == s % 3: step s's set, already in LDS
-                // this wave's B fragments: 4 token blocks x 3 parts
-                u32x4 bf[4][3];
-                const u32x4* src = bs[s & 1] + (wc * 4) * 192 + lane;
+            // (the empty asm statements keep every LDS access on its side of
+            // the wait and the barrier: neither builtin orders memory)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(kPfWait));
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            load_step(u, s + kPfRing);
+            read_frags(fa[(u + 1) & 1], fb[(u + 1) & 1], (u + 1) % kPfRing);
+            // the reads are issued here, ahead of the MFMAs they overlap
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            u32x4 a[4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-#pragma unroll
-                    for (int q = 0; q < 3; ++q) bf[c][q] = src[c * 192 + q * 64];
-                u32x4 a[4];
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    uint32_t pr[4];
-                    unpack_pairs(ring[u][b].x, ring[u][b].y, ring[u][b].z, pr);
-                    a[b] = u32x4{pr[0], pr[1], pr[2], pr[3]};
-                }
-                issue_a(ring[u], s + kPfDepth + 1);
-                // every fragment read is issued before the first MFMA, so the
-                // LDS latency is paid once per step, not between MFMAs
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int q = 0; q < 3; ++q)
-#pragma unroll
-                    for (int b = 0; b < 4; ++b)
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) acc[b][c] = mfma(a[b], bf[c][q], acc[b][c]);
-                store_b(breg[(u + 1) % 3], (s + 1) & 1);  // past the end: zeros nobody reads
-                __syncthreads();
+            for (int b = 0; b < 4; ++b) {
+                uint32_t pr[4];
+                unpack_pairs(fa[u & 1][b].x, fa[u & 1][b].y, fa[u & 1][b].z, pr);
+                a[b] = u32x4{pr[0], pr[1], pr[2], pr[3]};
             }
+#pragma unroll
+            for (int q = 0; q < 3; ++q)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[b][c] = mfma(a[b], fb[u & 1][q][c], acc[b][c]);
         }
     }
+    // the last loads (zeros into slots nobody reads) land before the
+    // workgroup's LDS can be handed on
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 
     // epilogue: lane l holds token 16 c + l%16 and rows 4(l/16) + 0..3 of each tile
     const int q = lane >> 4, jj = lane & 15;
@@ -291,42 +350,62 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
         }
     }
     // (b) the exceptions of the wave's 64 rows (the tiles hold zeros there), in
-    // list order, 8 entries at a time: x' of the lane's 4 tokens at each
-    // entry's column gathered from x (fp32), the product added to the output
-    // that holds the entry's row
+    // list order, 8 entries at a time, the next batch's metadata and x'
+    // gathers issued before the current one is added: each entry's row,
+    // column and value are wave-uniform (scalar loads), x' of the lane's 4
+    // tokens at its column comes from the transposed copy (the wave's 64
+    // tokens of one column: 256 contiguous bytes), and a switch on the row's
+    // (row block, row) slot adds the product to that output only, in the
+    // lanes of the row's quarter
     const int64_t rlo = blk0 * 16;
     if (rlo < N) {
         const int32_t e_lo = rp[rlo], e_hi = rp[min(rlo + 64, (int64_t)N)];
-        for (int32_t e0 = e_lo; e0 < e_hi; e0 += 8) {
-            int rr[8];
-            float evv[8], xv[8][4];
+        constexpr int EB = 8;
+        const float* xtw = xt + (int64_t)(tb0 + wc * 4) * 16 + jj;  // token block c at + 16 c
+        int nr[EB];
+        float nv[EB], ng[EB][4];
+        auto fetch = [&](int32_t e0) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < EB; ++j) {
                 const int32_t e = min(e0 + j, e_hi - 1);
-                rr[j] = (int)(er[e] - rlo);
-                evv[j] = e0 + j < e_hi ? ev[e] : 0.0f;
-                const int col = ec[e];
-                float wl = 1.0f;
-                if constexpr (LN) wl = __uint_as_float((uint32_t)lnw[col] << 16);
+                nr[j] = (int)(er[e] - rlo);
+                nv[j] = ev[e];
+                const float* xc = xtw + (int64_t)ec[e] * tp;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const float* xr = x + (int64_t)min(tok[c], T - 1) * xs;
-                    const float g = xr[col];
-                    if constexpr (M2) xv[j][c] = silu_mul(g, xr[K + col]);
-                    else xv[j][c] = LN ? g * wl : g;
-                }
+                for (int c = 0; c < 4; ++c) ng[j][c] = xc[c * 16];
             }
+        };
+        fetch(e_lo);
+        for (int32_t e0 = e_lo; e0 < e_hi; e0 += EB) {
+            int rr[EB];
+            float evv[EB], xv[EB][4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int eb = rr[j] >> 4, eq = (rr[j] & 15) >> 2, ei = rr[j] & 3;
+            for (int j = 0; j < EB; ++j) {
+                rr[j] = nr[j];
+                evv[j] = nv[j];
 #pragma unroll
-                for (int b = 0; b < 4; ++b)
+                for (int c = 0; c < 4; ++c) xv[j][c] = ng[j][c];
+            }
+            if (e0 + EB < e_hi) fetch(e0 + EB);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const bool hit = b == eb && i == ei && q == eq;
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) v[b][c][i] += hit ? evv[j] * xv[j][c] : 0.0f;
-                    }
+            for (int j = 0; j < EB; ++j) {
+                if (e0 + j >= e_hi) break;
+                const int r = rr[j];
+                const bool mine = q == ((r & 15) >> 2);
+#define RV12_EXC_CASE(B, I)                                                                 \
+    case (B) * 4 + (I):                                                                     \
+        if (mine) {                                                                         \
+            _Pragma("unroll") for (int c = 0; c < 4; ++c) v[B][c][I] += evv[j] * xv[j][c]; \
+        }                                                                                   \
+        break;
+                switch (((r >> 4) << 2) | (r & 3)) {
+                    RV12_EXC_CASE(0, 0) RV12_EXC_CASE(0, 1) RV12_EXC_CASE(0, 2) RV12_EXC_CASE(0, 3)
+                    RV12_EXC_CASE(1, 0) RV12_EXC_CASE(1, 1) RV12_EXC_CASE(1, 2) RV12_EXC_CASE(1, 3)
+                    RV12_EXC_CASE(2, 0) RV12_EXC_CASE(2, 1) RV12_EXC_CASE(2, 2) RV12_EXC_CASE(2, 3)
+                    RV12_EXC_CASE(3, 0) RV12_EXC_CASE(3, 1) RV12_EXC_CASE(3, 2) RV12_EXC_CASE(3, 3)
+                    default: break;
+                }
+#undef RV12_EXC_CASE
             }
         }
     }
@@ -359,7 +438,7 @@ int prefill_tokens_padded(int T) { return (T + kPfTokBlocks * 16 - 1) / (kPfTokB
 
 size_t prefill_ws_bytes(int K, int T) {
     const size_t tp = (size_t)prefill_tokens_padded(T);
-    return tp * (size_t)K * 6 + tp * 8;
+    return tp * (size_t)K * 10 + tp * 8;  // parts, P and R, transposed x'
 }
 
 void launch_prefill(const rv12_matrix& w, const float* x, float* y, int T, int mode, const uint16_t* lnw, float eps,
@@ -369,14 +448,20 @@ void launch_prefill(const rv12_matrix& w, const float* x, float* y, int T, int m
     u32x4* xb = reinterpret_cast<u32x4*>(ws);
     int* P = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + (size_t)tp * K * 6);
     float* R = reinterpret_cast<float*>(P + tp);
+    float* xt = R + tp;
     const int xs = mode == 2 ? 2 * K : K;
-    hipLaunchKernelGGL(k_prefill_x, dim3(tp / 16), dim3(kPxThreads), 0, st, x, T, K, xs, mode == 2 ? 1 : 0, lnw, eps, xb, P,
-                       R);
+    const int m2 = mode == 2 ? 1 : 0;
+    hipLaunchKernelGGL(k_prefill_stats, dim3(tp / (kPsThreads / 64)), dim3(kPsThreads), 0, st, x, T, K, xs, m2, lnw, eps,
+                       P, R);
+    hipLaunchKernelGGL(k_prefill_parts, dim3(tp / 32, (K + 63) / 64), dim3(kPpThreads), 0, st, x, T, K, xs, m2, lnw, P,
+                       xb, xt, tp);
     const int64_t nblk = ((int64_t)N + 15) / 16;
-    const dim3 grid((unsigned)((nblk + kPfRowBlocks - 1) / kPfRowBlocks), (unsigned)(tp / (kPfTokBlocks * 16)));
-    const auto kern = mode == 2 ? k_prefill_mm<true, false> : (lnw ? k_prefill_mm<false, true> : k_prefill_mm<false, false>);
-    hipLaunchKernelGGL(kern, grid, dim3(kPfThreads), 0, st, reinterpret_cast<const uint32_t*>(w.tiles), w.rbase, xb,
-                       P, w.rp, w.er, w.ec, w.ev, x, lnw, R, y, N, K, T, xs, mode == 2 ? 1 : 0, mode != 0 ? 1 : 0);
+    const dim3 grid((unsigned)((nblk + kPfRowBlocks - 1) / kPfRowBlocks * (tp / (kPfTokBlocks * 16))));
+    const auto kern = lnw ? k_prefill_mm<true> : k_prefill_mm<false>;
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kPfLds);
+    hipLaunchKernelGGL(kern, grid, dim3(kPfThreads), kPfLds, st, reinterpret_cast<const uint32_t*>(w.tiles), w.rbase, xb,
+                       P, w.rp, w.er, w.ec, w.ev, xt, tp, R, y, N, K, T, mode != 0 ? 1 : 0);
 }
 
 }  // namespace rv12

@@ -215,8 +215,9 @@ int rv12_gemm_static(const rv12_matrix* w, const float* x, float* y, int t, cons
  * x' is split per token into three bf16 parts (24 significand bits, after an
  * exact power-of-two scale), every weight is read once in its 12-bit form,
  * products and sums are fp32, the exceptions are added in list order.  ws:
- * rv12_prefill_workspace_bytes(k, t) bytes (6 bytes per column and padded
- * token, the parts, and 8 per padded token), 16-byte aligned.  Replaces the
+ * rv12_prefill_workspace_bytes(k, t) bytes (10 bytes per column and padded
+ * token: the parts and a transposed fp32 copy of x' for the exception
+ * entries; and 8 per padded token), 16-byte aligned.  Replaces the
  * blocked prefill's rmsg_k + matrix() (decode_rows + the fp32 GEMM mm_k),
  * ramvi/engine/ramvi_engine/kernels/prefill.py:66-78, 94-99,
  * ramvi/engine/ramvi_engine/kernels/prefill_kernels.py:8-26, 58-110. */

@@ -27,7 +27,7 @@ def test_prefill_workspace_bytes():
     arguments."""
     from ai_amd import _lib
     L = _lib.lib()
-    assert L.rv12_prefill_workspace_bytes(4096, 2048) == 2048 * 4096 * 6 + 2048 * 8
-    assert L.rv12_prefill_workspace_bytes(1024, 300) == 384 * 1024 * 6 + 384 * 8
+    assert L.rv12_prefill_workspace_bytes(4096, 2048) == 2048 * 4096 * 10 + 2048 * 8
+    assert L.rv12_prefill_workspace_bytes(1024, 300) == 384 * 1024 * 10 + 384 * 8
     assert L.rv12_prefill_workspace_bytes(1000, 5) == 0 and L.rv12_prefill_workspace_bytes(1024, 0) == 0
     assert L.rv12_prefill_workspace_bytes(1024, (1 << 16) + 1) == 0
