@@ -27,8 +27,8 @@ EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_pack_p
            "rv12_gemv", "rv12_gemm", "rv12_gemm_static", "rv12_decode_rows", "rv12_attn_workspace_bytes", "rv12_rope_attn",
            "rv12_attn_batch_workspace_bytes", "rv12_rope_attn_batch", "rv12_prefill_attn_workspace_bytes",
            "rv12_prefill_rope_attn", "rv12_prefill_workspace_bytes",
-           "rv12_prefill_linear")
-ABI_VERSION = 6
+           "rv12_prefill_linear", "rv12_decode_advance")
+ABI_VERSION = 7
 STATIC_SCRATCH_BYTES = 8 << 20  # RV12_STATIC_SCRATCH_BYTES
 
 
@@ -123,6 +123,8 @@ def lib():
         L.rv12_prefill_workspace_bytes.argtypes = [I, I]
         L.rv12_prefill_linear.restype = I
         L.rv12_prefill_linear.argtypes = [ctypes.POINTER(Matrix), P, P, I, P, F, I, P, SZ, P]
+        L.rv12_decode_advance.restype = I
+        L.rv12_decode_advance.argtypes = [P, P, ctypes.c_int64, I, P, P, ctypes.c_int64, P, P, P, P]
         L.rv12_attn_batch_workspace_bytes.restype = SZ
         L.rv12_attn_batch_workspace_bytes.argtypes = [ctypes.POINTER(Attn), I]
         L.rv12_rope_attn_batch.restype = I

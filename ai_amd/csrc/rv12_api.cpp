@@ -448,6 +448,17 @@ size_t rv12_head_workspace_bytes(int n, int k, int t, const rv12_launch* cfg) {
     return head_ws(n, t, c).total;
 }
 
+int rv12_decode_advance(const int64_t* ids, const uint16_t* emb, int64_t vocab, int hidden, float* x, int64_t* out,
+                        int64_t out_len, int64_t* steps, int64_t* pos, int64_t* tok, void* stream) {
+    if (!ids || !emb || !x || !out || !steps || !pos) return RV12_E_NULL;
+    if (vocab < 1 || hidden < 1 || out_len < 0) return RV12_E_SHAPE;
+    if (((uintptr_t)ids | (uintptr_t)out | (uintptr_t)steps | (uintptr_t)pos | (uintptr_t)tok) & 7u ||
+        ((uintptr_t)x & 3u) || ((uintptr_t)emb & 1u))
+        return RV12_E_ALIGN;
+    launch_decode_advance(ids, emb, vocab, hidden, x, out, out_len, steps, pos, tok, (hipStream_t)stream);
+    return launch_status();
+}
+
 int rv12_head_argmax(const rv12_matrix* w, const float* x, int t, const uint16_t* lnw, float eps, float* logits,
                      int64_t* ids, const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream) {
     int rc = check_matrix(w);

@@ -516,6 +516,35 @@ void launch_pick(const float* v, const int32_t* ix, int64_t n, int64_t stride, i
     hipLaunchKernelGGL(k_pick, dim3(1, T), dim3(kPickThreads), 0, st, tv, ti, nc, nc, nc, nullptr, nullptr, ids);
 }
 
+// the decode step's bookkeeping after its greedy pick: id = ids[0] is recorded
+// in out[*steps] (when steps lies in [0, out_len)), becomes the next input
+// token (tok, when given) and its embedding row (bf16, converted exactly) the
+// next step's activations x; *steps and *pos advance by one.  The id used for
+// the row is clamped into [0, vocab).
+__global__ __launch_bounds__(256) void k_decode_advance(const int64_t* __restrict__ ids,
+                                                        const uint16_t* __restrict__ emb, int64_t vocab, int hidden,
+                                                        float* __restrict__ x, int64_t* __restrict__ out,
+                                                        int64_t out_len, int64_t* __restrict__ steps,
+                                                        int64_t* __restrict__ pos, int64_t* __restrict__ tok) {
+    const int64_t id = ids[0];
+    const uint16_t* row = emb + min(max(id, (int64_t)0), vocab - 1) * (int64_t)hidden;
+    for (int k = threadIdx.x; k < hidden; k += blockDim.x) x[k] = __uint_as_float((uint32_t)row[k] << 16);
+    if (threadIdx.x == 0) {
+        const int64_t s = *steps;
+        if (s >= 0 && s < out_len) out[s] = id;
+        *steps = s + 1;
+        *pos += 1;
+        if (tok) *tok = id;
+    }
+}
+
+void launch_decode_advance(const int64_t* ids, const uint16_t* emb, int64_t vocab, int hidden, float* x,
+                           int64_t* out, int64_t out_len, int64_t* steps, int64_t* pos, int64_t* tok,
+                           hipStream_t st) {
+    hipLaunchKernelGGL(k_decode_advance, dim3(1), dim3(256), 0, st, ids, emb, vocab, hidden, x, out, out_len, steps,
+                       pos, tok);
+}
+
 // ------------------------------------------------------------------ launch
 template <int T, int RB, bool M2, bool LN>
 static void launch_t(const LinearParams& p, dim3 grid, int threads, size_t lds, hipStream_t st) {

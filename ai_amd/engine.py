@@ -19,9 +19,11 @@ ramvi/engine/ramvi_engine/generation/head.py:29-88), followed by argmax, the
 smallest id on ties (head.py:76-79).
 
 A decode step is one HIP graph (the reference captures one per batch bucket,
-engine.py:432-444): the embedding row of the current token, all layers, the
-head, argmax, and the bookkeeping (next token becomes the input, position and
-output counter advance) run on the device, so the host only replays the graph.
+engine.py:432-444): all layers on the embedding row of the current token,
+the head with its fused pick, and one small library kernel
+(rv12_decode_advance) for the bookkeeping (the id recorded, the next token's
+embedding row written, position and output counter advanced) run on the
+device, so the host only replays the graph.
 The step's attention (head norms, RoPE, KV write, grouped-query attention)
 is one HIP kernel per layer (ai_amd.attn); passes of 2..16 tokens use the
 batch kernels of the same library, the blocked prefill its prompt kernels.
@@ -43,6 +45,7 @@ import os
 
 import torch
 
+from . import _lib
 from . import prefill as blocked_prefill
 from . import wcomp
 from .attn import RopeAttn
@@ -186,14 +189,18 @@ class Engine:
         self.xb[:T].copy_(self.emb.index_select(0, self.tok[:T]).float())
 
     def _step(self):
-        """One decode step, all on the device (graph body)."""
-        self._embed(1)
+        """One decode step, all on the device (graph body): the layers on the
+        activations xb[0] (the embedding row of the current token), the greedy
+        pick, then rv12_decode_advance records the id in out[steps], makes it
+        the next token, writes its embedding row into xb[0] and advances pos
+        and steps (one kernel in place of torch's lookup, conversion, index
+        copy and counter additions)."""
         self._layers(self.xb[:1], 1)
         self._head_row(self.xb[:1])
-        self.out.index_copy_(0, self.steps, self.nxt[:1])
-        self.tok[:1].copy_(self.nxt[:1])
-        self.pos.add_(1)
-        self.steps.add_(1)
+        _lib.check(_lib.lib().rv12_decode_advance(
+            wcomp._ptr(self.nxt), wcomp._ptr(self.emb), self.emb.shape[0], self.emb.shape[1], wcomp._ptr(self.xb),
+            wcomp._ptr(self.out), self.out.numel(), wcomp._ptr(self.steps), wcomp._ptr(self.pos),
+            wcomp._ptr(self.tok), wcomp._stream(self.xb.device)), "rv12_decode_advance")
 
     def reset(self):
         for c in self.Kc + self.Vc:
@@ -336,6 +343,7 @@ class Engine:
         first = self.prefill(prompt)
         self.out[:1].copy_(first)
         self.tok[:1].copy_(first)
+        self._embed(1)  # the first step's activations; each step writes the next one's
         self.steps.fill_(1)
         e[1].record()
         for _ in range(max_new - 1):

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define RV12_ABI_VERSION 6
+#define RV12_ABI_VERSION 7
 
 enum rv12_status {
     RV12_OK = 0,
@@ -188,6 +188,20 @@ int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint1
  * :76-79) and vocab_a_k, ramvi/engine/ramvi_engine/kernels/vocab8.py:19-44. */
 int rv12_head_argmax(const rv12_matrix* w, const float* x, int t, const uint16_t* lnw, float eps, float* logits,
                      int64_t* ids, const rv12_launch* cfg, void* ws, size_t ws_bytes, void* stream);
+
+/* The decode step's bookkeeping after its greedy pick, on the device (one
+ * small kernel, no host synchronisation, graph-capturable): id = ids[0] is
+ * recorded in out[*steps] (only when 0 <= *steps < out_len), becomes the next
+ * input token (*tok, tok may be NULL), and its embedding row
+ * emb[id][0:hidden) (bf16, id clamped into [0, vocab)) is written to x as
+ * float32, the next step's activations; *steps and *pos are incremented.
+ * ids, out, steps, pos, tok: 8-byte aligned; x 4-byte; emb 2-byte.  Replaces
+ * the step's embedding lookup and the bookkeeping after the pick (the next
+ * token becomes the input, position and step counters advance) that the
+ * reference's decode graph does with torch operations,
+ * ramvi/engine/ramvi_engine/core/engine.py:432-444. */
+int rv12_decode_advance(const int64_t* ids, const uint16_t* emb, int64_t vocab, int hidden, float* x, int64_t* out,
+                        int64_t out_len, int64_t* steps, int64_t* pos, int64_t* tok, void* stream);
 
 /* Workspace bytes of rv12_head_argmax for (n, k, t, cfg) (never 0 for valid
  * arguments; 0 where rv12_head_argmax would reject them). */

@@ -31,7 +31,7 @@ def test_library_exports_every_symbol():
 def test_abi_version_and_strerror():
     from ai_amd import _lib
     L = _lib.lib()
-    assert L.rv12_abi_version() == 6
+    assert L.rv12_abi_version() == 7
     for s in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -20):
         assert _lib.strerror(s) and _lib.strerror(s) != "unknown rv12 status"
     assert _lib.strerror(-99) == "unknown rv12 status"
@@ -335,3 +335,25 @@ def test_build_manifest_checked_at_load(monkeypatch):
     monkeypatch.undo()
     monkeypatch.setattr(build, "CODEGEN", build.CODEGEN[:-4])
     assert "other flags" in build.manifest_problem()
+
+
+def test_decode_advance_argument_errors():
+    """The decode step's bookkeeping entry reports NULL pointers, empty shapes
+    and misaligned pointers as statuses before any device work (tok alone
+    may be NULL)."""
+    from ai_amd import _lib
+    L = _lib.lib()
+
+    def call(vocab=151936, hidden=4096, out_len=64, odd=(), **null):
+        names = ("ids", "emb", "x", "out", "steps", "pos", "tok")
+        a = {k: (None if k in null else ctypes.c_void_p(0x1000 + (2 if k in odd else 0))) for k in names}
+        return L.rv12_decode_advance(a["ids"], a["emb"], vocab, hidden, a["x"], a["out"], out_len, a["steps"],
+                                     a["pos"], a["tok"], None)
+
+    for k in ("ids", "emb", "x", "out", "steps", "pos"):
+        assert call(**{k: None}) == _lib.RV12_E_NULL, k
+    assert call(vocab=0) == _lib.RV12_E_SHAPE
+    assert call(hidden=0) == _lib.RV12_E_SHAPE
+    assert call(out_len=-1) == _lib.RV12_E_SHAPE
+    for k in ("ids", "out", "steps", "pos", "tok", "x"):
+        assert call(odd=(k,)) == _lib.RV12_E_ALIGN, k
