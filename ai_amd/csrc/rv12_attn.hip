@@ -622,6 +622,8 @@ static void launch_batch_t(const AttnParams& p, int S, hipStream_t st) {
                        dim3(kAttnThreads), lds, st, p);
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));  // four bf16 MFMA operand bits
+
 // ---------------------------------------------------------------------------
 // Prompt attention (the blocked prefill's att_k,
 // ramvi/engine/ramvi_engine/kernels/prefill_kernels.py:29-54): token r of a
@@ -691,6 +693,15 @@ __global__ __launch_bounds__(512) void k_prefill_attn(AttnParams p) {
             }
         }
     }
+    // bf16 caches: the keys and values are exact bf16, so the products run on
+    // the bf16 matrix cores with q and the probabilities split into three bf16
+    // parts (hi + mid + lo = the float32 value to 24 bits; every product of
+    // bf16 values is exact in float32): q's parts once per tile here
+    u32x4 qp[BF16 ? NA : 1][3];
+    if constexpr (BF16) {
+#pragma unroll
+        for (int a = 0; a < NA; ++a) split3(qv[a], qp[a][0], qp[a][1], qp[a][2]);
+    }
     const int last = min((int)p0 + t0 + 15, n - 1);  // last position any token of the tile sees
     const int nkb = last / 16 + 1;
 
@@ -747,10 +758,22 @@ __global__ __launch_bounds__(512) void k_prefill_attn(AttnParams p) {
         if (kb + 1 < nkb) load_block(kb + 1);
         // scores of positions kb 16 + 4 q4 + r for token tq
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (BF16) {
+            // v_mfma_f32_16x16x32_bf16: A = the lane's 8 key dims 32a + 8 q4 ..
+            // of position c16, B = the same dims of its token's q part
 #pragma unroll
-        for (int a = 0; a < NA; ++a)
+            for (int a = 0; a < NA; ++a) {
+                const u32x4 ka = {kcur[a][0], kcur[a][1], kcur[a][2], kcur[a][3]};
 #pragma unroll
-            for (int b = 0; b < 8; ++b) s = __builtin_amdgcn_mfma_f32_16x16x4f32(word_f(kcur[a], b), qv[a][b], s, 0, 0, 0);
+                for (int c = 0; c < 3; ++c) s = mfma(ka, qp[a][c], s);
+            }
+        } else {
+#pragma unroll
+            for (int a = 0; a < NA; ++a)
+#pragma unroll
+                for (int b = 0; b < 8; ++b)
+                    s = __builtin_amdgcn_mfma_f32_16x16x4f32(word_f(kcur[a], b), qv[a][b], s, 0, 0, 0);
+        }
         float sc[4], pr[4];
         float mb = -INFINITY;
 #pragma unroll
@@ -771,11 +794,41 @@ __global__ __launch_bounds__(512) void k_prefill_attn(AttnParams p) {
         }
         l = l * alpha + ls;
         m = mn;
+        if constexpr (BF16) {
+            // v_mfma_f32_16x16x16_bf16 per output dim tile: A = dim DT c16 + d
+            // of positions 4 q4 + 0..3 (from the lane's four value rows), B =
+            // the lane's own probabilities of those positions, per part
+            uint32_t ph[4], pm[4], pl[4];
 #pragma unroll
-        for (int d = 0; d < DT; ++d) {
-            o[d] *= alpha;
+            for (int j = 0; j < 4; ++j) {
+                ph[j] = bf16_bits(pr[j]);
+                const float r1 = pr[j] - bf16_value(ph[j]);
+                pm[j] = bf16_bits(r1);
+                pl[j] = bf16_bits(r1 - bf16_value(pm[j]));
+            }
+            const s16x4 pb[3] = {__builtin_bit_cast(s16x4, uint2{ph[0] | ph[1] << 16, ph[2] | ph[3] << 16}),
+                                 __builtin_bit_cast(s16x4, uint2{pm[0] | pm[1] << 16, pm[2] | pm[3] << 16}),
+                                 __builtin_bit_cast(s16x4, uint2{pl[0] | pl[1] << 16, pl[2] | pl[3] << 16})};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(word_f(vcur[j], d), pr[j], o[d], 0, 0, 0);
+            for (int d = 0; d < DT; ++d) {
+                o[d] *= alpha;
+                const int w = d >> 1;
+                const uint32_t a01 = (d & 1) ? (vcur[0][w] >> 16) | (vcur[1][w] & 0xFFFF0000u)
+                                             : (vcur[0][w] & 0xFFFFu) | (vcur[1][w] << 16);
+                const uint32_t a23 = (d & 1) ? (vcur[2][w] >> 16) | (vcur[3][w] & 0xFFFF0000u)
+                                             : (vcur[2][w] & 0xFFFFu) | (vcur[3][w] << 16);
+                const s16x4 va = __builtin_bit_cast(s16x4, uint2{a01, a23});
+#pragma unroll
+                for (int c = 0; c < 3; ++c) o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb[c], o[d], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+                o[d] *= alpha;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(word_f(vcur[j], d), pr[j], o[d], 0, 0, 0);
+            }
         }
     }
     l += __shfl_xor(l, 16);
