@@ -44,8 +44,13 @@ def _check(cnp, T, seed, add, mode=None, scales=None, rms=False):
         prefill.matrix(torch.from_numpy(X).cuda(), c, y, add=add, lnw=ln)
     torch.cuda.synchronize()
     got = y.cpu().numpy().astype(np.float64)
+    # outputs beyond the float32 range: the closed form rounded to float32
+    # (inf), as an fp32 evaluation must produce
+    with np.errstate(over="ignore"):
+        ref = ref.astype(np.float32).astype(np.float64)
     fin = np.isfinite(ref)
     assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(got[np.isinf(ref)], ref[np.isinf(ref)])
     err = np.abs(got[fin] - ref[fin])
     assert np.all(err <= 1e-3 + 1e-2 * np.abs(ref[fin])), float(err.max())
     # plus the rounding of the final add into y (2^-23 |y|) where y is accumulated
@@ -165,3 +170,36 @@ def test_qwen3_8b_gu_2048_tokens_against_the_decode_kernels():
     assert np.all(err <= 4 * (K + 8) * 2.0 ** -24 * mag + 1e-30), float(err.max())
     del c, w, x, y
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("K", [160, 224, 288])
+def test_step_counts_off_the_ring(K):
+    """K / 32 steps that are not a multiple of the kernel's four-slot load
+    ring (5, 7, 9 steps): the padded steps of the last round load zeros
+    through the 0-byte descriptors and add nothing; every mode, with and
+    without the RMS prologue, exceptions in many rows."""
+    rng = np.random.default_rng(K)
+    w = (rng.standard_normal((300, K)) * 0.02).astype(np.float32)
+    w[rng.choice(300, 3)] *= 20
+    w.reshape(-1)[rng.choice(w.size, 60, replace=False)] = 1e-30
+    cnp = codec.compress(codec.f32_to_bf16_rne(w), CH=32)
+    assert cnp["er"].size > 30
+    for T in (17, 130):
+        for mode in (0, 1, 2):
+            print("K", K, "T", T, "mode", mode, flush=True)
+            _check(cnp, T, K + T + mode, mode != 0, mode=mode)
+        _check(cnp, T, K + T + 7, False, mode=0, rms=True)
+
+
+@pytest.mark.parametrize("case", ["special_values", "all_zero"])
+def test_matrix_on_golden_special_values(golden, case):
+    """Golden matrices with infinities, NaNs, subnormals and zeros among the
+    weights: NaN and infinite outputs where the closed form (rounded to
+    float32) has them, every finite output within the tolerance.  (The
+    golden matrices of weights near the top of the float32 range, huge_with_inf
+    and window_hits_inf, are decode vectors only: a sum of their products
+    overflows float32 part-way in an order-dependent way, so an infinite
+    weight meets an overflowed partial sum of either sign.)"""
+    cnp = ref_dict(golden[case])
+    for add in (False, True):
+        _check(cnp, 40, 3, add)
