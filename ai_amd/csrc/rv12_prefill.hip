@@ -261,10 +261,7 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     auto read_frags = [&](u32x3 (&ra)[4], u32x4 (&rb)[3][4], int slot) {
         const u32x4* d = bs + slot * kPfSlot;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const u32x4 v = d[(wr * 4 + b) * 64 + lane];
-            ra[b] = u32x3{v.x, v.y, v.z};
-        }
+        for (int b = 0; b < 4; ++b) ra[b] = *reinterpret_cast<const u32x3*>(d + (wr * 4 + b) * 64 + lane);
         const u32x4* src = d + kPfSlotA + (wc * 4) * 192 + lane;
 #pragma unroll
         for (int q = 0; q < 3; ++q)
