@@ -45,6 +45,13 @@ namespace rv12 {
 constexpr int kPfRowBlocks = 16;  // row blocks (of 16 rows) per workgroup
 constexpr int kPfTokBlocks = 8;   // token blocks (of 16 tokens) per workgroup
 constexpr int kPfThreads = 512;
+// wave tile: kPfWB row blocks x kPfWT token blocks (8 waves: 16 / kPfWB along
+// the rows times 8 / kPfWT along the tokens)
+#define RV12_PF_WB 4
+constexpr int kPfWB = RV12_PF_WB;
+constexpr int kPfWR = kPfRowBlocks / kPfWB;                          // waves along the rows
+constexpr int kPfWT = kPfTokBlocks / (kPfThreads / 64 / kPfWR);  // token blocks per wave
+static_assert(kPfWR * (kPfTokBlocks / kPfWT) == kPfThreads / 64, "8 waves cover the workgroup tile");
 constexpr int kPfRing = 4;  // LDS slots: the A tiles and B parts of steps s .. s + 3
 // slot layout (u32x4 units): 16 A tiles of 1 KB (a 12-byte-per-lane load with
 // the LDS destination writes lane l at 16 l: 768 B of each KB), then the B
@@ -204,13 +211,13 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     extern __shared__ u32x4 bs[];  // [kPfRing][kPfSlot]: A tiles and B parts of steps s .. s + 3
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wr = wave & 3, wc = wave >> 2;
+    const int wr = wave % kPfWR, wc = wave / kPfWR;
     const int nsteps = K >> 5;
     const int64_t nblk = (N + 15) / 16;
     const int nx = (int)((nblk + kPfRowBlocks - 1) / kPfRowBlocks);
     int rt, tt;
     prefill_tile(blockIdx.x, gridDim.x, nx, gridDim.x / nx, rt, tt);
-    const int64_t blk0 = (int64_t)rt * kPfRowBlocks + wr * 4;  // this wave's first row block
+    const int64_t blk0 = (int64_t)rt * kPfRowBlocks + wr * kPfWB;  // this wave's first row block
     const int tb0 = tt * kPfTokBlocks;                          // the workgroup's first token block
     const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
     typedef __attribute__((address_space(3))) void* lds_ptr;
@@ -258,22 +265,22 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     // this wave's fragments of the step in slot `slot`: its 4 row blocks' A
     // groups (12 bytes per lane) and 3 parts x 4 token blocks of B,
     // part-major so the first part's MFMAs wait only for its own reads
-    auto read_frags = [&](u32x3 (&ra)[4], u32x4 (&rb)[3][4], int slot) {
+    auto read_frags = [&](u32x3 (&ra)[kPfWB], u32x4 (&rb)[3][kPfWT], int slot) {
         const u32x4* d = bs + slot * kPfSlot;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) ra[b] = *reinterpret_cast<const u32x3*>(d + (wr * 4 + b) * 64 + lane);
-        const u32x4* src = d + kPfSlotA + (wc * 4) * 192 + lane;
+        for (int b = 0; b < kPfWB; ++b) ra[b] = *reinterpret_cast<const u32x3*>(d + (wr * kPfWB + b) * 64 + lane);
+        const u32x4* src = d + kPfSlotA + (wc * kPfWT) * 192 + lane;
 #pragma unroll
         for (int q = 0; q < 3; ++q)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) rb[q][c] = src[c * 192 + q * 64];
+            for (int c = 0; c < kPfWT; ++c) rb[q][c] = src[c * 192 + q * 64];
     };
 
-    f32x4 acc[4][4];
+    f32x4 acc[kPfWB][kPfWT];
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < kPfWB; ++b)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[b][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < kPfWT; ++c) acc[b][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     // prologue: steps 0-3 into slots 0-3, all landed; step 0's fragments read
 #pragma unroll
     for (int i = 0; i < kPfRing; ++i) load_step(i, i);
@@ -281,8 +288,8 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    u32x3 fa[2][4];
-    u32x4 fb[2][3][4];
+    u32x3 fa[2][kPfWB];
+    u32x4 fb[2][3][kPfWT];
     read_frags(fa[0], fb[0], 0);
 
     // Step s, software-pipelined: wait for this wave's loads of step s + 1
@@ -308,9 +315,9 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
             // the reads are issued here, ahead of the MFMAs they overlap
             asm volatile("" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
-            u32x4 a[4];
+            u32x4 a[kPfWB];
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
+            for (int b = 0; b < kPfWB; ++b) {
                 uint32_t pr[4];
                 unpack_pairs(fa[u & 1][b].x, fa[u & 1][b].y, fa[u & 1][b].z, pr);
                 a[b] = u32x4{pr[0], pr[1], pr[2], pr[3]};
@@ -318,9 +325,9 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
 #pragma unroll
             for (int q = 0; q < 3; ++q)
 #pragma unroll
-                for (int b = 0; b < 4; ++b)
+                for (int b = 0; b < kPfWB; ++b)
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) acc[b][c] = mfma(a[b], fb[u & 1][q][c], acc[b][c]);
+                    for (int c = 0; c < kPfWT; ++c) acc[b][c] = mfma(a[b], fb[u & 1][q][c], acc[b][c]);
         }
     }
     // the last loads (zeros into slots nobody reads) land before the
@@ -331,14 +338,14 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     // epilogue: lane l holds token 16 c + l%16 and rows 4(l/16) + 0..3 of each tile
     const int q = lane >> 4, jj = lane & 15;
     // (a) rescale: v = acc 2^(sc_row - P_t), exact
-    float v[4][4][4];
-    int tok[4];
+    float v[kPfWB][kPfWT][4];
+    int tok[kPfWT];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        tok[c] = (tb0 + wc * 4 + c) * 16 + jj;
+    for (int c = 0; c < kPfWT; ++c) {
+        tok[c] = (tb0 + wc * kPfWT + c) * 16 + jj;
         const int pt = tok[c] < T ? P[tok[c]] : 0;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
+        for (int b = 0; b < kPfWB; ++b) {
             const int64_t n = (blk0 + b) * 16 + q * 4;
             const float av[4] = {acc[b][c].x, acc[b][c].y, acc[b][c].z, acc[b][c].w};
 #pragma unroll
@@ -356,11 +363,11 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     // lanes of the row's quarter
     const int64_t rlo = blk0 * 16;
     if (rlo < N) {
-        const int32_t e_lo = rp[rlo], e_hi = rp[min(rlo + 64, (int64_t)N)];
+        const int32_t e_lo = rp[rlo], e_hi = rp[min(rlo + 16 * kPfWB, (int64_t)N)];
         constexpr int EB = 8;
-        const float* xtw = xt + (int64_t)(tb0 + wc * 4) * 16 + jj;  // token block c at + 16 c
+        const float* xtw = xt + (int64_t)(tb0 + wc * kPfWT) * 16 + jj;  // token block c at + 16 c
         int nr[EB];
-        float nv[EB], ng[EB][4];
+        float nv[EB], ng[EB][kPfWT];
         auto fetch = [&](int32_t e0) {
 #pragma unroll
             for (int j = 0; j < EB; ++j) {
@@ -369,19 +376,19 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
                 nv[j] = ev[e];
                 const float* xc = xtw + (int64_t)ec[e] * tp;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) ng[j][c] = xc[c * 16];
+                for (int c = 0; c < kPfWT; ++c) ng[j][c] = xc[c * 16];
             }
         };
         fetch(e_lo);
         for (int32_t e0 = e_lo; e0 < e_hi; e0 += EB) {
             int rr[EB];
-            float evv[EB], xv[EB][4];
+            float evv[EB], xv[EB][kPfWT];
 #pragma unroll
             for (int j = 0; j < EB; ++j) {
                 rr[j] = nr[j];
                 evv[j] = nv[j];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) xv[j][c] = ng[j][c];
+                for (int c = 0; c < kPfWT; ++c) xv[j][c] = ng[j][c];
             }
             if (e0 + EB < e_hi) fetch(e0 + EB);
 #pragma unroll
@@ -392,7 +399,7 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
 #define RV12_EXC_CASE(B, I)                                                                 \
     case (B) * 4 + (I):                                                                     \
         if (mine) {                                                                         \
-            _Pragma("unroll") for (int c = 0; c < 4; ++c) v[B][c][I] += evv[j] * xv[j][c]; \
+            _Pragma("unroll") for (int c = 0; c < kPfWT; ++c) v[B][c][I] += evv[j] * xv[j][c]; \
         }                                                                                   \
         break;
                 switch (((r >> 4) << 2) | (r & 3)) {
@@ -400,6 +407,12 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
                     RV12_EXC_CASE(1, 0) RV12_EXC_CASE(1, 1) RV12_EXC_CASE(1, 2) RV12_EXC_CASE(1, 3)
                     RV12_EXC_CASE(2, 0) RV12_EXC_CASE(2, 1) RV12_EXC_CASE(2, 2) RV12_EXC_CASE(2, 3)
                     RV12_EXC_CASE(3, 0) RV12_EXC_CASE(3, 1) RV12_EXC_CASE(3, 2) RV12_EXC_CASE(3, 3)
+#if RV12_PF_WB > 4
+                    RV12_EXC_CASE(4, 0) RV12_EXC_CASE(4, 1) RV12_EXC_CASE(4, 2) RV12_EXC_CASE(4, 3)
+                    RV12_EXC_CASE(5, 0) RV12_EXC_CASE(5, 1) RV12_EXC_CASE(5, 2) RV12_EXC_CASE(5, 3)
+                    RV12_EXC_CASE(6, 0) RV12_EXC_CASE(6, 1) RV12_EXC_CASE(6, 2) RV12_EXC_CASE(6, 3)
+                    RV12_EXC_CASE(7, 0) RV12_EXC_CASE(7, 1) RV12_EXC_CASE(7, 2) RV12_EXC_CASE(7, 3)
+#endif
                     default: break;
                 }
 #undef RV12_EXC_CASE
@@ -409,17 +422,17 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     // (c) with RMS the token's rs; store or add; rows past N and tokens past
     // T are skipped
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < kPfWT; ++c) {
         if (tok[c] >= T) continue;
         if constexpr (LN) {
             const float rs = R[tok[c]];
 #pragma unroll
-            for (int b = 0; b < 4; ++b)
+            for (int b = 0; b < kPfWB; ++b)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[b][c][i] *= rs;
         }
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
+        for (int b = 0; b < kPfWB; ++b) {
             const int64_t n = (blk0 + b) * 16 + q * 4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
