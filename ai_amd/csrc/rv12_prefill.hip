@@ -47,8 +47,7 @@ constexpr int kPfTokBlocks = 8;   // token blocks (of 16 tokens) per workgroup
 constexpr int kPfThreads = 512;
 // wave tile: kPfWB row blocks x kPfWT token blocks (8 waves: 16 / kPfWB along
 // the rows times 8 / kPfWT along the tokens)
-#define RV12_PF_WB 4
-constexpr int kPfWB = RV12_PF_WB;
+constexpr int kPfWB = 4;
 constexpr int kPfWR = kPfRowBlocks / kPfWB;                          // waves along the rows
 constexpr int kPfWT = kPfTokBlocks / (kPfThreads / 64 / kPfWR);  // token blocks per wave
 static_assert(kPfWR * (kPfTokBlocks / kPfWT) == kPfThreads / 64, "8 waves cover the workgroup tile");
@@ -402,17 +401,12 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
             _Pragma("unroll") for (int c = 0; c < kPfWT; ++c) v[B][c][I] += evv[j] * xv[j][c]; \
         }                                                                                   \
         break;
+                static_assert(kPfWB == 4, "one case per (row block, row) slot of the wave");
                 switch (((r >> 4) << 2) | (r & 3)) {
                     RV12_EXC_CASE(0, 0) RV12_EXC_CASE(0, 1) RV12_EXC_CASE(0, 2) RV12_EXC_CASE(0, 3)
                     RV12_EXC_CASE(1, 0) RV12_EXC_CASE(1, 1) RV12_EXC_CASE(1, 2) RV12_EXC_CASE(1, 3)
                     RV12_EXC_CASE(2, 0) RV12_EXC_CASE(2, 1) RV12_EXC_CASE(2, 2) RV12_EXC_CASE(2, 3)
                     RV12_EXC_CASE(3, 0) RV12_EXC_CASE(3, 1) RV12_EXC_CASE(3, 2) RV12_EXC_CASE(3, 3)
-#if RV12_PF_WB > 4
-                    RV12_EXC_CASE(4, 0) RV12_EXC_CASE(4, 1) RV12_EXC_CASE(4, 2) RV12_EXC_CASE(4, 3)
-                    RV12_EXC_CASE(5, 0) RV12_EXC_CASE(5, 1) RV12_EXC_CASE(5, 2) RV12_EXC_CASE(5, 3)
-                    RV12_EXC_CASE(6, 0) RV12_EXC_CASE(6, 1) RV12_EXC_CASE(6, 2) RV12_EXC_CASE(6, 3)
-                    RV12_EXC_CASE(7, 0) RV12_EXC_CASE(7, 1) RV12_EXC_CASE(7, 2) RV12_EXC_CASE(7, 3)
-#endif
                     default: break;
                 }
 #undef RV12_EXC_CASE
