@@ -124,6 +124,20 @@ def test_qwen3_8b_architecture_4_layers_2048_prompt_bf16_cache():
     _check(ck, prompt, 64, kv_dtype=torch.bfloat16, maxt=2048 + 256, prefill="blocked", prefill_min=256)
 
 
+def test_qwen3_8b_full_depth_2048_prompt_64_tokens_cpu_oracle():
+    """Qwen3-8B architecture at full depth (36 layers, the 151936 x 4096
+    head), random init: 2048-token random prompt through the blocked
+    prefill, bf16 KV cache, context as the benchmark's (2304 positions), the
+    first 64 greedy ids equal to the fp32 oracle's, which runs on the CPU
+    (the engine path is the one bench.py times; the held-off case above ran
+    its oracle on the GPU)."""
+    from ai_amd.model import QWEN3, RandomCkpt
+    print("qwen3-8b full depth, oracle on the cpu", flush=True)
+    ck = RandomCkpt(QWEN3["8b"], seed=0)
+    prompt = [int(t) for t in np.random.default_rng(0).integers(0, ck.V, 2048)]
+    _check(ck, prompt, 64, kv_dtype=torch.bfloat16, maxt=2048 + 256, prefill="blocked", prefill_min=256)
+
+
 def test_qwen3_32b_architecture_2_layers_4096_prompt_and_8_token_pass():
     """Qwen3-32B dimensions with 2 of its 64 layers, random init: 4096-token
     random prompt, bf16 KV cache, the first 16 greedy ids equal to the fp32
