@@ -585,7 +585,6 @@ int rv12_rope_attn(const rv12_attn* a, const float* qkv, const float* qn, const 
 
 size_t rv12_attn_batch_workspace_bytes(const rv12_attn* a, int t) {
     if (check_attn(a) || t < 1 || t > 16) return 0;
-    if (attn_batch_lds_bytes(a->head_dim) > kMaxLds) return 0;
     const size_t q = align256((size_t)t * a->n_heads * a->head_dim * 4);
     const size_t rows = (size_t)t * (a->n_heads / a->n_kv);
     return q + (a->splits > 1 ? 4 * (size_t)a->n_kv * a->splits * rows * (a->head_dim + 2) : 0);

@@ -440,187 +440,8 @@ __global__ __launch_bounds__(64) void k_qk_rope_cache(AttnParams p) {
     }
 }
 
-// 2. grid (kv heads, splits, row chunks), 320 threads: workgroup (g, sp, c)
-// covers the positions [lo, hi) of 0..p0 + T - 1 (at most 80) for rows
-// c R16 .. c R16 + 15 of kv head g (row i: token i / G, head i % G of the
-// group; R16 = kAttnRows), each row seeing positions j <= p0 + its token.
-// The phases of k_rope_attn: cache values loaded first (a quarter key row per
-// thread, value pairs of 16 (8) positions), the chunk's q rows staged in
-// LDS, quarter-dim scores joined by lane exchanges, per-row softmax
-// statistics in one pass, value sums over position groups joined in a fixed
-// order; out (one split) or (acc, m, l) partials for k_attn_combine.
-template <int HD, bool BF16>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_rows(AttnParams p) {
-    extern __shared__ float lds[];
-    constexpr int RC = kAttnRows;
-    constexpr int NW = kAttnThreads / 64;
-    constexpr int P = kAttnSpan;
-    constexpr int EB = BF16 ? 2 : 4;
-    constexpr int QD = HD / 4;
-    constexpr int KW = QD * EB / 16;
-    constexpr int DP = HD / 2;
-    constexpr int PG = kAttnThreads / DP;
-    constexpr int PPG = P / PG;
-    const int g = blockIdx.x, sp = blockIdx.y, S = gridDim.y, c = blockIdx.z;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int H = p.n_heads, G = H / p.n_kv, R = p.T * G;
-    const int r0 = c * RC;  // first row of the chunk
-    const int64_t p0 = *p.pos;
-    float* qs = lds;                 // [RC][HD]
-    float* wt = qs + RC * HD;        // [P][RC] weights exp(s - m)
-    float* red = wt + P * RC;        // [2][NW][RC] per-wave maxima, sums
-    float* stat = red + 2 * NW * RC; // [2 RC] m, l
-    float* wacc = stat + 2 * RC;     // [PG][RC][HD] value sums of the position groups
-    float* part = p.part + ((int64_t)g * S + sp) * R * (HD + 2);  // [n_kv][S][R][HD + 2]
-    if (p0 < 0 || p0 + p.T > p.maxt) {  // zeros out (or partials that combine to zeros), no cache access
-        for (int o = t; o < RC * (HD + 2); o += kAttnThreads) {
-            const int i = o / (HD + 2), d = o % (HD + 2), r = r0 + i;
-            if (r >= R) continue;
-            if (S == 1) {
-                if (d < HD) p.out[((int64_t)(r / G) * H + g * G + r % G) * HD + d] = 0.0f;
-            } else {
-                part[r * (HD + 2) + d] =
-                    d < HD ? 0.0f : (d == HD ? (sp == 0 ? 0.0f : -INFINITY) : (sp == 0 ? 1.0f : 0.0f));
-            }
-        }
-        return;
-    }
-    const int n = (int)p0 + p.T;  // positions 0..n-1; n <= 10240 and S <= 128: 32-bit products
-    const int lo = (int)((uint32_t)(sp * n) / (uint32_t)S), hi = (int)((uint32_t)((sp + 1) * n) / (uint32_t)S);
-    const int span = hi - lo;  // <= P (host)
-    const int64_t row0 = (int64_t)g * p.maxt * HD;
-
-    // ---- 0. cache values of positions [lo, hi): descriptors end at hi
-    const uint32_t cbytes = (uint32_t)hi * HD * EB;
-    const __amdgpu_buffer_rsrc_t kr = attn_rsrc(reinterpret_cast<const char*>(p.kc) + row0 * EB, cbytes);
-    const __amdgpu_buffer_rsrc_t vr = attn_rsrc(reinterpret_cast<const char*>(p.vc) + row0 * EB, cbytes);
-    const int pl = t >> 2, qq = t & 3;
-    uint32_t kw[KW][4];
-    load_words<KW>(kr, ((lo + pl) * HD + qq * QD) * EB, kw);
-    const int dp = t % DP, pg = t / DP;
-    uint32_t vw[PPG][2];
-#pragma unroll
-    for (int r = 0; r < PPG; ++r) {
-        const int off = ((lo + pg * PPG + r) * HD + 2 * dp) * EB;
-        if constexpr (BF16) {
-            vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(vr, off, 0, 0);
-            vw[r][1] = 0;
-        } else {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(vr, off, 0, 0);
-            vw[r][0] = v[0];
-            vw[r][1] = v[1];
-        }
-    }
-    // the chunk's q rows (rows past R read as zeros)
-    for (int o = t; o < RC * HD; o += kAttnThreads) {
-        const int i = o / HD, d = o % HD, r = r0 + i;
-        qs[o] = r < R ? p.qo[((int64_t)(r / G) * H + g * G + r % G) * HD + d] : 0.0f;
-    }
-    __syncthreads();
-
-    // ---- 1. scores; row i sees position j when j <= p0 + its token
-    const int j = lo + pl;
-    float sc[RC];
-#pragma unroll
-    for (int i = 0; i < RC; ++i) {
-        const float* qrow = qs + i * HD + qq * QD;
-        float s = 0.0f;
-#pragma unroll
-        for (int d = 0; d < QD; d += 4) {
-            const float4 q4 = *reinterpret_cast<const float4*>(qrow + d);
-            s = fmaf(q4.x, word_val<BF16>(kw, d), s);
-            s = fmaf(q4.y, word_val<BF16>(kw, d + 1), s);
-            s = fmaf(q4.z, word_val<BF16>(kw, d + 2), s);
-            s = fmaf(q4.w, word_val<BF16>(kw, d + 3), s);
-        }
-        s += dpp<kDppXor1>(s);
-        s += dpp<kDppXor2>(s);
-        const int r = r0 + i;
-        const bool vis = pl < span && r < R && j <= (int)p0 + r / G;
-        sc[i] = vis ? s * p.scale : -INFINITY;
-    }
-
-    // ---- 2. per-row softmax statistics in one pass (as k_rope_attn); a row
-    // that sees none of the split's positions gets m = -inf, l = 0
-#pragma unroll
-    for (int i = 0; i < RC; ++i) {
-        const float mw = wave_max(sc[i]);
-        const float e = sc[i] > -INFINITY ? expf(sc[i] - mw) : 0.0f;
-        const float lw = wave_sum(qq == 0 ? e : 0.0f);
-        if (lane == 0) {
-            red[wave * RC + i] = mw;
-            red[(NW + wave) * RC + i] = lw;
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < RC; ++i) {
-        float m = red[i];
-        for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w * RC + i]);
-        if (qq == 0 && pl < P) wt[pl * RC + i] = sc[i] > -INFINITY ? expf(sc[i] - m) : 0.0f;
-    }
-    if (t < RC) {
-        float m = red[t];
-        for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w * RC + t]);
-        float l = 0.0f;
-        for (int w = 0; w < NW; ++w) {
-            const float lw = red[(NW + w) * RC + t];
-            l += lw > 0.0f ? lw * expf(red[w * RC + t] - m) : 0.0f;
-        }
-        stat[t] = m;
-        stat[RC + t] = l;
-    }
-    __syncthreads();
-
-    // ---- 3. weighted values: thread (dp, pg) over its PPG positions
-    float acc[RC][2];
-#pragma unroll
-    for (int i = 0; i < RC; ++i) acc[i][0] = acc[i][1] = 0.0f;
-#pragma unroll
-    for (int r = 0; r < PPG; ++r) {
-        const int pj = pg * PPG + r;
-        const float v0 = pair_val<BF16>(vw[r], 0), v1 = pair_val<BF16>(vw[r], 1);
-#pragma unroll
-        for (int i = 0; i < RC; ++i) {
-            const float w8 = wt[pj * RC + i];  // zero where the row does not see the position
-            acc[i][0] = fmaf(w8, v0, acc[i][0]);
-            acc[i][1] = fmaf(w8, v1, acc[i][1]);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < RC; ++i) {
-        wacc[(pg * RC + i) * HD + 2 * dp] = acc[i][0];
-        wacc[(pg * RC + i) * HD + 2 * dp + 1] = acc[i][1];
-    }
-    __syncthreads();
-
-    // ---- 4. output or partials
-    for (int o = t; o < RC * HD; o += kAttnThreads) {
-        const int i = o / HD, d = o % HD, r = r0 + i;
-        if (r >= R) continue;
-        float v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < PG; ++w) v += wacc[(w * RC + i) * HD + d];
-        if (S == 1) p.out[((int64_t)(r / G) * H + g * G + r % G) * HD + d] = v / stat[RC + i];
-        else part[r * (HD + 2) + d] = v;
-    }
-    if (S > 1 && t < RC && r0 + t < R) {
-        part[(r0 + t) * (HD + 2) + HD] = stat[t];
-        part[(r0 + t) * (HD + 2) + HD + 1] = stat[RC + t];
-    }
-}
-
-template <int HD, bool BF16>
-static void launch_batch_t(const AttnParams& p, int S, hipStream_t st) {
-    const int R = p.T * (p.n_heads / p.n_kv);
-    hipLaunchKernelGGL((k_qk_rope_cache<HD, BF16>), dim3(p.n_heads + 2 * p.n_kv, p.T), dim3(64), 0, st, p);
-    const size_t lds = attn_batch_lds_bytes(HD);
-    if (lds > kDefaultLds)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_rows<HD, BF16>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((k_attn_rows<HD, BF16>), dim3(p.n_kv, S, (R + kAttnRows - 1) / kAttnRows),
-                       dim3(kAttnThreads), lds, st, p);
-}
+// 2. the attention itself: k_prefill_attn below over S position splits
+// (launch_batch_t), then k_attn_combine.
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));  // four bf16 MFMA operand bits
 
@@ -632,8 +453,11 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));  // four bf16 MFMA oper
 // on the float32 matrix cores, v_mfma_f32_16x16x4_f32 (lane l: A row l%16,
 // B column l%16, k = l/16; result rows 4(l/16) + 0..3, column l%16).
 //
-// Grid (token tiles of 16, kv heads), the last tile first (it has the most
-// positions); workgroup = the G query heads of kv head g, one wave per head,
+// Grid (token tiles of 16, kv heads, position splits), the last tile first
+// (it has the most positions); with S > 1 splits (the batched pass: T <= 16,
+// one tile) split sp covers blocks [sp nkb / S, (sp + 1) nkb / S) of the
+// tile's nkb blocks of 16 positions and writes (sums, m, l) partials for
+// k_attn_combine; workgroup = the G query heads of kv head g, one wave per head,
 // all reading the same cache rows.  Per block of 16 positions a wave computes
 // the scores transposed, S^T = K . Q^T (rows = positions, columns = its 16
 // tokens), so each lane holds 4 positions of one token: the online softmax
@@ -661,15 +485,26 @@ __global__ __launch_bounds__(512) void k_prefill_attn(AttnParams p) {
     const int q4 = lane >> 4, c16 = lane & 15;
     const int H = p.n_heads, KV = p.n_kv, G = H / KV;
     const int g = blockIdx.y, h = g * G + wv;
+    const int S = gridDim.z, sp = blockIdx.z;  // position splits (S > 1: T <= 16, one token tile)
     const int T = p.T;
     const int ntile = (T + 15) >> 4;
     const int t0 = (ntile - 1 - (int)blockIdx.x) * 16;
     const int tq = t0 + c16;  // this lane's token
     const int64_t p0 = *p.pos;
     float* orow = p.out + (int64_t)min(tq, T - 1) * H * HD + h * HD;
+    // split partials [n_kv][S][R][HD + 2], row tq G + (h - g G) of R = T G
+    float* prow =
+        S > 1 ? p.part + (((int64_t)g * S + sp) * T * G + (int64_t)min(tq, T - 1) * G + wv) * (HD + 2) : nullptr;
     if (p0 < 0 || p0 + T > p.maxt) {  // a block outside the cache: zeros, as the prologue writes nothing
-        if (tq < T && q4 == 0)
-            for (int d = 0; d < HD; ++d) orow[d] = 0.0f;
+        if (tq < T && q4 == 0) {
+            if (S == 1) {
+                for (int d = 0; d < HD; ++d) orow[d] = 0.0f;
+            } else {  // partials that combine to zeros: acc 0, and l = 1 on split 0 only
+                for (int d = 0; d < HD; ++d) prow[d] = 0.0f;
+                prow[HD] = sp == 0 ? 0.0f : -INFINITY;
+                prow[HD + 1] = sp == 0 ? 1.0f : 0.0f;
+            }
+        }
         return;
     }
     const int n = (int)p0 + T;  // positions in the cache after the block
@@ -703,7 +538,9 @@ __global__ __launch_bounds__(512) void k_prefill_attn(AttnParams p) {
         for (int a = 0; a < NA; ++a) split3(qv[a], qp[a][0], qp[a][1], qp[a][2]);
     }
     const int last = min((int)p0 + t0 + 15, n - 1);  // last position any token of the tile sees
+    // this split's blocks of 16 positions: [kb0, kb1) of the tile's nkb
     const int nkb = last / 16 + 1;
+    const int kb0 = (int)((int64_t)sp * nkb / S), kb1 = (int)((int64_t)(sp + 1) * nkb / S);
 
     uint32_t kw[NA][KWD], vw[4][VWD];
     auto load_block = [&](int kb) {
@@ -744,8 +581,8 @@ __global__ __launch_bounds__(512) void k_prefill_attn(AttnParams p) {
     for (int d = 0; d < DT; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
     const int qpos = (int)p0 + tq;  // the last position this lane's token sees
-    load_block(0);
-    for (int kb = 0; kb < nkb; ++kb) {
+    if (kb0 < kb1) load_block(kb0);
+    for (int kb = kb0; kb < kb1; ++kb) {
         uint32_t kcur[NA][KWD], vcur[4][VWD];
 #pragma unroll
         for (int a = 0; a < NA; ++a)
@@ -755,7 +592,7 @@ __global__ __launch_bounds__(512) void k_prefill_attn(AttnParams p) {
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < VWD; ++i) vcur[j][i] = vw[j][i];
-        if (kb + 1 < nkb) load_block(kb + 1);
+        if (kb + 1 < kb1) load_block(kb + 1);
         // scores of positions kb 16 + 4 q4 + r for token tq
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (BF16) {
@@ -784,12 +621,15 @@ __global__ __launch_bounds__(512) void k_prefill_attn(AttnParams p) {
         }
         mb = fmaxf(mb, __shfl_xor(mb, 16));
         mb = fmaxf(mb, __shfl_xor(mb, 32));
-        const float mn = fmaxf(m, mb);  // finite from block 0 on: position 0 is seen by every token
-        const float alpha = expf(m - mn);
+        // finite from the first block with a position the token sees (block 0
+        // for every token of an unsplit range); before it nothing accumulates
+        const float mn = fmaxf(m, mb);
+        const bool none = mn == -INFINITY;
+        const float alpha = none ? 1.0f : expf(m - mn);
         float ls = 0.0f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            pr[r] = expf(sc[r] - mn);
+            pr[r] = none ? 0.0f : expf(sc[r] - mn);
             ls += pr[r];
         }
         l = l * alpha + ls;
@@ -833,6 +673,21 @@ __global__ __launch_bounds__(512) void k_prefill_attn(AttnParams p) {
     }
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
+    if (S > 1) {  // the split's partial: unnormalised sums, m, l
+        if (tq < T) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float* dst = prow + DT * (4 * q4 + r);
+#pragma unroll
+                for (int d = 0; d < DT; ++d) dst[d] = o[d][r];
+            }
+            if (q4 == 0) {
+                prow[HD] = m;
+                prow[HD + 1] = l;
+            }
+        }
+        return;
+    }
     if (tq < T) {
         // lane l holds dims DT (4 q4 + r) + dt of its token
 #pragma unroll
@@ -866,7 +721,17 @@ int launch_prefill_attn(const AttnParams& p, hipStream_t st) {
     return 0;
 }
 
+// the batched pass (T <= 16 tokens): the prologue, then the prompt attention
+// kernel over S position splits (one token tile, its G waves per kv head on
+// the matrix cores), then the combine of the splits
+template <int HD, bool BF16>
+static void launch_batch_t(const AttnParams& p, int S, hipStream_t st) {
+    hipLaunchKernelGGL((k_qk_rope_cache<HD, BF16>), dim3(p.n_heads + 2 * p.n_kv, p.T), dim3(64), 0, st, p);
+    hipLaunchKernelGGL((k_prefill_attn<HD, BF16>), dim3(1, p.n_kv, S), dim3(64 * (p.n_heads / p.n_kv)), 0, st, p);
+}
+
 int launch_attn_batch(const AttnParams& p, int S, hipStream_t st) {
+    if (p.T < 1 || p.T > 16) return -1;
     if (p.head_dim == 128) {
         if (p.kv_bf16) launch_batch_t<128, true>(p, S, st);
         else launch_batch_t<128, false>(p, S, st);

@@ -113,13 +113,8 @@ inline size_t attn_part_floats(int n_kv, int g, int hd, int splits) {
     return (size_t)n_kv * splits * g * (hd + 2);
 }
 int launch_attn(const AttnParams& p, int splits, hipStream_t st);
-// batch of T tokens: rows of one kv head = T * G, handled kAttnRows at a time
-constexpr int kAttnRows = 16;
-inline size_t attn_batch_lds_bytes(int hd) {
-    const size_t pg = kAttnThreads / (hd / 2);
-    return 4 * ((size_t)kAttnRows * hd + (size_t)kAttnSpan * kAttnRows + 2 * (kAttnThreads / 64) * kAttnRows +
-                2 * kAttnRows + pg * kAttnRows * hd);
-}
+// batch of T <= 16 tokens: rows of one kv head = T * G (the prompt attention
+// kernel over position splits, then the combine)
 int launch_attn_batch(const AttnParams& p, int splits, hipStream_t st);
 // prompt block of T tokens: the q/k/v prologue, then causal attention on the
 // float32 matrix cores (one wave per head and 16 tokens)
