@@ -277,9 +277,10 @@ int rv12_rope_attn(const rv12_attn* a, const float* qkv, const float* qn, const 
  * head RMSNorm and RoPE at their position, k and v (rounded to the cache dtype)
  * go into the caches, and token r attends over positions 0..*pos + r (causal)
  * into out[r] (t rows of n_heads * head_dim floats).  Three passes (q/k/v
- * prologue; attention of the batch's 16-token tile over a.splits position
- * splits, one wave per query head on the matrix cores — float32 products, as
- * rv12_prefill_rope_attn; the ordered combine), no atomics.  A batch
+ * prologue; attention of the batch's 16-token tile over min(a.splits,
+ * ceil(256 / n_kv)) position splits, one wave per query head on the matrix
+ * cores — float32 products, as rv12_prefill_rope_attn; the ordered combine),
+ * no atomics.  A batch
  * outside [0, maxt) gives zeros and leaves the caches untouched.  ws:
  * rv12_attn_batch_workspace_bytes(a, t) bytes (the q rows and the split
  * partials), 16-byte aligned.  Replaces qk_rope_cache_k and attn_k,
