@@ -28,7 +28,7 @@ EXPORTS = ("rv12_abi_version", "rv12_strerror", "rv12_tiles_bytes", "rv12_pack_p
            "rv12_attn_batch_workspace_bytes", "rv12_rope_attn_batch", "rv12_prefill_attn_workspace_bytes",
            "rv12_prefill_rope_attn", "rv12_prefill_workspace_bytes",
            "rv12_prefill_linear", "rv12_decode_advance")
-ABI_VERSION = 7
+ABI_VERSION = 8
 STATIC_SCRATCH_BYTES = 8 << 20  # RV12_STATIC_SCRATCH_BYTES
 
 
@@ -120,7 +120,7 @@ def lib():
         L.rv12_rope_attn.restype = I
         L.rv12_rope_attn.argtypes = [ctypes.POINTER(Attn), P, P, P, P, P, P, P, P, P, SZ, P]
         L.rv12_prefill_workspace_bytes.restype = SZ
-        L.rv12_prefill_workspace_bytes.argtypes = [I, I]
+        L.rv12_prefill_workspace_bytes.argtypes = [I, I, I]
         L.rv12_prefill_linear.restype = I
         L.rv12_prefill_linear.argtypes = [ctypes.POINTER(Matrix), P, P, I, P, F, I, P, SZ, P]
         L.rv12_decode_advance.restype = I

@@ -497,9 +497,9 @@ int rv12_head_argmax(const rv12_matrix* w, const float* x, int t, const uint16_t
     return launch_status();
 }
 
-size_t rv12_prefill_workspace_bytes(int k, int t) {
-    if (k < 32 || k % 32 || k > kMaxK || t < 1 || t > kMaxPrefillTokens) return 0;
-    return prefill_ws_bytes(k, t);
+size_t rv12_prefill_workspace_bytes(int n, int k, int t) {
+    if (n < 1 || k < 32 || k % 32 || k > kMaxK || t < 1 || t > kMaxPrefillTokens) return 0;
+    return prefill_ws_bytes(n, k, t);
 }
 
 int rv12_prefill_linear(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps,
@@ -512,7 +512,7 @@ int rv12_prefill_linear(const rv12_matrix* w, const float* x, float* y, int t, c
     if (lnw && (uintptr_t)lnw % 16) return RV12_E_ALIGN;
     if (t < 1 || t > kMaxPrefillTokens) return RV12_E_TOKENS;
     if (!aligned16(x) || !aligned16(y)) return RV12_E_ALIGN;
-    const size_t need = prefill_ws_bytes(w->k, t);
+    const size_t need = prefill_ws_bytes(w->n, w->k, t);
     if (!ws || ws_bytes < need) return RV12_E_WORKSPACE;
     if (!aligned16(ws)) return RV12_E_ALIGN;
     launch_prefill(*w, x, y, t, mode, lnw, eps, ws, (hipStream_t)stream);

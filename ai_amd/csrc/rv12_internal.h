@@ -140,7 +140,8 @@ void launch_pick(const float* v, const int32_t* ix, int64_t n, int64_t stride, i
                  int64_t* ids, hipStream_t st);
 // --- prefill linear (k_prefill_x + k_prefill_mm), any T
 constexpr int kMaxPrefillTokens = 1 << 16;
-size_t prefill_ws_bytes(int K, int T);
+size_t prefill_ws_bytes(int N, int K, int T);
+int prefill_splits(int N, int K, int T);
 void launch_decode_advance(const int64_t* ids, const uint16_t* emb, int64_t vocab, int hidden, float* x,
                            int64_t* out, int64_t out_len, int64_t* steps, int64_t* pos, int64_t* tok,
                            hipStream_t st);

@@ -206,12 +206,15 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
                                                            const int32_t* __restrict__ ec,
                                                            const float* __restrict__ ev, const float* __restrict__ xt,
                                                            int tp, const float* __restrict__ R, float* __restrict__ y,
-                                                           int N, int K, int T, int add) {
+                                                           float* __restrict__ part, int N, int K, int T, int add) {
     extern __shared__ u32x4 bs[];  // [kPfRing][kPfSlot]: A tiles and B parts of steps s .. s + 3
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wr = wave % kPfWR, wc = wave / kPfWR;
     const int nsteps = K >> 5;
+    // K split blockIdx.y of gridDim.y: steps [s_lo, s_hi)
+    const int S = gridDim.y, sp = blockIdx.y;
+    const int s_lo = (int)((int64_t)sp * nsteps / S), s_hi = (int)((int64_t)(sp + 1) * nsteps / S);
     const int64_t nblk = (N + 15) / 16;
     const int nx = (int)((nblk + kPfRowBlocks - 1) / kPfRowBlocks);
     int rt, tt;
@@ -247,8 +250,9 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     // step s's A tiles and B parts into LDS slot `slot`; a step past the end
     // goes through the 0-byte descriptors, which write zeros, so the loop has
     // no branch around a load
-    auto load_step = [&](int slot, int s) {
-        const bool in = s < nsteps;
+    auto load_step = [&](int slot, int j) {  // step s_lo + j
+        const int s = s_lo + j;
+        const bool in = s < s_hi;
         const __amdgpu_buffer_rsrc_t ra = in ? rv : rnull, rb = in ? rbx : rbnull;
         const int sa = (in ? s : 0) * kStepBytes, sb = (in ? s : 0) * 192 * 16;
         u32x4* d = bs + slot * kPfSlot;
@@ -296,9 +300,9 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
     // step s + 1 have landed, and every wave is done reading slot s % 4);
     // step s + 4 into that slot; the fragments of step s + 1 read while the
     // A groups of step s are unpacked and its 48 MFMAs run.  The loop runs
-    // whole rounds of the unroll: steps past nsteps read zeros (A and B) and
+    // whole rounds of the unroll: steps past the split read zeros (A and B) and
     // add nothing.
-    const int nround = (nsteps + kPfRing - 1) / kPfRing * kPfRing;
+    const int nround = (s_hi - s_lo + kPfRing - 1) / kPfRing * kPfRing;
     for (int s0 = 0; s0 < nround; s0 += kPfRing) {
 #pragma unroll
         for (int u = 0; u < kPfRing; ++u) {
@@ -365,7 +369,10 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
         const int32_t e_lo = rp[rlo], e_hi = rp[min(rlo + 16 * kPfWB, (int64_t)N)];
         constexpr int EB = 8;
         const float* xtw = xt + (int64_t)(tb0 + wc * kPfWT) * 16 + jj;  // token block c at + 16 c
+        // (with a K split, the entries whose column lies in the split's steps)
+        const int c_lo = s_lo * 32, c_hi = s_hi * 32;
         int nr[EB];
+        bool nin[EB];
         float nv[EB], ng[EB][kPfWT];
         auto fetch = [&](int32_t e0) {
 #pragma unroll
@@ -373,7 +380,9 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
                 const int32_t e = min(e0 + j, e_hi - 1);
                 nr[j] = (int)(er[e] - rlo);
                 nv[j] = ev[e];
-                const float* xc = xtw + (int64_t)ec[e] * tp;
+                const int col = ec[e];
+                nin[j] = col >= c_lo && col < c_hi;
+                const float* xc = xtw + (int64_t)col * tp;
 #pragma unroll
                 for (int c = 0; c < kPfWT; ++c) ng[j][c] = xc[c * 16];
             }
@@ -381,10 +390,12 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
         fetch(e_lo);
         for (int32_t e0 = e_lo; e0 < e_hi; e0 += EB) {
             int rr[EB];
+            bool rin[EB];
             float evv[EB], xv[EB][kPfWT];
 #pragma unroll
             for (int j = 0; j < EB; ++j) {
                 rr[j] = nr[j];
+                rin[j] = nin[j];
                 evv[j] = nv[j];
 #pragma unroll
                 for (int c = 0; c < kPfWT; ++c) xv[j][c] = ng[j][c];
@@ -393,6 +404,7 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
 #pragma unroll
             for (int j = 0; j < EB; ++j) {
                 if (e0 + j >= e_hi) break;
+                if (!rin[j]) continue;
                 const int r = rr[j];
                 const bool mine = q == ((r & 15) >> 2);
 #define RV12_EXC_CASE(B, I)                                                                 \
@@ -414,7 +426,23 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
         }
     }
     // (c) with RMS the token's rs; store or add; rows past N and tokens past
-    // T are skipped
+    // T are skipped.  With a K split: the split's sums to part[sp][token][row]
+    // (rs and the store or add are the reduce pass's)
+    if (S > 1) {
+        float* ps = part + (int64_t)sp * tp * N;
+#pragma unroll
+        for (int c = 0; c < kPfWT; ++c) {
+            if (tok[c] >= T) continue;
+#pragma unroll
+            for (int b = 0; b < kPfWB; ++b) {
+                const int64_t n = (blk0 + b) * 16 + q * 4;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (n + i < N) ps[(int64_t)tok[c] * N + n + i] = v[b][c][i];
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < kPfWT; ++c) {
         if (tok[c] >= T) continue;
@@ -440,9 +468,50 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
 
 int prefill_tokens_padded(int T) { return (T + kPfTokBlocks * 16 - 1) / (kPfTokBlocks * 16) * (kPfTokBlocks * 16); }
 
-size_t prefill_ws_bytes(int K, int T) {
+// 3. (K split only) y[t][n] (=|+=) rs_t * sum over the splits, in split order
+__global__ __launch_bounds__(256) void k_prefill_reduce(const float* __restrict__ part, const float* __restrict__ R,
+                                                        float* __restrict__ y, int64_t N, int T, int tp, int S,
+                                                        int add) {
+    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (n >= N) return;
+    for (int t = blockIdx.y; t < T; t += gridDim.y) {
+        float v = 0.0f;
+        for (int sp = 0; sp < S; ++sp) v += part[((int64_t)sp * tp + t) * N + n];
+        if (R) v *= R[t];
+        float* yp = y + (int64_t)t * N + n;
+        *yp = add ? *yp + v : v;
+    }
+}
+
+// K splits of the GEMM: the fewest that minimise a model of its rounds of
+// workgroups (one per CU) — each round costs the steps of a split at 1.4 us
+// plus 10 us — and of the reduce pass over the (S + 1) T N partial floats
+// (3 us + bytes at 5 TB/s); no split below 8 steps
+int prefill_splits(int N, int K, int T) {
+    const int64_t nx = ((int64_t)N + 16 * kPfRowBlocks - 1) / (16 * kPfRowBlocks);
+    const int64_t tp = prefill_tokens_padded(T);
+    const int64_t G = nx * (tp / (kPfTokBlocks * 16));
+    const int nsteps = K / 32;
+    int best = 1;
+    double best_us = 0.0;
+    for (int S = 1; S <= 16; ++S) {
+        if (S > 1 && nsteps / S < 8) break;
+        const double rounds = (double)((G * S + 255) / 256);
+        double us = rounds * ((double)nsteps / S * 1.4 + 10.0);
+        if (S > 1) us += 3.0 + (double)(S + 1) * tp * N * 4 / 5e6;
+        if (S == 1 || us < best_us) {
+            best = S;
+            best_us = us;
+        }
+    }
+    return best;
+}
+
+size_t prefill_ws_bytes(int N, int K, int T) {
     const size_t tp = (size_t)prefill_tokens_padded(T);
-    return tp * (size_t)K * 10 + tp * 8;  // parts, P and R, transposed x'
+    const int S = prefill_splits(N, K, T);
+    // parts, P and R, transposed x', split partials
+    return tp * (size_t)K * 10 + tp * 8 + (S > 1 ? (size_t)S * tp * (size_t)N * 4 : 0);
 }
 
 void launch_prefill(const rv12_matrix& w, const float* x, float* y, int T, int mode, const uint16_t* lnw, float eps,
@@ -453,19 +522,24 @@ void launch_prefill(const rv12_matrix& w, const float* x, float* y, int T, int m
     int* P = reinterpret_cast<int*>(reinterpret_cast<char*>(ws) + (size_t)tp * K * 6);
     float* R = reinterpret_cast<float*>(P + tp);
     float* xt = R + tp;
+    float* part = xt + (size_t)tp * K;
     const int xs = mode == 2 ? 2 * K : K;
     const int m2 = mode == 2 ? 1 : 0;
     hipLaunchKernelGGL(k_prefill_stats, dim3(tp / (kPsThreads / 64)), dim3(kPsThreads), 0, st, x, T, K, xs, m2, lnw, eps,
                        P, R);
     hipLaunchKernelGGL(k_prefill_parts, dim3(tp / 32, (K + 63) / 64), dim3(kPpThreads), 0, st, x, T, K, xs, m2, lnw, P,
                        xb, xt, tp);
+    const int S = prefill_splits(N, K, T);
     const int64_t nblk = ((int64_t)N + 15) / 16;
-    const dim3 grid((unsigned)((nblk + kPfRowBlocks - 1) / kPfRowBlocks * (tp / (kPfTokBlocks * 16))));
+    const dim3 grid((unsigned)((nblk + kPfRowBlocks - 1) / kPfRowBlocks * (tp / (kPfTokBlocks * 16))), (unsigned)S);
     const auto kern = lnw ? k_prefill_mm<true> : k_prefill_mm<false>;
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)kPfLds);
     hipLaunchKernelGGL(kern, grid, dim3(kPfThreads), kPfLds, st, reinterpret_cast<const uint32_t*>(w.tiles), w.rbase, xb,
-                       P, w.rp, w.er, w.ec, w.ev, xt, tp, R, y, N, K, T, mode != 0 ? 1 : 0);
+                       P, w.rp, w.er, w.ec, w.ev, xt, tp, R, y, part, N, K, T, mode != 0 ? 1 : 0);
+    if (S > 1)
+        hipLaunchKernelGGL(k_prefill_reduce, dim3((unsigned)((N + 255) / 256), (unsigned)min(T, 65535)), dim3(256), 0, st, part,
+                           lnw ? R : nullptr, y, (int64_t)N, T, tp, S, mode != 0 ? 1 : 0);
 }
 
 }  // namespace rv12

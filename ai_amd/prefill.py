@@ -62,7 +62,7 @@ def _linear(x, c, y, mode, lnw=None, eps=1e-6):
     if lnw is not None and (lnw.dtype != torch.bfloat16 or not lnw.is_contiguous() or lnw.numel() < K):
         raise ValueError("prefill: lnw must be a contiguous bf16 vector of K entries")
     L = _lib.lib()
-    need = L.rv12_prefill_workspace_bytes(K, T)
+    need = L.rv12_prefill_workspace_bytes(N, K, T)
     if need == 0:
         raise ValueError("prefill: too many tokens")
     key = str(x.device)

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define RV12_ABI_VERSION 7
+#define RV12_ABI_VERSION 8
 
 enum rv12_status {
     RV12_OK = 0,
@@ -228,14 +228,18 @@ int rv12_gemm_static(const rv12_matrix* w, const float* x, float* y, int t, cons
  * as rv12_gemv.  The 12-bit decode is fused into a bf16 MFMA GEMM:
  * x' is split per token into three bf16 parts (24 significand bits, after an
  * exact power-of-two scale), every weight is read once in its 12-bit form,
- * products and sums are fp32, the exceptions are added in list order.  ws:
- * rv12_prefill_workspace_bytes(k, t) bytes (10 bytes per column and padded
- * token: the parts and a transposed fp32 copy of x' for the exception
- * entries; and 8 per padded token), 16-byte aligned.  Replaces the
+ * products and sums are fp32, the exceptions are added in list order.  Where
+ * the rows and tokens give too few workgroups to fill the GPU (few tokens, or
+ * a last round of workgroups mostly empty), K is split and an ordered pass
+ * sums the splits.  ws: rv12_prefill_workspace_bytes(n, k, t) bytes (10 bytes
+ * per column and padded token: the parts and a transposed fp32 copy of x'
+ * for the exception entries; 8 per padded token; with a K split, 4 per split,
+ * padded token and row for the partial sums), 16-byte aligned; 0 for
+ * arguments rv12_prefill_linear rejects.  Replaces the
  * blocked prefill's rmsg_k + matrix() (decode_rows + the fp32 GEMM mm_k),
  * ramvi/engine/ramvi_engine/kernels/prefill.py:66-78, 94-99,
  * ramvi/engine/ramvi_engine/kernels/prefill_kernels.py:8-26, 58-110. */
-size_t rv12_prefill_workspace_bytes(int k, int t);
+size_t rv12_prefill_workspace_bytes(int n, int k, int t);
 int rv12_prefill_linear(const rv12_matrix* w, const float* x, float* y, int t, const uint16_t* lnw, float eps,
                         int mode, void* ws, size_t ws_bytes, void* stream);
 

@@ -31,7 +31,7 @@ def test_library_exports_every_symbol():
 def test_abi_version_and_strerror():
     from ai_amd import _lib
     L = _lib.lib()
-    assert L.rv12_abi_version() == 7
+    assert L.rv12_abi_version() == 8
     for s in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -20):
         assert _lib.strerror(s) and _lib.strerror(s) != "unknown rv12 status"
     assert _lib.strerror(-99) == "unknown rv12 status"
