@@ -479,7 +479,7 @@ def cpu_baseline(dev, gpu_ids_0_6b=None, budget=0.7):
                   dot it with every token), from the reference codec's own
                   arrays, per Qwen3-8B shape at M=1;
       matmat16    the CPU layer's bf16 linear (cpu/cpu_layer.py:35-48), per shape;
-      e2e_qwen3_0_6b  config 1 end to end: CpuLayer.__call__ over 28 layers +
+      e2e_qwen3_0_6b  Qwen3-0.6B end to end: CpuLayer.__call__ over 28 layers +
                   the exact greedy head (cpu/cpu_layer.py:155-175,
                   generation/head.py:19-26), 128-token prompt, 64 new tokens.
     value: the gemv_12bit leg over one Qwen3-8B layer's qkv / o / gu / down
@@ -538,7 +538,7 @@ def cpu_baseline(dev, gpu_ids_0_6b=None, budget=0.7):
     n, dt = _timed(one_layer, 3.0)  # 0.33 GB of codec arrays per pass: beyond the host caches
     value = cbytes * n / dt / 1e9
     del layer
-    # config 1 end to end (weights drawn on the GPU, as the GPU engine's)
+    # Qwen3-0.6B end to end (weights drawn on the GPU, as the GPU engine's)
     ck = RandomCkpt(QWEN3["0.6b"], seed=0)
     m = cpu_qwen3.load(ck, dev)
     prompt = [int(t) for t in np.random.default_rng(0).integers(0, ck.V, 128)]
