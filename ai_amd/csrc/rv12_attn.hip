@@ -17,7 +17,8 @@
 //   2. scores s[i][j] = scale * q_i . K[j]: each of the 4 threads of a
 //      position sums its quarter of the dims, two lane exchanges add them;
 //      j == pos uses the step's own k;
-//   3. per head the split's max m and sum l of exp(s - m);
+//   3. per head (one wave each, the scores passed through LDS) the split's
+//      max m, the weights exp(s - m) and their sum l;
 //   4. acc[i][d] = sum_j exp(s[i][j] - m_i) V[j][d]: threads over dim pairs and
 //      position groups, the groups added through LDS in a fixed order;
 //   5. one split: out = acc / l.  Several: (acc, m, l) partials, combined by
@@ -111,14 +112,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
     constexpr int half = HD / 2, HPW = (G + NW) / NW;
     const int g = blockIdx.x, sp = blockIdx.y, S = gridDim.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wu = __builtin_amdgcn_readfirstlane(wave);
     const int H = p.n_kv * G;
     const int64_t pos = *p.pos;
     float* qs = lds;                // [G][HD]
     float* kn = qs + G * HD;        // [HD] step key (normed, roped, rounded)
     float* vn = kn + HD;            // [HD] step value (rounded)
     float* wt = vn + HD;            // [P][G] weights exp(s - m)
-    float* red = wt + P * G;        // [2][NW][G] per-wave maxima, sums
-    float* stat = red + 2 * NW * G; // [2 G] m, l
+    float* ss = wt + P * G;         // [G][P] scaled scores (-inf beyond the span)
+    float* stat = ss + G * P;       // [2 G] m, l
     float* wacc = stat + 2 * G;     // [PG][G][HD] value sums of the position groups
     if (pos < 0 || pos >= p.maxt) {  // a position outside the cache: zeros out, no cache access
         if (S == 1) {
@@ -203,25 +205,41 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
     }
     __syncthreads();
 
-    // ---- 2. scores: thread (pl, qq) sums its quarter of the dims
+    // ---- 2. scores: thread (pl, qq) sums its quarter of the dims.  The key
+    // quarter (the step's own key at j == pos, whose cache slot reads as
+    // zeros) and the G heads' q quarters are in registers before the first
+    // product, so the LDS reads are waited for once
     const bool valid = pl < span;
     const bool own = lo + pl == pos;
+    float kf[QD];
+#pragma unroll
+    for (int d = 0; d < QD; ++d) kf[d] = word_val<BF16>(kw, d);
+    if (own) {
+#pragma unroll
+        for (int d = 0; d < QD; d += 4) {
+            const float4 k4 = *reinterpret_cast<const float4*>(kn + qq * QD + d);
+            kf[d] = k4.x;
+            kf[d + 1] = k4.y;
+            kf[d + 2] = k4.z;
+            kf[d + 3] = k4.w;
+        }
+    }
+    float4 qv[G][QD / 4];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+#pragma unroll
+        for (int d = 0; d < QD; d += 4) qv[i][d / 4] = *reinterpret_cast<const float4*>(qs + i * HD + qq * QD + d);
+    }
     float sc[G];
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-        const float* qrow = qs + i * HD + qq * QD;
         float s = 0.0f;
 #pragma unroll
         for (int d = 0; d < QD; d += 4) {
-            const float4 q4 = *reinterpret_cast<const float4*>(qrow + d);
-            s = fmaf(q4.x, word_val<BF16>(kw, d), s);
-            s = fmaf(q4.y, word_val<BF16>(kw, d + 1), s);
-            s = fmaf(q4.z, word_val<BF16>(kw, d + 2), s);
-            s = fmaf(q4.w, word_val<BF16>(kw, d + 3), s);
-        }
-        if (own) {  // the step's own key (its cache slot read as zeros)
-            s = 0.0f;
-            for (int d = 0; d < QD; ++d) s = fmaf(qrow[d], kn[qq * QD + d], s);
+            s = fmaf(qv[i][d / 4].x, kf[d], s);
+            s = fmaf(qv[i][d / 4].y, kf[d + 1], s);
+            s = fmaf(qv[i][d / 4].z, kf[d + 2], s);
+            s = fmaf(qv[i][d / 4].w, kf[d + 3], s);
         }
         sc[i] = s;
     }
@@ -233,36 +251,29 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
         sc[i] = valid ? s * p.scale : -INFINITY;
     }
 
-    // ---- 3. softmax statistics in one pass: each wave's max m_w of a head's
-    // scores and sum l_w of exp(s - m_w); after one barrier the split's max
-    // M = max_w m_w, the weights exp(s - M) and L = sum_w l_w exp(m_w - M)
+    // ---- 3. softmax statistics: the scores go through LDS, then the wave
+    // of each head (wave w takes the heads w, w + NW, ..) finds the split's
+    // max m, the weights exp(s - m) and their sum l with wave-wide reductions
+    // only (lane j holds the positions j and j + 64)
+    if (qq == 0) {
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-        const float mw = wave_max(sc[i]);
-        const float e = valid ? expf(sc[i] - mw) : 0.0f;
-        const float lw = wave_sum(qq == 0 ? e : 0.0f);
-        if (lane == 0) {
-            red[wave * G + i] = mw;
-            red[(NW + wave) * G + i] = lw;
-        }
+        for (int i = 0; i < G; ++i) ss[i * P + pl] = sc[i];
     }
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-        float m = red[i];
-        for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w * G + i]);
-        if (qq == 0) wt[pl * G + i] = valid ? expf(sc[i] - m) : 0.0f;
-    }
-    if (t < G) {
-        float m = red[t];
-        for (int w = 1; w < NW; ++w) m = fmaxf(m, red[w * G + t]);
-        float l = 0.0f;
-        for (int w = 0; w < NW; ++w) {
-            const float lw = red[(NW + w) * G + t];
-            l += lw > 0.0f ? lw * expf(red[w * G + t] - m) : 0.0f;
+    static_assert(P > 64 && P <= 128, "two positions per lane");
+    for (int i = wu; i < G; i += NW) {
+        const bool v1 = lane < span, v2 = lane + 64 < span;
+        const float a = ss[i * P + lane];
+        const float b = lane + 64 < P ? ss[i * P + lane + 64] : -INFINITY;
+        const float m = wave_max(fmaxf(a, b));
+        const float ea = v1 ? expf(a - m) : 0.0f, eb = v2 ? expf(b - m) : 0.0f;
+        wt[lane * G + i] = ea;
+        if (lane + 64 < P) wt[(lane + 64) * G + i] = eb;
+        const float l = wave_sum(ea + eb);
+        if (lane == 0) {
+            stat[i] = m;
+            stat[G + i] = l;
         }
-        stat[t] = m;
-        stat[G + t] = l;
     }
     __syncthreads();  // the weights of every position
 
@@ -271,17 +282,21 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < G; ++i) acc[i][0] = acc[i][1] = 0.0f;
     const float vn0 = vn[2 * dp], vn1 = vn[2 * dp + 1];
+    float w[PPG][G];  // the weights (zero beyond the span), read before the first product
 #pragma unroll
     for (int r = 0; r < PPG; ++r) {
-        const int pj = pg * PPG + r;
-        const bool ownj = lo + pj == pos;
+#pragma unroll
+        for (int i = 0; i < G; ++i) w[r][i] = wt[(pg * PPG + r) * G + i];
+    }
+#pragma unroll
+    for (int r = 0; r < PPG; ++r) {
+        const bool ownj = lo + pg * PPG + r == pos;
         const float v0 = ownj ? vn0 : pair_val<BF16>(vw[r], 0);
         const float v1 = ownj ? vn1 : pair_val<BF16>(vw[r], 1);
 #pragma unroll
         for (int i = 0; i < G; ++i) {
-            const float w8 = wt[pj * G + i];  // zero beyond the span
-            acc[i][0] = fmaf(w8, v0, acc[i][0]);
-            acc[i][1] = fmaf(w8, v1, acc[i][1]);
+            acc[i][0] = fmaf(w[r][i], v0, acc[i][0]);
+            acc[i][1] = fmaf(w[r][i], v1, acc[i][1]);
         }
     }
 #pragma unroll

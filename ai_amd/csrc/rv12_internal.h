@@ -105,7 +105,7 @@ constexpr int kAttnSpan = 80;         // positions one attention workgroup cover
 constexpr int kAttnMaxSplits = 128;   // so the context is at most 10240 positions
 inline size_t attn_lds_bytes(int hd, int g) {
     const size_t pg = kAttnThreads / (hd / 2);  // position groups of the value sums
-    return 4 * ((size_t)g * hd + 2 * (size_t)hd + (size_t)kAttnSpan * g + 2 * (kAttnThreads / 64) * (size_t)g +
+    return 4 * ((size_t)g * hd + 2 * (size_t)hd + (size_t)kAttnSpan * g + (size_t)kAttnSpan * g +
                 2 * (size_t)g +
                 pg * g * hd);
 }
