@@ -334,12 +334,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
 // 12 splits: 7.42 -> 7.24 us with 16 against 32).
 // R rows per kv head (G at one token, T G for a batch: row i is token i / G,
 // head i % G of the group); out is [T][n_heads][HD].
-template <int CB>
+// HD is a template argument, so the loops over the workgroup's waves unroll.
+template <int HD, int CB>
 __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out, int S,
-                                                      int G, int HD, int R, int H) {
+                                                      int G, int R, int H) {
+    constexpr int nw = HD >> 6;
     __shared__ float wts[kAttnMaxSplits];
-    __shared__ float red[2][2];
-    const int h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6, nw = HD >> 6;
+    __shared__ float red[2][nw];
+    const int h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
     const int g = h / R, i = h % R;
     const int stride = R * (HD + 2) * 4;  // bytes from one split's partial of row i to the next
     const __amdgpu_buffer_rsrc_t r =
@@ -393,12 +395,16 @@ __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ 
 // the combine pass over R rows per kv head (nothing to do for one split)
 static void launch_combine(const AttnParams& p, int S, int G, int R, hipStream_t st) {
     const dim3 grid((unsigned)(p.n_kv * R)), block((unsigned)p.head_dim);
-    if (S > 1 && S <= 16)
-        hipLaunchKernelGGL(k_attn_combine<16>, grid, block, 0, st, p.part, p.out, S, G, p.head_dim, R, p.n_heads);
-    else if (S > 16 && S <= 32)
-        hipLaunchKernelGGL(k_attn_combine<32>, grid, block, 0, st, p.part, p.out, S, G, p.head_dim, R, p.n_heads);
-    else if (S > 32)
-        hipLaunchKernelGGL(k_attn_combine<64>, grid, block, 0, st, p.part, p.out, S, G, p.head_dim, R, p.n_heads);
+    if (S <= 1) return;
+    if (p.head_dim == 128) {
+        if (S <= 16) hipLaunchKernelGGL((k_attn_combine<128, 16>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
+        else if (S <= 32) hipLaunchKernelGGL((k_attn_combine<128, 32>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
+        else hipLaunchKernelGGL((k_attn_combine<128, 64>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
+    } else {
+        if (S <= 16) hipLaunchKernelGGL((k_attn_combine<64, 16>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
+        else if (S <= 32) hipLaunchKernelGGL((k_attn_combine<64, 32>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
+        else hipLaunchKernelGGL((k_attn_combine<64, 64>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
+    }
 }
 
 // ---------------------------------------------------------------- batches
