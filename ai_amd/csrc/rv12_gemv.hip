@@ -457,18 +457,20 @@ __global__ __launch_bounds__(kPickThreads) void k_pick(const float* __restrict__
     const int32_t* it = ix ? ix + (int64_t)t * stride : nullptr;
     float bv = -__builtin_inff();
     int bi = 0x7FFFFFFF;
-    // four independent loads per thread in flight per round
-    for (int64_t i0 = lo + threadIdx.x; i0 < hi; i0 += 4 * (int64_t)kPickThreads) {
-        float a[4];
-        int ai[4];
+    // eight independent loads per thread in flight per round: a chunk of
+    // kPickChunk entries takes one memory round trip
+    static_assert(kPickChunk <= 8 * kPickThreads, "one round per chunk");
+    for (int64_t i0 = lo + threadIdx.x; i0 < hi; i0 += 8 * (int64_t)kPickThreads) {
+        float a[8];
+        int ai[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < 8; ++u) {
             const int64_t i = i0 + (int64_t)u * kPickThreads;
             a[u] = i < hi ? vt[i] : -__builtin_inff();
             ai[u] = i < hi ? (it ? it[i] : (int)i) : 0x7FFFFFFF;
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < 8; ++u)
             if (pick_beats(a[u], ai[u], bv, bi)) {
                 bv = a[u];
                 bi = ai[u];
@@ -528,7 +530,33 @@ __global__ __launch_bounds__(256) void k_decode_advance(const int64_t* __restric
                                                         int64_t* __restrict__ pos, int64_t* __restrict__ tok) {
     const int64_t id = ids[0];
     const uint16_t* row = emb + min(max(id, (int64_t)0), vocab - 1) * (int64_t)hidden;
-    for (int k = threadIdx.x; k < hidden; k += blockDim.x) x[k] = __uint_as_float((uint32_t)row[k] << 16);
+    if (((uintptr_t)row & 15u) == 0 && ((uintptr_t)x & 15u) == 0 && hidden % 8 == 0) {
+        // 8 values per 16-byte load, four loads per thread in flight before
+        // the first store (one memory round trip for hidden <= 8192)
+        const int ng = hidden / 8;
+        for (int g0 = threadIdx.x; g0 < ng; g0 += 4 * (int)blockDim.x) {
+            uint4 w[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int gi = g0 + u * (int)blockDim.x;
+                w[u] = gi < ng ? reinterpret_cast<const uint4*>(row)[gi] : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int gi = g0 + u * (int)blockDim.x;
+                if (gi < ng) {
+                    const uint32_t c[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+                    float4* o = reinterpret_cast<float4*>(x) + 2 * (int64_t)gi;
+                    o[0] = make_float4(__uint_as_float(c[0] << 16), __uint_as_float(c[0] & 0xFFFF0000u),
+                                       __uint_as_float(c[1] << 16), __uint_as_float(c[1] & 0xFFFF0000u));
+                    o[1] = make_float4(__uint_as_float(c[2] << 16), __uint_as_float(c[2] & 0xFFFF0000u),
+                                       __uint_as_float(c[3] << 16), __uint_as_float(c[3] & 0xFFFF0000u));
+                }
+            }
+        }
+    } else {
+        for (int k = threadIdx.x; k < hidden; k += blockDim.x) x[k] = __uint_as_float((uint32_t)row[k] << 16);
+    }
     if (threadIdx.x == 0) {
         const int64_t s = *steps;
         if (s >= 0 && s < out_len) out[s] = id;

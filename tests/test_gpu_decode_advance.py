@@ -47,3 +47,23 @@ def test_decode_advance_records_embeds_and_counts():
     assert _call(ids, emb, x, out, steps, pos, tok, out_len=2) == 0  # out_len bounds the write
     torch.cuda.synchronize()
     assert out.tolist() == [-5, -5, -5, 417, -5, -5, -5, -5] and torch.equal(x[0], emb[5].float())
+
+
+@pytest.mark.parametrize("H", [1024, 1004, 10240, 12])
+def test_decode_advance_row_widths(H):
+    """The embedding row copy at widths that take the 16-byte path (1024,
+    10240: more than one round of loads per thread) and the element path
+    (1004 and 12: rows not 16-byte aligned); nothing past the row is written."""
+    g = torch.Generator(device="cuda").manual_seed(H)
+    V = 64
+    emb = torch.randn(V, H, device="cuda", generator=g).bfloat16()
+    x = torch.full((H + 8,), 7.0, device="cuda")
+    out = torch.full((4,), -5, dtype=torch.long, device="cuda")
+    steps = torch.tensor([0], dtype=torch.long, device="cuda")
+    pos = torch.tensor([0], dtype=torch.long, device="cuda")
+    for i, tid in enumerate((37, 1, V - 1)):
+        ids = torch.tensor([tid], dtype=torch.long, device="cuda")
+        assert _call(ids, emb, x, out, steps, pos, None) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(x[:H], emb[tid].float()) and torch.all(x[H:] == 7.0)
+        assert out[i].item() == tid and steps.item() == i + 1 and pos.item() == i + 1
