@@ -161,6 +161,31 @@ def test_qwen3_32b_architecture_2_layers_4096_prompt_and_8_token_pass():
     torch.cuda.empty_cache()
 
 
+def test_qwen3_32b_full_depth_512_prompt_and_8_token_pass_cpu_oracle():
+    """Qwen3-32B architecture at full depth (64 layers, 48 GB of 12-bit
+    weights held in HBM, the 151936 x 5120 head), random init: 512-token
+    random prompt through the blocked prefill, bf16 KV cache, the first 16
+    greedy ids equal to the fp32 oracle's, which runs on the CPU (the prompt
+    is shorter than the benchmark's 4096 so that the oracle finishes in about
+    a minute; the 2-layer test above covers the 4096-position attention);
+    then one 8-token batch pass picks the same ids as 8 single-token steps."""
+    from ai_amd.model import QWEN3, RandomCkpt
+    print("qwen3-32b full depth, oracle on the cpu", flush=True)
+    ck = RandomCkpt(QWEN3["32b"], seed=0)
+    P = 512
+    prompt = [int(t) for t in np.random.default_rng(0).integers(0, ck.V, P)]
+    ids, eng = _check(ck, prompt, 16, kv_dtype=torch.bfloat16, maxt=P + 128 + 8, prefill="blocked",
+                      prefill_min=256, keep=True)
+    eng.reset()
+    first = eng.prefill(prompt).tolist()
+    assert first == ids[:1]
+    got = eng.process(ids[:8], P)
+    print("8-token pass", got, "single steps", ids[1:9], flush=True)
+    assert got == ids[1:9]
+    del eng
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.skip(reason=OFF_GPU)
 def test_qwen3_32b_4096_prompt_and_8_token_pass():
     """Qwen3-32B architecture, random init, held in HBM: 4096-token random
