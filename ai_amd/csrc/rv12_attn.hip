@@ -86,15 +86,30 @@ __device__ __forceinline__ float wave_max(float v) {
 // RMSNorm (weight pair wa, wb) and rotate-half RoPE (cos c, sin sn) of one
 // head held by one wave: lane l < HD/2 holds the pair (a, b) = (x[l], x[l + HD/2])
 // (the other lanes hold zeros), so the whole transform needs no barrier.
-template <int HD>
+// BF16: the results are rounded to bf16 (the cache dtype of the step's key);
+// a non-null crow (the key's cache row, bf16 or float32) receives them too.
+template <int HD, bool BF16 = false>
 __device__ __forceinline__ void norm_rope_wave(float a, float b, float wa, float wb, float c, float sn, float eps,
-                                               float* dst, int lane) {
+                                               float* dst, int lane, void* crow = nullptr) {
     constexpr int half = HD / 2;
     const float rs = 1.0f / sqrtf(wave_sum(a * a + b * b) / (float)HD + eps);
     if (lane < half) {
         const float x = wa * (a * rs), y = wb * (b * rs);
-        dst[lane] = x * c - y * sn;
-        dst[lane + half] = y * c + x * sn;
+        float o0 = x * c - y * sn, o1 = y * c + x * sn;
+        if constexpr (BF16) {
+            const uint16_t b0 = f2bf16(o0), b1 = f2bf16(o1);
+            o0 = bf16f(b0);
+            o1 = bf16f(b1);
+            if (crow) {
+                static_cast<uint16_t*>(crow)[lane] = b0;
+                static_cast<uint16_t*>(crow)[lane + half] = b1;
+            }
+        } else if (crow) {
+            static_cast<float*>(crow)[lane] = o0;
+            static_cast<float*>(crow)[lane + half] = o1;
+        }
+        dst[lane] = o0;
+        dst[lane + half] = o1;
     }
 }
 
@@ -184,24 +199,23 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
         const int i = wave + j * NW;
-        if (i < G) norm_rope_wave<HD>(qa[j], qb[j], wqa, wqb, cs, sn, p.eps, qs + i * HD, lane);
-        else if (i == G) norm_rope_wave<HD>(qa[j], qb[j], wka, wkb, cs, sn, p.eps, kn, lane);
-    }
-    if (t < HD) vn[t] = vown;
-    __syncthreads();
-    if (t < HD) {
-        if constexpr (BF16) {
-            const uint16_t kb = f2bf16(kn[t]), vb = f2bf16(vn[t]);
-            kn[t] = bf16f(kb);
-            vn[t] = bf16f(vb);
-            if (sp == 0) {
-                reinterpret_cast<uint16_t*>(p.kc)[row0 + pos * HD + t] = kb;
-                reinterpret_cast<uint16_t*>(p.vc)[row0 + pos * HD + t] = vb;
-            }
-        } else if (sp == 0) {
-            reinterpret_cast<float*>(p.kc)[row0 + pos * HD + t] = kn[t];
-            reinterpret_cast<float*>(p.vc)[row0 + pos * HD + t] = vn[t];
+        if (i < G) {
+            norm_rope_wave<HD>(qa[j], qb[j], wqa, wqb, cs, sn, p.eps, qs + i * HD, lane);
+        } else if (i == G) {  // k, rounded to the cache dtype; split 0 writes it at pos
+            void* krow = sp == 0 ? static_cast<char*>(p.kc) + (row0 + pos * HD) * EB : nullptr;
+            norm_rope_wave<HD, BF16>(qa[j], qb[j], wka, wkb, cs, sn, p.eps, kn, lane, krow);
         }
+    }
+    if (t < HD) {  // v, rounded to the cache dtype; split 0 writes it at pos
+        float v = vown;
+        if constexpr (BF16) {
+            const uint16_t vb = f2bf16(v);
+            v = bf16f(vb);
+            if (sp == 0) reinterpret_cast<uint16_t*>(p.vc)[row0 + pos * HD + t] = vb;
+        } else if (sp == 0) {
+            reinterpret_cast<float*>(p.vc)[row0 + pos * HD + t] = v;
+        }
+        vn[t] = v;
     }
     __syncthreads();
 
@@ -285,8 +299,19 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
     float w[PPG][G];  // the weights (zero beyond the span), read before the first product
 #pragma unroll
     for (int r = 0; r < PPG; ++r) {
+        if constexpr (G % 4 == 0) {  // 16-byte reads: wt is 16-byte aligned (offsets G HD + 2 HD floats)
 #pragma unroll
-        for (int i = 0; i < G; ++i) w[r][i] = wt[(pg * PPG + r) * G + i];
+            for (int i = 0; i < G; i += 4) {
+                const float4 w4 = *reinterpret_cast<const float4*>(wt + (pg * PPG + r) * G + i);
+                w[r][i] = w4.x;
+                w[r][i + 1] = w4.y;
+                w[r][i + 2] = w4.z;
+                w[r][i + 3] = w4.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < G; ++i) w[r][i] = wt[(pg * PPG + r) * G + i];
+        }
     }
 #pragma unroll
     for (int r = 0; r < PPG; ++r) {
