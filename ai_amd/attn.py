@@ -42,12 +42,31 @@ class RopeAttn:
         need = lib().rv12_attn_batch_workspace_bytes(ctypes.byref(self.a), 16)
         self.wsb = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
 
-    def __call__(self, qkv, qn, kn, inv, pos, kc, vc, out):
+    def _check(self, qkv, qn, kn, inv, pos, kc, vc, out, T):
+        """The tensors' dtypes, layouts, sizes and device: the C ABI sees only
+        pointers, so a cache of another dtype or shape than this object's
+        would be written out of bounds."""
+        a = self.a
         for t in (qkv, qn, kn, inv, out):
             if t.dtype != torch.float32 or not t.is_contiguous():
                 raise ValueError("qkv, qn, kn, inv and out must be contiguous float32")
-        if pos.dtype != torch.int64:
+        if pos.dtype != torch.int64 or pos.numel() < 1:
             raise ValueError("pos must be int64")
+        dev = qkv.device
+        if any(t.device != dev for t in (qn, kn, inv, pos, kc, vc, out)):
+            raise ValueError("every tensor must be on the device of qkv")
+        if qkv.numel() < T * (a.n_heads + 2 * a.n_kv) * a.head_dim or out.numel() < T * a.n_heads * a.head_dim:
+            raise ValueError(f"qkv and out need {T} rows")
+        if qn.numel() < a.head_dim or kn.numel() < a.head_dim or inv.numel() < a.head_dim // 2:
+            raise ValueError("qn, kn need head_dim entries and inv head_dim / 2")
+        want = torch.bfloat16 if a.kv_bf16 else torch.float32
+        for c in (kc, vc):
+            if c.dtype != want or not c.is_contiguous() or tuple(c.shape) != (a.n_kv, a.maxt, a.head_dim):
+                raise ValueError(f"kc and vc must be contiguous {want} caches of shape "
+                                 f"({a.n_kv}, {a.maxt}, {a.head_dim})")
+
+    def __call__(self, qkv, qn, kn, inv, pos, kc, vc, out):
+        self._check(qkv, qn, kn, inv, pos, kc, vc, out, 1)
         p = lambda t: ctypes.c_void_p(t.data_ptr())
         rc = lib().rv12_rope_attn(ctypes.byref(self.a), p(qkv), p(qn), p(kn), p(inv), p(pos), p(kc), p(vc), p(out),
                                   p(self.ws), self.ws.numel(),
@@ -57,11 +76,7 @@ class RopeAttn:
     def batch(self, qkv, qn, kn, inv, pos, kc, vc, out, T):
         """T <= 16 tokens at positions pos .. pos + T - 1: rows of qkv in, rows
         of out written; K/V of the T positions into the caches."""
-        for t in (qkv, qn, kn, inv, out):
-            if t.dtype != torch.float32 or not t.is_contiguous():
-                raise ValueError("qkv, qn, kn, inv and out must be contiguous float32")
-        if pos.dtype != torch.int64:
-            raise ValueError("pos must be int64")
+        self._check(qkv, qn, kn, inv, pos, kc, vc, out, int(T))
         p = lambda t: ctypes.c_void_p(t.data_ptr())
         rc = lib().rv12_rope_attn_batch(ctypes.byref(self.a), int(T), p(qkv), p(qn), p(kn), p(inv), p(pos), p(kc),
                                         p(vc), p(out), p(self.wsb), self.wsb.numel(),
@@ -73,11 +88,7 @@ class RopeAttn:
         device int64): rows of qkv in, rows of out written; K/V of the T
         positions into the caches.  The q rows live in a workspace kept for
         the largest T seen."""
-        for t in (qkv, qn, kn, inv, out):
-            if t.dtype != torch.float32 or not t.is_contiguous():
-                raise ValueError("qkv, qn, kn, inv and out must be contiguous float32")
-        if pos.dtype != torch.int64:
-            raise ValueError("pos must be int64")
+        self._check(qkv, qn, kn, inv, pos, kc, vc, out, int(T))
         L = lib()
         need = L.rv12_prefill_attn_workspace_bytes(ctypes.byref(self.a), int(T))
         if need == 0:

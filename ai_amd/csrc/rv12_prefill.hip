@@ -387,7 +387,9 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill_mm(const uint32_t* __res
                 for (int c = 0; c < kPfWT; ++c) ng[j][c] = xc[c * 16];
             }
         };
-        fetch(e_lo);
+        // no entry for these rows (n_exc = 0 included, where er / ec / ev may
+        // be null): nothing is fetched, so no index below e_lo is formed
+        if (e_lo < e_hi) fetch(e_lo);
         for (int32_t e0 = e_lo; e0 < e_hi; e0 += EB) {
             int rr[EB];
             bool rin[EB];

@@ -68,10 +68,15 @@ class Engine:
               RAMVI_PREFILL_MIN_TOKENS, 256)
     stream_layers  the last n layers live in pinned host memory and are
               streamed through `slots` HBM slots every pass (ai_amd.stream)
+    tune      measure the launch shapes of the four layer linears on this
+              device first (ai_amd.tune, cached per library and device), with
+              the prologues the engine runs them with: the RMSNorm for qkv and
+              gu, silu(g) * u for down (the reference tunes at load,
+              core/engine.py:207-208)
     """
 
     def __init__(self, ck, maxt=2048, kv_dtype=torch.float32, device="cuda", log=None, prefill=None,
-                 prefill_min=None, stream_layers=0, slots=2):
+                 prefill_min=None, stream_layers=0, slots=2, tune=False):
         if prefill is None:
             blocked_prefill.enabled()  # validates RAMVI_PREFILL
             prefill = os.environ.get("RAMVI_PREFILL", "legacy")
@@ -87,6 +92,11 @@ class Engine:
         self.V, self.maxt, self.kv_dtype = ck.V, maxt, kv_dtype
         dev = self.dev = torch.device(device)
         H, KV, HD = self.H, self.KV, self.HD
+        if tune:
+            from . import tune as tuner
+            P = ck.layer_params()
+            tuner.tune([(*P["qkv"], 0, True), (*P["o"], 1), (*P["gu"], 0, True), (*P["down"], 2)],
+                       log=log or (lambda *a: None))
         self.inv = (1.0 / (ck.theta ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)  # engine.py:204
         self.emb = ck.t("model.embed_tokens.weight", dev)
         if not 0 <= stream_layers <= self.L:
@@ -120,6 +130,7 @@ class Engine:
         self.attn = RopeAttn(H, KV, HD, maxt, kv_dtype, self.eps, dev)
         self.graph = None
         self.pgraph = None  # a full prefill chunk of BATCH tokens
+        self.tgraphs = {}   # T -> graph of one pass of T <= BATCH tokens (process)
 
     # ---------------------------------------------------------------- layers
     def _rope_attn(self, l, T, p0=None):
@@ -300,32 +311,47 @@ class Engine:
             return self.nxt[:1].tolist()
         self.pos.fill_(pos0)
         self.tok[:T].copy_(t)
+        self._pass_graph(T).replay()
+        self.pos.fill_(pos0 + T)
+        return self.nxt[:T].tolist()
+
+    def _pass(self, T):
+        """One pass of T <= 16 tokens (tokens in self.tok, first position in
+        self.pos, both on the device): embedding rows, every layer, the greedy
+        id after each token into self.nxt[:T]."""
         self._embed(T)
-        self._layers(self.xb[:T], T, pos0)
+        self._layers(self.xb[:T], T)
         if T == 1:
             self._head_row(self.xb[:1])
         else:
             self._head_rows(self.xb[:T], T)
-        self.pos.fill_(pos0 + T)
-        return self.nxt[:T].tolist()
 
-    def batch_pass_ms(self, T, p0, reps=10):
-        """ms of one pass of T tokens of one sequence through every layer (the
-        reference's _batch_layer, engine.py:344-356) at positions p0..p0+T-1,
-        replayed from a HIP graph (each replay rewrites those cache slots)."""
+    def _pass_graph(self, T):
+        """The HIP graph of a T-token pass, recorded on first use (the
+        reference captures one graph per pass size on first use and replays
+        it, engine.py:31, 393-444).  Recording runs the pass eagerly twice
+        with the current tokens and position; a pass writes its own cache
+        slots only, so those warm runs leave what the replay then writes."""
+        g = self.tgraphs.get(T)
+        if g is None:
+            g = self.tgraphs[T] = self._record(lambda: self._pass(T))
+        return g
+
+    def batch_pass_ms(self, T, p0, tokens=None, reps=10):
+        """ms per call of process() with T tokens of one sequence at positions
+        p0..p0+T-1 (the reference's _batch_layer, engine.py:344-356, replayed
+        from the pass's graph), the host's part of each call included (token
+        upload, graph launch, reading the ids back); tokens default to the
+        first T ids of the vocabulary."""
         if not 1 < T <= BATCH or p0 + T > self.maxt:
             raise ValueError("T must be in 2..16 and the pass must fit the context")
-
-        def body():
-            self._embed(T)
-            self._layers(self.xb[:T], T)
-
-        self.pos.fill_(p0)
-        g = self._record(body)
+        toks = list(tokens) if tokens is not None else list(range(T))
+        self.process(toks, p0)  # records the graph on first use
+        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(reps):
-            g.replay()
+            self.process(toks, p0)
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps

@@ -5,6 +5,12 @@ launch space (rv12_launch: kernel, row blocks, waves, K splits) and stores the
 fastest shape in `wcomp.CFG1` (one token, the decode step) and `wcomp.CFGT`
 (16 tokens, the batched pass), in the reference's value format
 (ramvi/engine/ramvi_engine/kernels/wcomp.py:115, 222: (BN, w) or (BN, w, S)).
+A shape may carry a fourth entry, rms: True times every candidate with the
+RMSNorm prologue the engine fuses into that linear (a bf16 weight vector),
+since the prologue moves the best launch shape; MODE 2 is always timed with
+its silu(g) * u prologue.  The engine tunes its four layer linears with the
+prologues it runs them with (Engine(tune=True), as the reference's engine
+does at load, core/engine.py:207-208).
 
 Measurement.  The MI355X keeps 256 MB in its memory-side cache, more than any
 single Qwen3 matrix, so a shape is timed over distinct matrices that together
@@ -78,9 +84,10 @@ def as_reference_cfg(shape):
     return (bn, waves, splits)
 
 
-def _measure(N, K, mode, T, shapes, min_bytes, reps):
+def _measure(N, K, mode, T, shapes, min_bytes, reps, rms=False):
     """us per launch of every shape (inf where it fails or disagrees with the
-    built-in shape's output), over distinct random matrices of > min_bytes."""
+    built-in shape's output), over distinct random matrices of > min_bytes;
+    rms: with the RMSNorm prologue (a bf16 weight vector of K entries)."""
     import ctypes
 
     import torch
@@ -96,6 +103,7 @@ def _measure(N, K, mode, T, shapes, min_bytes, reps):
     xs = 2 * K if mode == 2 else K
     x = torch.randn(T, xs, device=dev, generator=g).bfloat16().float()
     y = torch.zeros(T, N, device=dev)
+    lnw = (torch.rand(K, device=dev, generator=g) + 0.5).bfloat16() if rms else None
     st = torch.cuda.current_stream()
     mstructs = [wcomp._matrix(c) for c in mats]
     times, ref = {}, None
@@ -107,7 +115,8 @@ def _measure(N, K, mode, T, shapes, min_bytes, reps):
 
         def launches():
             for m in mstructs:
-                rc = L.rv12_gemm(ctypes.byref(m), p(x), p(y), T, None, 1e-6, mode, ctypes.byref(cfg), p(ws), need,
+                rc = L.rv12_gemm(ctypes.byref(m), p(x), p(y), T, None if lnw is None else p(lnw), 1e-6, mode,
+                                 ctypes.byref(cfg), p(ws), need,
                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
                 if rc:
                     raise ValueError(_lib.strerror(rc))
@@ -163,28 +172,34 @@ def _write(path, d):
     os.replace(tmp, path)
 
 
+def _key(N, K, mode, rms):
+    return f"{N}x{K}|{mode}" + ("|rms" if rms else "")
+
+
 def tune(shapes, log=print, cache=None, min_bytes=1 << 30, reps=10):
-    """Fill wcomp.CFG1 / CFGT for every (N, K, MODE) in shapes, from the cache
-    where it holds this library and device, else by measurement."""
+    """Fill wcomp.CFG1 / CFGT for every (N, K, MODE) or (N, K, MODE, rms) in
+    shapes, from the cache where it holds this library and device, else by
+    measurement (with the RMSNorm prologue where rms is true)."""
     path = cache or CACHE
     stored = _read(path, log)
     ident = _identity()
     entries = dict(stored["entries"]) if stored and stored.get("identity") == ident else {}
     changed = False
-    for N, K, mode in shapes:
-        key = f"{N}x{K}|{mode}"
+    shapes = [tuple(s) + (False,) * (4 - len(s)) for s in shapes]
+    for N, K, mode, rms in shapes:
+        key = _key(N, K, mode, rms)
         e = entries.get(key)
         if e is None:
             e = {}
             for name, T in TOKENS.items():
                 shp = candidates(N, K, T)
-                t = _measure(N, K, mode, T, shp, min_bytes, reps) if shp else {}
+                t = _measure(N, K, mode, T, shp, min_bytes, reps, rms=bool(rms)) if shp else {}
                 good = {s: v for s, v in t.items() if math.isfinite(v)}
                 if not good:
                     raise RuntimeError(f"tune: no launch shape runs for {N}x{K} mode {mode} at {T} tokens")
                 best = min(good, key=good.get)
                 e[name] = list(best)
-                log(f"tune: {N}x{K} mode {mode} {T} tok: {best} {good[best]:.2f} us "
+                log(f"tune: {N}x{K} mode {mode}{' rms' if rms else ''} {T} tok: {best} {good[best]:.2f} us "
                     f"(built-in {t.get(shp[0], float('inf')):.2f} us)")
             entries[key] = e
             changed = True
@@ -192,4 +207,4 @@ def tune(shapes, log=print, cache=None, min_bytes=1 << 30, reps=10):
         wcomp.CFGT[(N, K, mode)] = as_reference_cfg(tuple(e["batch"]))
     if changed:
         _write(path, {"identity": ident, "entries": entries})
-    return {k: entries[f"{k[0]}x{k[1]}|{k[2]}"] for k in shapes}
+    return {k[:3] if not k[3] else k: entries[_key(*k)] for k in shapes}

@@ -15,12 +15,24 @@ an engine with a cache of that dtype stores them
 (ramvi/engine/ramvi_engine/kernels/tkernels.py:187-190; the reference's
 validation oracle rounds to its fp16 cache the same way).
 
-device: where the float32 forward runs ("cpu" by default).  The large
-architectures (Qwen3-8B over a 2k-token prompt, Qwen3-32B over 4k) run it on
-the GPU with torch's float32 matrix products (IEEE float32 products and
-sums, no reduced-precision inputs) so that the check fits a test's time.
+device: where the float32 forward runs.  Only "cpu" is accepted: the oracle
+runs on the host, apart from the GPU code it checks.  Token ids and picks are
+range-checked on the host before any indexing.
 """
 import torch
+
+
+def _host(device):
+    dev = torch.device(device)
+    if dev.type != "cpu":
+        raise ValueError("the oracle runs on the CPU only (device must be 'cpu')")
+    return dev
+
+
+def _ids_in_range(ids, V, what):
+    bad = [i for i in ids if not 0 <= int(i) < V]
+    if bad:
+        raise ValueError(f"{what} outside [0, {V}): {bad[:8]}")
 
 
 def rms(x, w, eps):
@@ -38,7 +50,8 @@ def hidden(ck, tokens, kv_dtype=torch.float32, rotate=rotate_half, device="cpu")
     (reference.py:26-51)."""
     H, KV, HD, eps, F = ck.H, ck.KV, ck.HD, ck.eps, ck.FF
     T = len(tokens)
-    dev = torch.device(device)
+    dev = _host(device)
+    _ids_in_range(tokens, ck.V, "tokens")
     emb = ck.t("model.embed_tokens.weight", dev)
     x = emb[torch.tensor(tokens, device=dev)].float()
     del emb
@@ -92,6 +105,10 @@ def argmax(ck, tokens, kv_dtype=torch.float32, head_chunk=16384, margins=False, 
     best = torch.full((T,), -float("inf"), device=dev)
     second = torch.full((T,), -float("inf"), device=dev)
     arg = torch.zeros(T, dtype=torch.long, device=dev)
+    if picks is not None:
+        if len(picks) != T:
+            raise ValueError(f"picks must hold one id per position from first on ({T})")
+        _ids_in_range(picks, head.shape[0], "picks")
     pk = None if picks is None else torch.tensor(picks, dtype=torch.long, device=dev)
     pick_logit = torch.zeros(T, device=dev)
     for i in range(0, head.shape[0], head_chunk):

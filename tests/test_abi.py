@@ -357,3 +357,33 @@ def test_decode_advance_argument_errors():
     assert call(out_len=-1) == _lib.RV12_E_SHAPE
     for k in ("ids", "out", "steps", "pos", "tok", "x"):
         assert call(odd=(k,)) == _lib.RV12_E_ALIGN, k
+
+
+def test_attention_wrapper_checks_the_caches():
+    """RopeAttn rejects caches of another dtype, shape or layout than the one
+    it was built for, and rows too few for T, before any library call (the
+    C ABI sees only pointers, so such a cache would be written out of
+    bounds).  CPU tensors: every case raises before a launch."""
+    import torch
+    from ai_amd.attn import RopeAttn
+    H, KV, HD, maxt = 4, 2, 64, 96
+    f32 = lambda *s: torch.zeros(*s, dtype=torch.float32)
+    qkv, qn, kn, inv, out = f32((H + 2 * KV) * HD), f32(HD), f32(HD), f32(HD // 2), f32(H * HD)
+    pos = torch.zeros(1, dtype=torch.int64)
+    for kv_dtype, other in ((torch.bfloat16, torch.float32), (torch.float32, torch.bfloat16)):
+        a = RopeAttn(H, KV, HD, maxt, kv_dtype, 1e-6, "cpu")
+        good = torch.zeros(KV, maxt, HD, dtype=kv_dtype)
+        cases = [torch.zeros(KV, maxt, HD, dtype=other), torch.zeros(KV, maxt - 1, HD, dtype=kv_dtype),
+                 torch.zeros(KV + 1, maxt, HD, dtype=kv_dtype),
+                 torch.zeros(KV, HD, maxt, dtype=kv_dtype).transpose(1, 2)]
+        for bad in cases:
+            with pytest.raises(ValueError, match="kc and vc"):
+                a(qkv, qn, kn, inv, pos, bad, good, out)
+            with pytest.raises(ValueError, match="kc and vc"):
+                a.batch(qkv.repeat(2), qn, kn, inv, pos, good, bad, out.repeat(2), 2)
+            with pytest.raises(ValueError, match="kc and vc"):
+                a.prefill(qkv.repeat(2), qn, kn, inv, pos, bad, good, out.repeat(2), 2)
+        with pytest.raises(ValueError, match="rows"):
+            a.batch(qkv, qn, kn, inv, pos, good, good, out, 2)
+        with pytest.raises(ValueError, match="int64"):
+            a(qkv, qn, kn, inv, pos.int(), good, good, out)

@@ -69,8 +69,8 @@ def _run(c_gpu, X, Y0, mode, T, lnw=None, BN=None, w=None, S=None, eps=1e-6, use
                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "rv12_gemm")
     elif T == 1 and not use_tc:
         wcomp.gemvc1(x, c_gpu, y, mode, BN=BN, w=w, lnw=ln, eps=eps)
-    elif ln is not None:  # the C-ABI's RMS prologue at T > 1 (no reference operator has it)
-        wcomp._linear(x, c_gpu, y, mode, T, BN, w, S, ln, eps, "rv12_gemm")
+    elif ln is not None:  # the RMS prologue at T > 1 (an addition to the reference's gemvc_tc)
+        wcomp.gemvc_tc(x, c_gpu, y, mode, T, BN=BN, w=w, S=S, lnw=ln, eps=eps)
     else:
         wcomp.gemvc_tc(x, c_gpu, y, mode, T, BN=BN, w=w, S=S)
     torch.cuda.synchronize()
@@ -244,18 +244,26 @@ def test_default_launch_shape_families(N, K, shape1, shape2):
 
 def test_tuned_launch_shapes_keep_parity(tmp_path):
     """tune() fills CFG1 / CFGT on the GPU; the linears then run with those
-    launch shapes and still match the closed form."""
+    launch shapes and still match the closed form: a plain MODE 0 shape,
+    MODE 2 (timed with its silu(g) * u prologue) and a MODE 0 shape timed with
+    the RMSNorm prologue the engine fuses into qkv and gu, run with it."""
     from ai_amd import tune, wcomp
     N, K = 1024, 1024
-    tune.tune([(N, K, 0), (N, K, 2)], log=lambda *a: None, cache=str(tmp_path / "tune.json"))
+    Nr = 2048
+    tune.tune([(N, K, 0), (N, K, 2), (Nr, K, 0, True)], log=lambda *a: None, cache=str(tmp_path / "tune.json"))
     try:
-        assert (N, K, 0) in wcomp.CFG1 and (N, K, 2) in wcomp.CFGT
+        assert (N, K, 0) in wcomp.CFG1 and (N, K, 2) in wcomp.CFGT and (Nr, K, 0) in wcomp.CFG1
         bits = _random_matrix(N, K, 5, out_rows=0.01)
         cnp = codec.compress(bits)
         cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
         for mode in (0, 2):
             _check(cnp, cg, 1, mode, False, 21)
             _check(cnp, cg, 16, mode, False, 22, use_tc=True)
+        bits = _random_matrix(Nr, K, 6, out_rows=0.01)
+        cnp = codec.compress(bits)
+        cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+        _check(cnp, cg, 1, 0, True, 23)
+        _check(cnp, cg, 16, 0, True, 24, use_tc=True)
     finally:
         wcomp.CFG1.clear()
         wcomp.CFGT.clear()

@@ -110,3 +110,59 @@ def test_decode_attention_addresses(model):
         R = 16 * G
         assert ((KV - 1) * S + S - 1) * R * (HD + 2) + R * (HD + 2) - 1 < KV * S * R * (HD + 2)
         assert (S - 1) * R * (HD + 2) * 4 + (HD + 2) * 4 < U32
+
+
+def _prefill_exception_reads(rp, N, blk0, wb=4, eb=8):
+    """The exception-list indices k_prefill_mm's epilogue (rv12_prefill.hip,
+    step (b)) reads for the row tile starting at row block blk0: the entries
+    [e_lo, e_hi) of rows blk0*16 .. +16 wb, fetched eb at a time with each
+    index clamped to e_hi - 1, the first batch only when the range is not
+    empty, the next one only while it starts below e_hi."""
+    rlo = blk0 * 16
+    if rlo >= N:
+        return []
+    e_lo, e_hi = rp[rlo], rp[min(rlo + 16 * wb, N)]
+    reads = []
+
+    def fetch(e0):
+        reads.extend(min(e0 + j, e_hi - 1) for j in range(eb))
+
+    if e_lo < e_hi:
+        fetch(e_lo)
+    e0 = e_lo
+    while e0 < e_hi:
+        if e0 + eb < e_hi:
+            fetch(e0 + eb)
+        e0 += eb
+    return reads
+
+
+@pytest.mark.parametrize("case", ["no_exceptions", "first_tile_empty", "last_tile_only", "dense"])
+def test_prefill_exception_epilogue_reads_inside_the_list(case):
+    """Every exception entry the prefill GEMM's epilogue reads lies inside
+    [e_lo, e_hi) of its row tile, so inside the list: with no exceptions at
+    all (the list may be a null pointer) nothing is read, and a row tile with
+    no entries before or inside it reads nothing (the first fetch is guarded)."""
+    import numpy as np
+    N = 1000
+    per_row = np.zeros(N, np.int64)
+    if case == "first_tile_empty":
+        per_row[64:] = 1
+    elif case == "last_tile_only":
+        per_row[-3:] = 5
+    elif case == "dense":
+        per_row[:] = np.random.default_rng(0).integers(0, 20, N)
+    rp = np.concatenate([[0], np.cumsum(per_row)]).tolist()
+    n_exc = rp[-1]
+    nblk = (N + 15) // 16
+    total = 0
+    for blk0 in range(0, nblk, 4):
+        reads = _prefill_exception_reads(rp, N, blk0)
+        rlo = blk0 * 16
+        e_lo, e_hi = rp[rlo], rp[min(rlo + 64, N)]
+        assert all(e_lo <= e < e_hi for e in reads), (case, blk0)
+        assert all(0 <= e < n_exc for e in reads)
+        if e_lo == e_hi:
+            assert not reads
+        total += len(set(reads))
+    assert total == n_exc  # every entry is read, each tile its own

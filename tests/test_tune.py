@@ -25,7 +25,7 @@ def fake(monkeypatch):
 def test_unreadable_cache_ignored_and_failures_not_cached(fake, tmp_path):
     p = tmp_path / "tune.json"
     p.write_text("{bad")
-    fake.setattr(tune, "_measure", lambda N, K, mode, T, shp, mb, reps: {s: float("inf") for s in shp})
+    fake.setattr(tune, "_measure", lambda N, K, mode, T, shp, mb, reps, rms=False: {s: float("inf") for s in shp})
     logs = []
     tune.tune([], log=logs.append, cache=str(p))
     assert logs and "ignoring" in logs[0]
@@ -38,7 +38,7 @@ def test_fastest_shape_cached_and_read_back(fake, tmp_path):
     p = tmp_path / "tune.json"
     calls = []
 
-    def measure(N, K, mode, T, shp, mb, reps):
+    def measure(N, K, mode, T, shp, mb, reps, rms=False):
         calls.append(T)
         # the last candidate is the fastest; a failing one never wins
         return {s: (float("inf") if i == 0 else 10.0 - i) for i, s in enumerate(shp)}
@@ -65,3 +65,27 @@ def test_reference_cfg_maps_back_to_the_shape():
         bn, w, s = tune.as_reference_cfg(shape)
         c = wcomp._launch(bn, w, s, T)
         assert (c.kernel, c.rb, c.waves, c.splits) == shape
+
+
+def test_rms_shapes_measured_with_the_prologue_and_cached_apart(fake, tmp_path):
+    """A shape with rms=True is timed with the RMSNorm prologue and cached
+    under its own key; the plain shape of the same (N, K, MODE) is another
+    entry."""
+    p = tmp_path / "tune.json"
+    seen = []
+
+    def measure(N, K, mode, T, shp, mb, reps, rms=False):
+        seen.append((N, K, mode, T, rms))
+        return {s: 10.0 - i for i, s in enumerate(shp)}
+
+    fake.setattr(tune, "_measure", measure)
+    out = tune.tune([(6144, 4096, 0, True), (4096, 12288, 2)], log=lambda *a: None, cache=str(p))
+    assert (6144, 4096, 0, True, 1) in [s[:3] + (s[4], s[3]) for s in seen]
+    assert all(r for N, K, m, T, r in seen if N == 6144) and not any(r for N, K, m, T, r in seen if N == 4096)
+    d = json.loads(p.read_text())
+    assert set(d["entries"]) == {"6144x4096|0|rms", "4096x12288|2"}
+    assert (6144, 4096, 0, True) in out and (4096, 12288, 2) in out
+    n = len(seen)
+    tune.tune([(6144, 4096, 0)], log=lambda *a: None, cache=str(p))  # the plain shape is measured on its own
+    assert len(seen) > n
+    assert set(json.loads(p.read_text())["entries"]) == {"6144x4096|0|rms", "4096x12288|2", "6144x4096|0"}
