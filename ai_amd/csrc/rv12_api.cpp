@@ -25,8 +25,8 @@ struct Shape {
 
 bool shape_fits(int K, int T, const Shape& c) {
     if (c.kernel == 1) return T <= kMaxVectorTokens && gemv_fits(K, T, c.rb, c.waves, c.splits);
-    // MFMA: each thread stages at most 4 B-operand groups of the split's steps
-    return split_steps(K, c.splits) <= 4 * c.waves && gemm_fits(K, c.rb, c.waves, c.splits);
+    // MFMA: the split's staged activations (sized by the token columns) fit the LDS
+    return gemm_fits(K, T, c.rb, c.waves, c.splits);
 }
 
 // Built-in launch shapes, from launch-shape sweeps of the Qwen3-8B / 14B
@@ -78,21 +78,20 @@ Shape vector_shape(int N, int K, int T) {
 // Time model of the MFMA kernel, in us.  A workgroup stages x' for its K
 // split in LDS before streaming, so the launch runs in rounds of one
 // workgroup per CU.  Each round costs a fixed part plus the staging of its
-// split (per K step) plus its weight bytes at the smaller of the HBM rate and
-// a per-CU rate (the bytes one CU keeps in flight over the memory latency); a
-// K split adds the reduce pass, a launch plus a cost per MB of partials.  The
-// constants are fitted to a sweep of every launch shape of the kernel on 16
-// Qwen3-8B/14B/32B shapes at 4, 8 and 16 tokens on MI355X: the model's pick
-// lies within 0.5 % of the measured best on average and 6.6 % at worst
-// (4 % at worst for a shape left out of the fit), where the earlier model
-// (a 5 us prologue per round whatever the split) lost 5.2 % on average and
-// 19 % at worst (Qwen3-8B o 4096x4096 at 16 tokens: 13.4 against 11.3 us).
-constexpr double kModelRoundUs = 1.0;
-constexpr double kModelStepUs = 0.1;
-constexpr double kModelHbmGBs = 7500.0;
+// split (per K step, in proportion to the token columns staged) plus its
+// weight bytes at the smaller of the HBM rate and a per-CU rate (the bytes
+// one CU keeps in flight over the memory latency); a K split adds the reduce
+// pass, a launch plus a cost per MB of partials.  The constants are fitted to
+// a sweep of every launch shape the model considers on 14 Qwen3-8B/14B/32B
+// shapes (RMS and silu prologues as the engine runs them) at 4, 8 and 16
+// tokens on MI355X: the model's pick lies 1.7 % above the measured best on
+// average and 11 % at worst (Qwen3-32B gu at 4 tokens).
+constexpr double kModelRoundUs = 1.5;
+constexpr double kModelStepUs = 0.2;
+constexpr double kModelHbmGBs = 6500.0;
 constexpr double kModelCuGBs = 30.0;
-constexpr double kModelReduceUs = 1.0;
-constexpr double kModelReduceUsPerMB = 2.0;
+constexpr double kModelReduceUs = 0.5;
+constexpr double kModelReduceUsPerMB = 1.0;
 constexpr int kModelCUs = 256;
 constexpr double kModelStepBytes = 768.0;  // one (row block, step) tile
 
@@ -104,7 +103,7 @@ double mfma_model_us(int64_t nblk, int N, int K, int T, int rb, int waves, int s
     double t = 0.0;
     for (int64_t left = wgs; left > 0;) {
         const int64_t n = std::min<int64_t>(left, (int64_t)kModelCUs);
-        t += kModelRoundUs + kModelStepUs * steps +
+        t += kModelRoundUs + kModelStepUs * steps * gemm_tokens(T) / 16.0 +
              (double)n * wg_bytes / (std::min(kModelHbmGBs, (double)n * kModelCuGBs) * 1e3);
         left -= n;
     }
@@ -113,7 +112,7 @@ double mfma_model_us(int64_t nblk, int N, int K, int T, int rb, int waves, int s
 }
 
 // candidates: 1, 2 or 4 row blocks per wave, 4 or 8 waves, the fewest K
-// splits whose staging fits and up to 8 more
+// splits whose staging fits and up to 10 more
 Shape mfma_shape(int N, int K, int T) {
     const int64_t nblk = nblocks(N);
     const int nsteps = K / 32;
@@ -126,11 +125,14 @@ Shape mfma_shape(int N, int K, int T) {
     for (int rb : {1, 2, 4}) {
         for (int w : {4, 8}) {
             const int wv = std::min(w, nsteps);  // no more waves than K steps
-            auto fits = [&](int s) { return split_steps(K, s) <= 4 * wv && gemm_fits(K, rb, wv, s); };
+            // the built-in shapes keep every staged group in registers
+            // (4 per thread: 64 waves / TP steps), so no staging load waits
+            // behind the weight prefetch
+            auto fits = [&](int s) { return split_steps(K, s) <= 64 * wv / gemm_tokens(T) && gemm_fits(K, T, rb, wv, s); };
             int s0 = 1;
             while (s0 < std::min(kMaxSplits, nsteps) && !fits(s0)) ++s0;
             if (!fits(s0)) continue;
-            for (int s = s0; s <= std::min({s0 + 8, kMaxSplits, nsteps}); ++s) {
+            for (int s = s0; s <= std::min({s0 + 10, kMaxSplits, nsteps}); ++s) {
                 if (!fits(s)) continue;
                 const double t = mfma_model_us(nblk, N, K, T, rb, wv, s);
                 if (t < best_t) {

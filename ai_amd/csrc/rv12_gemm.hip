@@ -47,7 +47,7 @@
 namespace rv12 {
 
 
-constexpr int kGroupsPerThread = 4;  // B-operand groups a thread stages; host: steps <= 4 * waves
+constexpr int kGroupsPerThread = 4;  // B-operand groups a thread loads before the weight prefetch
 
 template <int RBW>
 __device__ __forceinline__ void issue_rows(u32x3 (&dst)[RBW], __amdgpu_buffer_rsrc_t rv,
@@ -59,11 +59,14 @@ __device__ __forceinline__ void issue_rows(u32x3 (&dst)[RBW], __amdgpu_buffer_rs
 }
 
 
-// M2: silu(g) * u prologue (MODE 2); LN: RMSNorm weight.  Template arguments,
-// so that the activation loads of step 1 are straight-line code that waits for
-// no kernel argument test.
-template <int RBW, bool M2, bool LN>
+// TP: the token columns staged, 4, 8 or 16 (T <= TP); G = 4 TP B-operand
+// groups per K step (4 k-groups of 8 x TP tokens).  M2: silu(g) * u prologue
+// (MODE 2); LN: RMSNorm weight.  Template arguments, so that the activation
+// loads of step 1 are straight-line code that waits for no kernel argument
+// test, and the group arithmetic is shifts.
+template <int TP, int RBW, bool M2, bool LN>
 __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int T) {
+    constexpr int G = 4 * TP;
     extern __shared__ u32x4 lds4[];
     const int W = blockDim.x >> 6;
     const int nthr = blockDim.x;
@@ -75,6 +78,7 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     const int s_lo = (int)((uint32_t)(sp * nsteps) / (uint32_t)S);
     const int s_hi = (int)((uint32_t)((sp + 1) * nsteps) / (uint32_t)S);
     const int nst = s_hi - s_lo, k_lo = s_lo * 32, krange = nst * 32;
+    const int ngr = nst * G;  // B-operand groups of the split
     const int64_t nblk = (p.N + 15) / 16;
     const int64_t blk0 = (int64_t)blockIdx.x * W * RBW;
     const int n0 = (int)(blk0 * 16);
@@ -82,25 +86,26 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     const int nw = (int)(wblk * 16);        // first row of this wave
     const int nvalid = (int)max((int64_t)0, min((int64_t)RBW, nblk - wblk));
 
-    u32x4* xb = lds4;                                               // [nst][3][64]
-    float* exc = reinterpret_cast<float*>(xb + (size_t)nst * 192);  // [W*RBW*16 rows][16 tokens]
-    float* ssq = exc + W * RBW * 256;                               // [W][16]
-    int* wflag = reinterpret_cast<int*>(ssq + W * 16);              // [W] x' outside the fast path's range
-    int* wexp = wflag + W;                                          // [W][16] slow path: largest exponent
+    u32x4* xb = lds4;                                                  // [nst][3][G]
+    float* exc = reinterpret_cast<float*>(xb + (size_t)nst * 3 * G);  // [W*RBW*16 rows][16 tokens]
+    float* ssq = exc + W * RBW * 256;                                  // [W][16]
+    int* wflag = reinterpret_cast<int*>(ssq + W * 16);                 // [W] x' outside the fast path's range
+    int* wexp = wflag + W;                                             // [W][16] slow path: largest exponent
 
-    // ---- 1. activations of this thread's B groups, as straight-line loads:
-    // a group past the split's steps reads column k_lo again and a token
-    // past T reads token T - 1 (both unused), so no load waits for a branch
+    // ---- 1. activations of this thread's B groups g = threadIdx.x + i nthr
+    // (step g / G, k-group (g % G) / TP, token g % TP), as straight-line
+    // loads: a group past the split reads column k_lo again and a token past
+    // T reads token T - 1 (both unused), so no load waits for a branch.
+    // Every group of a thread has the same token (nthr is a multiple of TP).
     f32x4 xa[kGroupsPerThread][2], ua[kGroupsPerThread][2];
     u32x4 la[kGroupsPerThread];
-    const int jj = lane & 15;  // token of every group of this thread
-    const bool tok = jj < T;
-    const float* xrow = p.x + (int64_t)min(jj, T - 1) * p.xs;
+    const int tg = threadIdx.x % TP;  // token of this thread's groups
+    const bool tgok = tg < T;
+    const float* xrow = p.x + (int64_t)min(tg, T - 1) * p.xs;
+    auto gcol = [&](int g) { return k_lo + (g < ngr ? (g / G) * 32 + ((g % G) / TP) * 8 : 0); };
 #pragma unroll
     for (int i = 0; i < kGroupsPerThread; ++i) {
-        const int g = threadIdx.x + i * nthr;
-        const int s = g >> 6;
-        const int k = k_lo + (s < nst ? s * 32 + ((g & 63) >> 4) * 8 : 0);
+        const int k = gcol(threadIdx.x + i * nthr);
         xa[i][0] = *reinterpret_cast<const f32x4*>(xrow + k);
         xa[i][1] = *reinterpret_cast<const f32x4*>(xrow + k + 4);
         if constexpr (M2) {
@@ -131,8 +136,11 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     // the x' staging below, so that the wait for these row pointers does not
     // hold up the staging), and per output the row window and, for an
     // accumulating single split, the old y (rows and tokens clamped into
-    // range: no branch)
+    // range: no branch).  Outputs are in the MFMA result layout: lane l holds
+    // token jj = l % 16 and rows 4 (l / 16) + 0..3 of each row block.
     const int q = lane >> 4;
+    const int jj = lane & 15;  // token of this lane's outputs
+    const bool tok = jj < T;
     const int32_t e_lo = p.rp[min(nw, p.N)], e_hi = p.rp[min(nw + RBW * 16, p.N)];
     // Per row block, lane l's four rows 4(l/16) + 0..3 are consecutive: one
     // 16-byte load of their windows and (one split, accumulating) of their
@@ -156,54 +164,68 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
             oy[b] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r_y, (min(jj, T - 1) * p.N + nb) * 4, 0, 0));
     }
 
-    // ---- 3. x' * 2^64 split into bf16 parts, in B-operand order; the
+    // ---- 3. x' * 2^64 split into bf16 parts, in B-operand order (group g at
+    // xb[(g / G) 3 G + g % G], parts G apart; tokens past T are zeros); the
     // exponent range of x' is tracked for the fast path's check
     float sq = 0.0f;
     int elo = 0, ehi = 0;
+    auto stage = [&](int g, f32x4 x0, f32x4 x1, f32x4 u0, f32x4 u1, u32x4 lw4) {
+        u32x4 hi = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
+        if (tgok) {
+            float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            if constexpr (LN) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sq += (v[e] * kSsqScale) * (v[e] * kSsqScale);
+            }
+            if constexpr (M2) {
+                const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = silu_mul(v[e], u[e]);
+            }
+            if constexpr (LN) {
+                const uint32_t lw[4] = {lw4.x, lw4.y, lw4.z, lw4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[2 * e] *= __uint_as_float(lw[e] << 16);
+                    v[2 * e + 1] *= __uint_as_float(lw[e] & 0xFFFF0000u);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                track_exp(v[e], elo, ehi);
+                v[e] *= kXScale;
+            }
+            split3(v, hi, mid, lo);
+        }
+        u32x4* d = xb + (size_t)(g / G) * 3 * G + (g % G);
+        d[0] = hi;
+        d[G] = mid;
+        d[2 * G] = lo;
+    };
 #pragma unroll
     for (int i = 0; i < kGroupsPerThread; ++i) {
         const int g = threadIdx.x + i * nthr;
-        const int s = g >> 6;
-        if (s < nst) {
-            u32x4 hi = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
-            if (tok) {
-                float v[8] = {xa[i][0].x, xa[i][0].y, xa[i][0].z, xa[i][0].w,
-                              xa[i][1].x, xa[i][1].y, xa[i][1].z, xa[i][1].w};
-                if constexpr (LN) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) sq += (v[e] * kSsqScale) * (v[e] * kSsqScale);
-                }
-                if constexpr (M2) {
-                    const float u[8] = {ua[i][0].x, ua[i][0].y, ua[i][0].z, ua[i][0].w,
-                                        ua[i][1].x, ua[i][1].y, ua[i][1].z, ua[i][1].w};
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = silu_mul(v[e], u[e]);
-                }
-                if constexpr (LN) {
-                    const uint32_t lw[4] = {la[i].x, la[i].y, la[i].z, la[i].w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        v[2 * e] *= __uint_as_float(lw[e] << 16);
-                        v[2 * e + 1] *= __uint_as_float(lw[e] & 0xFFFF0000u);
-                    }
-                }
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    track_exp(v[e], elo, ehi);
-                    v[e] *= kXScale;
-                }
-                split3(v, hi, mid, lo);
-            }
-            u32x4* d = xb + (size_t)s * 192 + (g & 63);
-            d[0] = hi;
-            d[64] = mid;
-            d[128] = lo;
+        if (g < ngr) stage(g, xa[i][0], xa[i][1], ua[i][0], ua[i][1], la[i]);
+    }
+    // groups beyond the register-staged ones (long splits at few tokens):
+    // loaded here, after the weight prefetch
+    for (int g = threadIdx.x + kGroupsPerThread * nthr; g < ngr; g += nthr) {
+        const int k = gcol(g);
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(xrow + k), x1 = *reinterpret_cast<const f32x4*>(xrow + k + 4);
+        f32x4 u0 = x0, u1 = x1;
+        if constexpr (M2) {
+            u0 = *reinterpret_cast<const f32x4*>(xrow + p.K + k);
+            u1 = *reinterpret_cast<const f32x4*>(xrow + p.K + k + 4);
         }
+        u32x4 lw4 = {0, 0, 0, 0};
+        if constexpr (LN) lw4 = *reinterpret_cast<const u32x4*>(p.lnw + k);
+        stage(g, x0, x1, u0, u1, lw4);
     }
     if constexpr (LN) {
-        sq += __shfl_xor(sq, 16);
-        sq += __shfl_xor(sq, 32);
-        if (lane < 16) ssq[wave * 16 + lane] = sq;
+        // lanes tg, tg + TP, ... of the wave hold token tg
+#pragma unroll
+        for (int o = TP; o < 64; o <<= 1) sq += __shfl_xor(sq, o);
+        if (lane < TP) ssq[wave * 16 + lane] = sq;
     }
     {
         const bool bad = elo < kXRangeLo || ehi > kXRangeHi;
@@ -228,7 +250,8 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     // ---- 3b. (rare) some nonzero |x'| of the split outside [2^-64, 2^63):
     // per-token scale exponents P from the largest |x'| of the split, and the
     // parts staged again from the inputs with x' * 2^P.  Pj is the exponent of
-    // this thread's token jj, the token of its outputs and exception sums.
+    // token jj (this lane's outputs and exception sums), Pg that of token tg
+    // (this thread's staged groups).
     int Pj = kXScaleExp;
     int anybad = 0;
     for (int w = 0; w < W; ++w) anybad |= wflag[w];
@@ -255,43 +278,46 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
             }
         };
         int em = -1000;
-        for (int i = 0; i < kGroupsPerThread; ++i) {
-            const int s = (threadIdx.x + i * nthr) >> 6;
-            if (s < nst && tok) {
+        if (tgok) {
+            for (int g = threadIdx.x; g < ngr; g += nthr) {
                 float v[8];
-                xprime(k_lo + s * 32 + (lane >> 4) * 8, v);
+                xprime(gcol(g), v);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) em = max(em, exp_or_min(v[e]));
             }
         }
-        // lanes jj, jj + 16, jj + 32, jj + 48 hold token jj
-        em = max(em, __shfl_xor(em, 16));
-        em = max(em, __shfl_xor(em, 32));
-        if (lane < 16) wexp[wave * 16 + lane] = em;
-        __syncthreads();
-        em = -1000;
-        for (int w = 0; w < W; ++w) em = max(em, wexp[w * 16 + jj]);
-        Pj = slow_scale_exp(em);
-        for (int i = 0; i < kGroupsPerThread; ++i) {
-            const int g = threadIdx.x + i * nthr;
-            const int s = g >> 6;
-            if (s < nst && tok) {
-                float v[8];
-                xprime(k_lo + s * 32 + (lane >> 4) * 8, v);
+        // lanes tg, tg + TP, ... hold token tg
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = ldexpf(v[e], Pj);
+        for (int o = TP; o < 64; o <<= 1) em = max(em, __shfl_xor(em, o));
+        if (lane < TP) wexp[wave * 16 + lane] = em;
+        __syncthreads();
+        int eg = -1000, ej = -1000;
+        for (int w = 0; w < W; ++w) {
+            eg = max(eg, wexp[w * 16 + tg]);
+            ej = max(ej, wexp[w * 16 + min(jj, TP - 1)]);
+        }
+        const int Pg = slow_scale_exp(eg);
+        Pj = slow_scale_exp(ej);
+        if (tgok) {
+            for (int g = threadIdx.x; g < ngr; g += nthr) {
+                float v[8];
+                xprime(gcol(g), v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = ldexpf(v[e], Pg);
                 u32x4 hi, mid, lo;
                 split3(v, hi, mid, lo);
-                u32x4* d = xb + (size_t)s * 192 + (g & 63);
+                u32x4* d = xb + (size_t)(g / G) * 3 * G + (g % G);
                 d[0] = hi;
-                d[64] = mid;
-                d[128] = lo;
+                d[G] = mid;
+                d[2 * G] = lo;
             }
         }
         __syncthreads();
     }
 
-    // ---- 4. main loop
+    // ---- 4. main loop: lane l reads the B group of token l % 16 and k-group
+    // l / 16; lanes of tokens >= TP take zeros without an LDS read
+    const int bl = jj < TP ? q * TP + jj : -1;
     f32x4 acc[RBW][3];
 #pragma unroll
     for (int b = 0; b < RBW; ++b)
@@ -307,8 +333,13 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
             for (int b = 0; b < RBW; ++b) cur[b] = buf[u][b];
             issue_rows<RBW>(buf[u], rv, rnull, voff, s_lo + sr + D, s_hi);
             if (sr < nst) {
-                const u32x4* bsrc = xb + (size_t)sr * 192 + lane;
-                const u32x4 b0 = bsrc[0], b1 = bsrc[64], b2 = bsrc[128];
+                u32x4 b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0}, b2 = {0, 0, 0, 0};
+                if (TP == 16 || bl >= 0) {
+                    const u32x4* bsrc = xb + (size_t)sr * 3 * G + bl;
+                    b0 = bsrc[0];
+                    b1 = bsrc[G];
+                    b2 = bsrc[2 * G];
+                }
 #pragma unroll
                 for (int b = 0; b < RBW; ++b) {
                     uint32_t pr[4];
@@ -353,11 +384,12 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
                 const float vv = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), src));
                 if (lane < T) {
                     // byte offset of x'(token lane, cc) in part 0: step cc/32,
-                    // B lane 16 * ((cc%32)/8) + token, element cc%8
-                    const int o = (((cc >> 5) * 192 + ((cc & 31) >> 3) * 16 + lane) * 16) + (cc & 7) * 2;
+                    // group ((cc%32)/8) TP + token, element cc%8; parts G 16
+                    // bytes apart
+                    const int o = ((cc >> 5) * 3 * G + ((cc & 31) >> 3) * TP + lane) * 16 + (cc & 7) * 2;
                     const float xv = bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o)) +
-                                     bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o + 1024)) +
-                                     bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o + 2048));
+                                     bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o + G * 16)) +
+                                     bf16_value(*reinterpret_cast<const uint16_t*>(xbytes + o + 2 * G * 16));
                     excw[rr * 16 + lane] += vv * ldexpf(xv, -Pj);
                 }
             }
@@ -415,34 +447,47 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     (void)n0;
 }
 
-template <int RBW, bool M2, bool LN>
+template <int TP, int RBW, bool M2, bool LN>
 static void launch_t(const LinearParams& p, int T, dim3 grid, int threads, size_t lds, hipStream_t st) {
     if (lds > kDefaultLds)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<RBW, M2, LN>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<TP, RBW, M2, LN>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((k_gemm<RBW, M2, LN>), grid, dim3(threads), lds, st, p, T);
+    hipLaunchKernelGGL((k_gemm<TP, RBW, M2, LN>), grid, dim3(threads), lds, st, p, T);
 }
 
-template <int RBW>
+template <int TP, int RBW>
 static void launch_r(const LinearParams& p, int T, dim3 grid, int threads, size_t lds, hipStream_t st) {
     const bool m2 = p.mode == 2, ln = p.lnw != nullptr;
-    if (m2 && ln) launch_t<RBW, true, true>(p, T, grid, threads, lds, st);
-    else if (m2) launch_t<RBW, true, false>(p, T, grid, threads, lds, st);
-    else if (ln) launch_t<RBW, false, true>(p, T, grid, threads, lds, st);
-    else launch_t<RBW, false, false>(p, T, grid, threads, lds, st);
+    if (m2 && ln) launch_t<TP, RBW, true, true>(p, T, grid, threads, lds, st);
+    else if (m2) launch_t<TP, RBW, true, false>(p, T, grid, threads, lds, st);
+    else if (ln) launch_t<TP, RBW, false, true>(p, T, grid, threads, lds, st);
+    else launch_t<TP, RBW, false, false>(p, T, grid, threads, lds, st);
+}
+
+template <int TP>
+static int launch_tp(const LinearParams& p, int T, int rbw, dim3 grid, int threads, size_t lds, hipStream_t st) {
+    switch (rbw) {
+        case 1: launch_r<TP, 1>(p, T, grid, threads, lds, st); return 0;
+        case 2: launch_r<TP, 2>(p, T, grid, threads, lds, st); return 0;
+        case 4: launch_r<TP, 4>(p, T, grid, threads, lds, st); return 0;
+    }
+    return -1;
 }
 
 int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st) {
     const int64_t nblk = (p.N + 15) / 16;
     const int64_t per_wg = (int64_t)rbw * waves;
     dim3 grid((unsigned)((nblk + per_wg - 1) / per_wg), (unsigned)splits);
-    const size_t lds = gemm_lds_bytes(p.K, rbw, waves, splits);
-    switch (rbw) {
-        case 1: launch_r<1>(p, T, grid, waves * 64, lds, st); break;
-        case 2: launch_r<2>(p, T, grid, waves * 64, lds, st); break;
-        case 4: launch_r<4>(p, T, grid, waves * 64, lds, st); break;
+    const int tp = gemm_tokens(T);
+    const size_t lds = gemm_lds_bytes(p.K, rbw, waves, splits, T);
+    int rc;
+    switch (tp) {
+        case 4: rc = launch_tp<4>(p, T, rbw, grid, waves * 64, lds, st); break;
+        case 8: rc = launch_tp<8>(p, T, rbw, grid, waves * 64, lds, st); break;
+        case 16: rc = launch_tp<16>(p, T, rbw, grid, waves * 64, lds, st); break;
         default: return -1;
     }
+    if (rc) return rc;
     if (splits > 1) launch_splitk_reduce(p, T, splits, st);
     return 0;
 }

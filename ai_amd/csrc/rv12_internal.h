@@ -72,16 +72,19 @@ inline bool gemv_prefetch_all(int K, int T, int waves, int splits) {
 }
 
 // --- MFMA linear (k_gemm), 1..16 tokens
-constexpr size_t kGemmMaxLds = 131072;
+constexpr size_t kGemmMaxLds = kMaxLds;
 constexpr int kGemmMaxWaves = 8;
-inline size_t gemm_lds_bytes(int K, int rbw, int waves, int splits) {
+// token columns the kernel stages for T tokens: 4, 8 or 16
+__host__ __device__ constexpr int gemm_tokens(int T) { return T <= 4 ? 4 : (T <= 8 ? 8 : 16); }
+inline size_t gemm_lds_bytes(int K, int rbw, int waves, int splits, int T) {
     const size_t steps = (size_t)split_steps(K, splits);
-    // parts, exception sums, sums of squares, range flags, slow-path exponents
-    return steps * 3 * 1024 + (size_t)waves * rbw * 16 * 16 * 4 + 16 * 4 * (size_t)waves + 4 * (size_t)waves +
-           16 * 4 * (size_t)waves;
+    // parts (3 x 4 k-groups x TP tokens x 16 bytes per step), exception sums,
+    // sums of squares, range flags, slow-path exponents
+    return steps * 3 * 64 * (size_t)gemm_tokens(T) + (size_t)waves * rbw * 16 * 16 * 4 + 16 * 4 * (size_t)waves +
+           4 * (size_t)waves + 16 * 4 * (size_t)waves;
 }
-inline bool gemm_fits(int K, int rbw, int waves, int splits) {
-    return waves <= kGemmMaxWaves && gemm_lds_bytes(K, rbw, waves, splits) <= kGemmMaxLds;
+inline bool gemm_fits(int K, int T, int rbw, int waves, int splits) {
+    return waves <= kGemmMaxWaves && gemm_lds_bytes(K, rbw, waves, splits, T) <= kGemmMaxLds;
 }
 
 // --- decode-step attention (k_rope_attn)

@@ -94,12 +94,19 @@ def test_launch_shapes():
     assert shape(4096, 4096, 8) == (2, 1, 8, 8)           # 8B o: 256 workgroups of 16 K steps
     assert shape(6144, 4096, 4) == (2, 2, 8, 10)          # 8B qkv: 240 workgroups
     assert shape(1024, 5120, 16) == (2, 1, 4, 16)         # 14B k/v: 64 row blocks, 16 splits of 10 steps
-    assert shape(5120, 5120, 4) == (2, 2, 8, 12)          # 14B o: 240 workgroups of 14 K steps
+    assert shape(5120, 5120, 4) == (2, 2, 8, 11)          # 14B o: 220 workgroups of 15 K steps
     assert shape(5120, 17408, 16)[:3] == (2, 4, 8)        # 14B down: four row blocks per wave
     assert shape(5120, 8192, 16) == (2, 2, 8, 12)         # 32B o
-    assert shape(5120, 25600, 8) == (2, 2, 8, 25)         # 32B down
-    # 4 waves of the MFMA kernel stage at most 16 steps: K = 5120 is split 10 ways
-    assert shape(5120, 5120, 16, _lib.Launch(2, 2, 4, 0)) == (2, 2, 4, 10)
+    assert shape(5120, 25600, 8) == (2, 4, 8, 23)         # 32B down
+    # a partial configuration keeps the built-in split where its staging fits
+    # the LDS (3 KB per K step at 16 tokens, 768 B at 4); an explicit split
+    # whose staging does not fit is rejected
+    assert shape(5120, 5120, 16, _lib.Launch(2, 2, 4, 0)) == (2, 2, 4, 11)
+    assert shape(5120, 5120, 4, _lib.Launch(2, 1, 4, 1)) == (2, 1, 4, 1)    # 160 steps of 768 B
+    c = _lib.Launch()
+    assert L.rv12_launch_shape(5120, 5120, 16, ctypes.byref(_lib.Launch(2, 2, 4, 2)),
+                               ctypes.byref(c)) == _lib.RV12_E_CONFIG     # 80 steps of 3 KB
+
     assert shape(5120, 5120, 1, _lib.Launch(1, 1, 4, 3)) == (1, 1, 4, 3)
     c = _lib.Launch()
     assert L.rv12_launch_shape(64, 100, 1, None, ctypes.byref(c)) == _lib.RV12_E_SHAPE

@@ -145,11 +145,14 @@ def test_shapes_and_launch_shapes(N, K):
             _check(cnp, cg, 1, mode, mode == 0, 7, BN=BN, w=w)
             _check(cnp, cg, 2, mode, False, 8, BN=BN, w=w, S=S, use_tc=True)
     # MFMA kernel (the built-in choice from 3 tokens): every row-block count
-    # per wave and wave count it takes (the split count left to the library),
-    # straight through the C ABI
+    # per wave and wave count it takes (the split count left to the library:
+    # the fewest splits whose staging fits the LDS, so long splits stage
+    # groups past the 4 per thread held in registers), straight through the
+    # C ABI, at token counts of each staged width (4, 8, 16 columns)
     for rb, w, S in [(rb, w, 0) for rb in (1, 2, 4) for w in (1, 2, 4, 8)] + [(1, 4, nsteps), (4, 2, nsteps // 4)]:
         print("  mfma launch", rb, w, S, flush=True)
-        for T, mode, rms in ((3, 0, True), (3, 2, False), (16, 1, False), (11, 2, True)):
+        for T, mode, rms in ((1, 0, True), (3, 0, True), (3, 2, False), (6, 1, False), (8, 2, True), (16, 1, False),
+                             (11, 2, True)):
             _check(cnp, cg, T, mode, rms, 9 + T, launch=(2, rb, w, S))
 
 
@@ -287,19 +290,22 @@ def test_two_tokens_with_k_beyond_the_vector_staging():
 
 
 def test_partial_launch_shape_sizes_its_workspace():
-    """BN and w given, S left to the library: with 2 waves the MFMA kernel
-    stages at most 8 steps of K, so K = 5120 is split at least 20 ways, more
-    than the built-in shape's split, and the workspace is sized for the split
-    the launch resolves to."""
+    """BN and w given, S left to the library, and an explicit S beyond the
+    built-in shape's: the workspace is sized for the split each launch
+    resolves to (the built-in 16-token launch's workspace would be too
+    small for 24 splits)."""
     from ai_amd import wcomp
     N, K = 2048, 5120
     bits = _random_matrix(N, K, 77, out_rows=0.01)
     cnp = codec.compress(bits)
     cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
-    shape = wcomp.launch_shape(N, K, 16, wcomp._launch(32, 2, None, 16))
-    assert shape[:3] == (2, 1, 2) and shape[3] >= 20 > wcomp.launch_shape(N, K, 16)[3]
+    builtin = wcomp.launch_shape(N, K, 16)[3]
+    partial = wcomp.launch_shape(N, K, 16, wcomp._launch(32, 2, None, 16))
+    assert partial[:3] == (2, 1, 2)
+    assert wcomp.launch_shape(N, K, 16, wcomp._launch(32, 2, 24, 16)) == (2, 1, 2, 24) and 24 > builtin
     for mode in (0, 2):
         _check(cnp, cg, 16, mode, False, 60 + mode, BN=32, w=2, use_tc=True)
+        _check(cnp, cg, 16, mode, False, 62 + mode, BN=32, w=2, S=24, use_tc=True)
 
 
 def _check_scaled(cnp, c_gpu, T, mode, rms, seed, e, both_halves=False, **kw):
@@ -343,7 +349,8 @@ def test_activation_scale(e):
     cnp = codec.compress(bits)
     cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
     cases = [(1, {}), (2, {}), (3, {"launch": (1, 1, 8, 0)}), (4, {"launch": (1, 1, 8, 0)}),  # vector kernel
-             (3, {}), (8, {}), (16, {}), (16, {"launch": (2, 2, 4, 0)})]                        # MFMA kernel
+             (3, {"launch": (2, 1, 4, 0)}), (4, {}), (6, {}), (8, {}), (16, {}),                  # MFMA kernel
+             (16, {"launch": (2, 2, 4, 0)}), (4, {"launch": (2, 1, 1, 0)})]
     for T, kw in cases:
         use_tc = T > 1
         for mode in (0, 1, 2):
@@ -362,7 +369,8 @@ def test_activation_scale_mixed_tokens():
     cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
     W = codec.decode_f32(cnp).astype(np.float64)
     rng = np.random.default_rng(5)
-    for T, kw in ((2, {}), (4, {"launch": (1, 1, 8, 0)}), (7, {}), (16, {})):
+    for T, kw in ((2, {}), (4, {"launch": (1, 1, 8, 0)}), (3, {"launch": (2, 1, 4, 0)}), (4, {}), (7, {}),
+                  (16, {})):
         for mode in (0, 2):
             K = cnp["K"]
             X = rng.standard_normal((T, 2 * K if mode == 2 else K))
