@@ -50,7 +50,7 @@ class Launch(ctypes.Structure):
                 ("splits", ctypes.c_int32)]
 
 
-KERNEL_VECTOR, KERNEL_MFMA = 1, 2
+KERNEL_VECTOR, KERNEL_MFMA, KERNEL_MFMA_KSPLIT = 1, 2, 3
 
 
 class Attn(ctypes.Structure):

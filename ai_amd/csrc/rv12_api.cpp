@@ -26,6 +26,7 @@ struct Shape {
 bool shape_fits(int K, int T, const Shape& c) {
     if (c.kernel == 1) return T <= kMaxVectorTokens && gemv_fits(K, T, c.rb, c.waves, c.splits);
     // MFMA: the split's staged activations (sized by the token columns) fit the LDS
+    if (c.kernel == 3) return gemm_ks_fits(K, T, c.rb, c.waves, c.splits);
     return gemm_fits(K, T, c.rb, c.waves, c.splits);
 }
 
@@ -90,30 +91,40 @@ constexpr double kModelRoundUs = 1.5;
 constexpr double kModelStepUs = 0.2;
 constexpr double kModelHbmGBs = 6500.0;
 constexpr double kModelCuGBs = 30.0;
+// kernel 3 (the waves split K): the per-CU rate fitted to the same sweep with
+// its shapes added; it is slower than kernel 2 on all but 2 of the 42 cases
+// (Qwen3-8B down and 32B o at 4 tokens, by 1-4 %), so the built-in choice is
+// kernel 2 and kernel 3 a candidate of the tuner and of explicit launches
+constexpr double kModelKsCuGBs = 10.0;
 constexpr double kModelReduceUs = 0.5;
 constexpr double kModelReduceUsPerMB = 1.0;
 constexpr int kModelCUs = 256;
 constexpr double kModelStepBytes = 768.0;  // one (row block, step) tile
 
-double mfma_model_us(int64_t nblk, int N, int K, int T, int rb, int waves, int splits) {
-    const int64_t per_wg = (int64_t)rb * waves;
+// kernel 2: each wave owns rb row blocks (rb x waves per workgroup); kernel
+// 3: the waves split K over rb row blocks per workgroup
+double mfma_model_us(int64_t nblk, int N, int K, int T, int rb, int waves, int splits, int kernel = 2) {
+    const int64_t per_wg = (int64_t)rb * (kernel == 3 ? 1 : waves);
     const int64_t wgs = (nblk + per_wg - 1) / per_wg * splits;
     const int steps = split_steps(K, splits);
     const double wg_bytes = (double)per_wg * steps * kModelStepBytes;
+    const double cu_rate = kernel == 3 ? kModelKsCuGBs : kModelCuGBs;
     double t = 0.0;
     for (int64_t left = wgs; left > 0;) {
         const int64_t n = std::min<int64_t>(left, (int64_t)kModelCUs);
         t += kModelRoundUs + kModelStepUs * steps * gemm_tokens(T) / 16.0 +
-             (double)n * wg_bytes / (std::min(kModelHbmGBs, (double)n * kModelCuGBs) * 1e3);
+             (double)n * wg_bytes / (std::min(kModelHbmGBs, (double)n * cu_rate) * 1e3);
         left -= n;
     }
     if (splits > 1) t += kModelReduceUs + kModelReduceUsPerMB * (double)(splits + 1) * T * N * 4 / 1e6;
     return t;
 }
 
-// candidates: 1, 2 or 4 row blocks per wave, 4 or 8 waves, the fewest K
-// splits whose staging fits and up to 10 more
-Shape mfma_shape(int N, int K, int T) {
+// candidates of MFMA kernel `kernel` (2, 3, or 0 for both): 1, 2 or 4 row
+// blocks per wave (kernel 2) or per workgroup (kernel 3, at most one per
+// wave), 4 or 8 waves, the fewest K splits whose staging fits and up to 10
+// more
+Shape mfma_shape(int N, int K, int T, int kernel = 2) {
     const int64_t nblk = nblocks(N);
     const int nsteps = K / 32;
     Shape best;
@@ -122,24 +133,32 @@ Shape mfma_shape(int N, int K, int T) {
     best.waves = 1;
     best.splits = nsteps;
     double best_t = 1e300;
-    for (int rb : {1, 2, 4}) {
-        for (int w : {4, 8}) {
-            const int wv = std::min(w, nsteps);  // no more waves than K steps
-            // the built-in shapes keep every staged group in registers
-            // (4 per thread: 64 waves / TP steps), so no staging load waits
-            // behind the weight prefetch
-            auto fits = [&](int s) { return split_steps(K, s) <= 64 * wv / gemm_tokens(T) && gemm_fits(K, T, rb, wv, s); };
-            int s0 = 1;
-            while (s0 < std::min(kMaxSplits, nsteps) && !fits(s0)) ++s0;
-            if (!fits(s0)) continue;
-            for (int s = s0; s <= std::min({s0 + 10, kMaxSplits, nsteps}); ++s) {
-                if (!fits(s)) continue;
-                const double t = mfma_model_us(nblk, N, K, T, rb, wv, s);
-                if (t < best_t) {
-                    best_t = t;
-                    best.rb = rb;
-                    best.waves = wv;
-                    best.splits = s;
+    for (int kn : {2, 3}) {
+        if (kernel && kn != kernel) continue;
+        for (int rb : {1, 2, 4}) {
+            for (int w : {4, 8}) {
+                const int wv = std::min(w, nsteps);  // no more waves than K steps
+                if (kn == 3 && wv < rb) continue;
+                // kernel 2's built-in shapes keep every staged group in
+                // registers (4 per thread: 64 waves / TP steps), so no
+                // staging load waits behind the weight prefetch
+                auto fits = [&](int s) {
+                    return kn == 3 ? gemm_ks_fits(K, T, rb, wv, s)
+                                   : split_steps(K, s) <= 64 * wv / gemm_tokens(T) && gemm_fits(K, T, rb, wv, s);
+                };
+                int s0 = 1;
+                while (s0 < std::min(kMaxSplits, nsteps) && !fits(s0)) ++s0;
+                if (!fits(s0)) continue;
+                for (int s = s0; s <= std::min({s0 + 10, kMaxSplits, nsteps}); ++s) {
+                    if (!fits(s)) continue;
+                    const double t = mfma_model_us(nblk, N, K, T, rb, wv, s, kn);
+                    if (t < best_t) {
+                        best_t = t;
+                        best.kernel = kn;
+                        best.rb = rb;
+                        best.waves = wv;
+                        best.splits = s;
+                    }
                 }
             }
         }
@@ -161,7 +180,7 @@ Shape default_shape(int N, int K, int T) {
     const bool vec3 = T == 3 && K <= 6144 && nblocks(N) <= 512;
     vec = vec || vec3;
     Shape c = vec ? vector_shape(N, K, T) : mfma_shape(N, K, T);
-    while (c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
+    while (c.kernel != 3 && c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
     // at one token the vector kernel's waves want at least 8 K steps each
     // (Qwen3-0.6B qkv 4096x1024: 4.6 us at 4 waves, 5.1 at 8)
     while (c.kernel == 1 && T == 1 && c.waves > 2 && split_steps(K, c.splits) < 8 * c.waves) c.waves >>= 1;
@@ -192,8 +211,8 @@ Shape default_shape(int N, int K, int T) {
 int resolve_launch(int N, int K, int T, const rv12_launch* cfg, Shape* out) {
     Shape c = default_shape(N, K, T);
     if (cfg) {
-        if (cfg->kernel && cfg->kernel != c.kernel)
-            c = cfg->kernel == 2 ? mfma_shape(N, K, T) : vector_shape(N, K, T);  // that kernel's own defaults first
+        if (cfg->kernel && cfg->kernel != c.kernel)  // that kernel's own defaults first
+            c = cfg->kernel >= 2 ? mfma_shape(N, K, T, cfg->kernel == 3 ? 3 : 2) : vector_shape(N, K, T);
         if (cfg->kernel) c.kernel = cfg->kernel;                            // an unknown kernel is rejected below
         if (cfg->rb) c.rb = cfg->rb;
         if (cfg->waves) c.waves = cfg->waves;
@@ -201,12 +220,12 @@ int resolve_launch(int N, int K, int T, const rv12_launch* cfg, Shape* out) {
             c.splits = cfg->splits;
         } else {
             // keep the staging / LDS bounds when only other fields were given
-            while (c.splits < kMaxSplits && c.splits < K / 32 && c.kernel >= 1 && c.kernel <= 2 &&
+            while (c.splits < kMaxSplits && c.splits < K / 32 && c.kernel >= 1 && c.kernel <= 3 &&
                    c.rb >= 1 && c.waves >= 1 && c.waves <= kMaxWaves && !shape_fits(K, T, c))
                 ++c.splits;
         }
     }
-    if (c.kernel != 1 && c.kernel != 2) return RV12_E_CONFIG;
+    if (c.kernel < 1 || c.kernel > 3) return RV12_E_CONFIG;
     if (c.kernel == 1 && T > kMaxVectorTokens) return RV12_E_CONFIG;
     if (c.rb != 1 && c.rb != 2 && c.rb != 4) return RV12_E_CONFIG;
     if (c.waves < 1 || c.waves > kMaxWaves) return RV12_E_CONFIG;
@@ -438,7 +457,7 @@ int rv12_gemm(const rv12_matrix* w, const float* x, float* y, int t, const uint1
     LinearParams p;
     fill_params(p, w, x, y, t, lnw, eps, mode, ws, splits, need != 0);
     const int lrc = c.kernel == 1 ? launch_gemv(p, t, c.rb, c.waves, splits, (hipStream_t)stream)
-                                  : launch_gemm(p, t, c.rb, c.waves, splits, (hipStream_t)stream);
+                                  : launch_gemm(p, t, c.rb, c.waves, splits, c.kernel == 3, (hipStream_t)stream);
     if (lrc) return RV12_E_CONFIG;
     return launch_status();
 }
@@ -489,7 +508,7 @@ int rv12_head_argmax(const rv12_matrix* w, const float* x, int t, const uint16_t
         lrc = launch_gemv(p, t, c.rb, c.waves, 1, st);
     } else {
         lrc = c.kernel == 1 ? launch_gemv(p, t, c.rb, c.waves, c.splits, st)
-                            : launch_gemm(p, t, c.rb, c.waves, c.splits, st);
+                            : launch_gemm(p, t, c.rb, c.waves, c.splits, c.kernel == 3, st);
     }
     if (lrc) return RV12_E_CONFIG;
     if (h.fused)

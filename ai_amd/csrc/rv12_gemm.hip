@@ -64,9 +64,16 @@ __device__ __forceinline__ void issue_rows(u32x3 (&dst)[RBW], __amdgpu_buffer_rs
 // (MODE 2); LN: RMSNorm weight.  Template arguments, so that the activation
 // loads of step 1 are straight-line code that waits for no kernel argument
 // test, and the group arithmetic is shifts.
-template <int TP, int RBW, bool M2, bool LN>
+// KS: the waves split the workgroup's K steps instead of its rows: the
+// workgroup covers RBW row blocks, wave w takes steps s_lo + w + W i of all of
+// them, the waves' sums are joined through LDS in a fixed order and wave b
+// < RBW finishes row block b (exceptions, scale, store).  One workgroup then
+// needs no K split for as many rows as the LDS holds x' for: at 4 token
+// columns (768 B per K step) K up to ~6000, so the split's reduce launch goes.
+template <int TP, int RBW, bool M2, bool LN, bool KS>
 __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int T) {
     constexpr int G = 4 * TP;
+    constexpr int ORB = KS ? 1 : RBW;  // row blocks of this wave's outputs
     extern __shared__ u32x4 lds4[];
     const int W = blockDim.x >> 6;
     const int nthr = blockDim.x;
@@ -80,15 +87,18 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     const int nst = s_hi - s_lo, k_lo = s_lo * 32, krange = nst * 32;
     const int ngr = nst * G;  // B-operand groups of the split
     const int64_t nblk = (p.N + 15) / 16;
-    const int64_t blk0 = (int64_t)blockIdx.x * W * RBW;
+    const int64_t blk0 = (int64_t)blockIdx.x * (KS ? 1 : W) * RBW;
     const int n0 = (int)(blk0 * 16);
-    const int64_t wblk = blk0 + wu * RBW;  // first row block of this wave
-    const int nw = (int)(wblk * 16);        // first row of this wave
+    const int64_t wblk = KS ? blk0 : blk0 + wu * RBW;  // first row block whose weights this wave loads
     const int nvalid = (int)max((int64_t)0, min((int64_t)RBW, nblk - wblk));
+    const int64_t oblk = KS ? blk0 + wu : wblk;  // first row block of this wave's outputs
+    const int nw = (int)(oblk * 16);             // first output row of this wave
+    const int onvalid = KS ? (wu < RBW && oblk < nblk ? 1 : 0) : nvalid;
 
     u32x4* xb = lds4;                                                  // [nst][3][G]
-    float* exc = reinterpret_cast<float*>(xb + (size_t)nst * 3 * G);  // [W*RBW*16 rows][16 tokens]
-    float* ssq = exc + W * RBW * 256;                                  // [W][16]
+    float* exc = reinterpret_cast<float*>(xb + (size_t)nst * 3 * G);  // [W*ORB*16 rows][16 tokens]
+    f32x4* red = reinterpret_cast<f32x4*>(exc + W * ORB * 256);       // KS: [W][RBW][64] the waves' sums
+    float* ssq = reinterpret_cast<float*>(red + (KS ? W * RBW * 64 : 0));  // [W][16]
     int* wflag = reinterpret_cast<int*>(ssq + W * 16);                 // [W] x' outside the fast path's range
     int* wexp = wflag + W;                                             // [W][16] slow path: largest exponent
 
@@ -128,8 +138,10 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
 #pragma unroll
     for (int b = 0; b < RBW; ++b) voff[b] = (int)(b * blk_bytes) + lane * 12;
     u32x3 buf[D][RBW];
+    const int s0 = s_lo + (KS ? wu : 0);  // this wave's first step
+    const int stride = KS ? W : 1;        // steps between this wave's consecutive steps
 #pragma unroll
-    for (int u = 0; u < D; ++u) issue_rows<RBW>(buf[u], rv, rnull, voff, s_lo + u, s_hi);
+    for (int u = 0; u < D; ++u) issue_rows<RBW>(buf[u], rv, rnull, voff, s0 + u * stride, s_hi);
 
     // what the epilogue reads, loaded now so that it arrives during the main
     // loop: the wave's exception range (its first 64 entries are loaded after
@@ -141,7 +153,7 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     const int q = lane >> 4;
     const int jj = lane & 15;  // token of this lane's outputs
     const bool tok = jj < T;
-    const int32_t e_lo = p.rp[min(nw, p.N)], e_hi = p.rp[min(nw + RBW * 16, p.N)];
+    const int32_t e_lo = p.rp[min(nw, p.N)], e_hi = p.rp[min(nw + ORB * 16, p.N)];
     // Per row block, lane l's four rows 4(l/16) + 0..3 are consecutive: one
     // 16-byte load of their windows and (one split, accumulating) of their
     // old y.  With N % 4 == 0 each such group lies wholly inside or wholly
@@ -150,14 +162,14 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     // y is loaded whatever the mode, so every load here is straight-line and
     // the waits of the staging below count exactly; with four row blocks per
     // wave y is read in the epilogue (registers).
-    constexpr bool kPreY = RBW <= 2;
+    constexpr bool kPreY = ORB <= 2;
     const bool vec = (p.N & 3) == 0;
     const __amdgpu_buffer_rsrc_t r_rb = make_rsrc(p.rbase, (uint32_t)p.N * 4u);
     const __amdgpu_buffer_rsrc_t r_y = make_rsrc(p.y, (uint32_t)((int64_t)T * p.N * 4));
-    u32x4 obase[RBW];
-    f32x4 oy[RBW];
+    u32x4 obase[ORB];
+    f32x4 oy[ORB];
 #pragma unroll
-    for (int b = 0; b < RBW; ++b) {
+    for (int b = 0; b < ORB; ++b) {
         const int nb = nw + b * 16 + q * 4;
         obase[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_rb, nb * 4, 0, 0));
         if constexpr (kPreY)
@@ -233,9 +245,9 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
         if (lane == 0) wflag[wave] = bm != 0;
     }
     // this wave's exception sums start at zero
-    float* excw = exc + wu * RBW * 256;
+    float* excw = exc + wu * ORB * 256;
 #pragma unroll
-    for (int i = 0; i < RBW * 4; ++i) excw[i * 64 + lane] = 0.0f;
+    for (int i = 0; i < ORB * 4; ++i) excw[i * 64 + lane] = 0.0f;
     // the wave's first 64 exception entries (a descriptor over the list reads
     // zeros past its end)
     const uint32_t exc_bytes = (uint32_t)min(p.n_exc, (int64_t)(1 << 28)) * 4u;
@@ -323,16 +335,18 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     for (int b = 0; b < RBW; ++b)
 #pragma unroll
         for (int c = 0; c < 3; ++c) acc[b][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int rounds = (nst + D - 1) / D;
+    const int per_wave = KS ? (nst + W - 1) / W : nst;
+    const int rounds = (per_wave + D - 1) / D;
     for (int r = 0; r < rounds; ++r) {
 #pragma unroll
         for (int u = 0; u < D; ++u) {
-            const int sr = r * D + u;  // step within the split
+            const int s = s0 + (r * D + u) * stride;
+            const int sr = s - s_lo;  // step within the split
             u32x3 cur[RBW];
 #pragma unroll
             for (int b = 0; b < RBW; ++b) cur[b] = buf[u][b];
-            issue_rows<RBW>(buf[u], rv, rnull, voff, s_lo + sr + D, s_hi);
-            if (sr < nst) {
+            issue_rows<RBW>(buf[u], rv, rnull, voff, s + D * stride, s_hi);
+            if (s < s_hi) {
                 u32x4 b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0}, b2 = {0, 0, 0, 0};
                 if (TP == 16 || bl >= 0) {
                     const u32x4* bsrc = xb + (size_t)sr * 3 * G + bl;
@@ -353,9 +367,24 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
         }
     }
 
-    // ---- 5. exceptions of this wave's rows, columns inside the split
+    // ---- 4b. this wave's output sums: KS joins the waves' sums through LDS
+    // in wave order, wave b < RBW taking row block b
+    f32x4 osum[ORB];
+    if constexpr (KS) {
+#pragma unroll
+        for (int b = 0; b < RBW; ++b) red[(wu * RBW + b) * 64 + lane] = acc[b][0] + acc[b][1] + acc[b][2];
+        __syncthreads();
+        osum[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (wu < RBW)
+            for (int w = 0; w < W; ++w) osum[0] += red[(w * RBW + wu) * 64 + lane];
+    } else {
+#pragma unroll
+        for (int b = 0; b < ORB; ++b) osum[b] = acc[b][0] + acc[b][1] + acc[b][2];
+    }
+
+    // ---- 5. exceptions of this wave's output rows, columns inside the split
     const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(xb);
-    if (nvalid > 0) {
+    if (onvalid > 0) {
         for (int32_t j0 = e_lo; j0 < e_hi; j0 += 64) {
             const int32_t j = j0 + lane;
             const bool valid = j < e_hi;
@@ -406,9 +435,9 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
         rs = rms_scale(v, p.K, p.eps);
     }
 #pragma unroll
-    for (int b = 0; b < RBW; ++b) {
-        if (b >= nvalid) break;
-        const f32x4 a = acc[b][0] + acc[b][1] + acc[b][2];
+    for (int b = 0; b < ORB; ++b) {
+        if (b >= onvalid) break;
+        const f32x4 a = osum[b];
         const float av[4] = {a.x, a.y, a.z, a.w};
         const int nb = nw + b * 16 + q * 4;
         int ob[4] = {(int)obase[b].x, (int)obase[b].y, (int)obase[b].z, (int)obase[b].w};
@@ -447,44 +476,49 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     (void)n0;
 }
 
-template <int TP, int RBW, bool M2, bool LN>
+template <int TP, int RBW, bool M2, bool LN, bool KS>
 static void launch_t(const LinearParams& p, int T, dim3 grid, int threads, size_t lds, hipStream_t st) {
     if (lds > kDefaultLds)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<TP, RBW, M2, LN>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm<TP, RBW, M2, LN, KS>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((k_gemm<TP, RBW, M2, LN>), grid, dim3(threads), lds, st, p, T);
+    hipLaunchKernelGGL((k_gemm<TP, RBW, M2, LN, KS>), grid, dim3(threads), lds, st, p, T);
 }
 
-template <int TP, int RBW>
+template <int TP, int RBW, bool KS>
 static void launch_r(const LinearParams& p, int T, dim3 grid, int threads, size_t lds, hipStream_t st) {
     const bool m2 = p.mode == 2, ln = p.lnw != nullptr;
-    if (m2 && ln) launch_t<TP, RBW, true, true>(p, T, grid, threads, lds, st);
-    else if (m2) launch_t<TP, RBW, true, false>(p, T, grid, threads, lds, st);
-    else if (ln) launch_t<TP, RBW, false, true>(p, T, grid, threads, lds, st);
-    else launch_t<TP, RBW, false, false>(p, T, grid, threads, lds, st);
+    if (m2 && ln) launch_t<TP, RBW, true, true, KS>(p, T, grid, threads, lds, st);
+    else if (m2) launch_t<TP, RBW, true, false, KS>(p, T, grid, threads, lds, st);
+    else if (ln) launch_t<TP, RBW, false, true, KS>(p, T, grid, threads, lds, st);
+    else launch_t<TP, RBW, false, false, KS>(p, T, grid, threads, lds, st);
 }
 
-template <int TP>
+template <int TP, bool KS>
 static int launch_tp(const LinearParams& p, int T, int rbw, dim3 grid, int threads, size_t lds, hipStream_t st) {
     switch (rbw) {
-        case 1: launch_r<TP, 1>(p, T, grid, threads, lds, st); return 0;
-        case 2: launch_r<TP, 2>(p, T, grid, threads, lds, st); return 0;
-        case 4: launch_r<TP, 4>(p, T, grid, threads, lds, st); return 0;
+        case 1: launch_r<TP, 1, KS>(p, T, grid, threads, lds, st); return 0;
+        case 2: launch_r<TP, 2, KS>(p, T, grid, threads, lds, st); return 0;
+        case 4: launch_r<TP, 4, KS>(p, T, grid, threads, lds, st); return 0;
     }
     return -1;
 }
 
-int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st) {
+// ks: the waves split K (kernel 3): rbw row blocks per workgroup, waves >= rbw
+int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, bool ks, hipStream_t st) {
     const int64_t nblk = (p.N + 15) / 16;
-    const int64_t per_wg = (int64_t)rbw * waves;
+    const int64_t per_wg = (int64_t)rbw * (ks ? 1 : waves);
     dim3 grid((unsigned)((nblk + per_wg - 1) / per_wg), (unsigned)splits);
     const int tp = gemm_tokens(T);
-    const size_t lds = gemm_lds_bytes(p.K, rbw, waves, splits, T);
+    const size_t lds = ks ? gemm_ks_lds_bytes(p.K, rbw, waves, splits, T) : gemm_lds_bytes(p.K, rbw, waves, splits, T);
+    if (ks && waves < rbw) return -1;
     int rc;
-    switch (tp) {
-        case 4: rc = launch_tp<4>(p, T, rbw, grid, waves * 64, lds, st); break;
-        case 8: rc = launch_tp<8>(p, T, rbw, grid, waves * 64, lds, st); break;
-        case 16: rc = launch_tp<16>(p, T, rbw, grid, waves * 64, lds, st); break;
+    switch (tp * 2 + (ks ? 1 : 0)) {
+        case 8: rc = launch_tp<4, false>(p, T, rbw, grid, waves * 64, lds, st); break;
+        case 9: rc = launch_tp<4, true>(p, T, rbw, grid, waves * 64, lds, st); break;
+        case 16: rc = launch_tp<8, false>(p, T, rbw, grid, waves * 64, lds, st); break;
+        case 17: rc = launch_tp<8, true>(p, T, rbw, grid, waves * 64, lds, st); break;
+        case 32: rc = launch_tp<16, false>(p, T, rbw, grid, waves * 64, lds, st); break;
+        case 33: rc = launch_tp<16, true>(p, T, rbw, grid, waves * 64, lds, st); break;
         default: return -1;
     }
     if (rc) return rc;

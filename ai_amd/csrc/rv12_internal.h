@@ -86,6 +86,17 @@ inline size_t gemm_lds_bytes(int K, int rbw, int waves, int splits, int T) {
 inline bool gemm_fits(int K, int T, int rbw, int waves, int splits) {
     return waves <= kGemmMaxWaves && gemm_lds_bytes(K, rbw, waves, splits, T) <= kGemmMaxLds;
 }
+// the waves split K (kernel 3): rbw row blocks per workgroup, every wave's
+// output sums (1 KB per row block) joined through LDS; one output row block
+// per wave for the exception sums
+inline size_t gemm_ks_lds_bytes(int K, int rbw, int waves, int splits, int T) {
+    const size_t steps = (size_t)split_steps(K, splits);
+    return steps * 3 * 64 * (size_t)gemm_tokens(T) + (size_t)waves * 16 * 16 * 4 + (size_t)waves * rbw * 1024 +
+           16 * 4 * (size_t)waves + 4 * (size_t)waves + 16 * 4 * (size_t)waves;
+}
+inline bool gemm_ks_fits(int K, int T, int rbw, int waves, int splits) {
+    return waves <= kGemmMaxWaves && waves >= rbw && gemm_ks_lds_bytes(K, rbw, waves, splits, T) <= kGemmMaxLds;
+}
 
 // --- decode-step attention (k_rope_attn)
 struct AttnParams {
@@ -125,7 +136,8 @@ constexpr int kMaxPrefillAttnTokens = 1 << 15;  // the prologue grid's second di
 int launch_prefill_attn(const AttnParams& p, hipStream_t st);
 
 int launch_gemv(const LinearParams& p, int T, int rb, int waves, int splits, hipStream_t st);
-int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, hipStream_t st);
+// ks: the waves of a workgroup split its K steps (kernel 3) instead of its rows (kernel 2)
+int launch_gemm(const LinearParams& p, int T, int rbw, int waves, int splits, bool ks, hipStream_t st);
 // workspace bytes of the launch rv12_gemm resolves (n, k, t, cfg) to; a
 // negative status where it rejects the shape or cfg
 int64_t launch_ws_bytes(int n, int k, int t, const rv12_launch* cfg);

@@ -64,6 +64,9 @@ def candidates(N, K, T):
         raw += [(1, rb, w, s) for rb in (1, 2) for w in (4, 8, 16) for s in (0, 2, 3, 4)]
     else:
         raw += [(2, rb, w, 0) for rb in (1, 2, 4) for w in (4, 8)]
+        # kernel 3 with fewer row blocks than waves (as_reference_cfg tells
+        # the two MFMA kernels apart by BN < 16 waves)
+        raw += [(3, rb, w, s) for rb in (1, 2, 4) for w in (4, 8) if rb < w for s in (0, 2)]
     out = []
     for c in raw:
         if c[3] > nsteps:
@@ -80,7 +83,7 @@ def as_reference_cfg(shape):
     """(kernel, rb, waves, splits) -> the reference's (BN, w, S): BN rows per
     workgroup, w waves, S K splits (wcomp._launch maps it back)."""
     kernel, rb, waves, splits = shape
-    bn = 16 * rb if kernel == 1 else 16 * rb * waves
+    bn = 16 * rb if kernel in (1, 3) else 16 * rb * waves
     return (bn, waves, splits)
 
 

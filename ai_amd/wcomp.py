@@ -30,7 +30,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import KERNEL_MFMA, KERNEL_VECTOR, Codec, Launch, Matrix, check, lib
+from ._lib import KERNEL_MFMA, KERNEL_MFMA_KSPLIT, KERNEL_VECTOR, Codec, Launch, Matrix, check, lib
 
 CFG1 = {}  # (N, K, MODE) -> (BN, waves) or (BN, waves, S); filled by ai_amd.tune
 CFGT = {}  # (N, K, MODE) -> (BN, waves, S); filled by ai_amd.tune
@@ -258,24 +258,29 @@ def decompress(c):
 
 def _launch(BN, w, S, T):
     """Launch struct for the reference's tuning triple.  BN = rows per
-    workgroup: row blocks of 16 per workgroup in the vector kernel (T <= 2),
-    row blocks per wave times waves in the MFMA kernel (T > 2).  A given BN
-    names its kernel; without one the library picks (rv12_launch_shape: the
-    vector kernel up to 2 tokens, except where it would have to split K at 2
-    tokens, and at 3 tokens on small matrices)."""
+    workgroup: row blocks of 16 per workgroup in the vector kernel (T <= 2);
+    above 2 tokens the MFMA kernel, with row blocks per wave times waves when
+    BN covers at least one row block per wave, else BN / 16 row blocks shared
+    by the waves, which split K between them (kernel 3).  A given BN names its
+    kernel; without one the library picks (rv12_launch_shape: the vector
+    kernel up to 2 tokens, except where it would have to split K at 2 tokens,
+    and at 3 tokens on small matrices)."""
     rb = kernel = 0
     if BN:
         vec = T <= VECTOR_TOKENS
-        per = BN // 16 if vec else BN // (16 * int(w or 8))
+        waves = int(w or 8)
+        ks = not vec and BN // 16 < waves
+        per = BN // 16 if vec or ks else BN // (16 * waves)
         rb = 1 if per <= 1 else (2 if per <= 2 else 4)
-        kernel = KERNEL_VECTOR if vec else KERNEL_MFMA
+        kernel = KERNEL_VECTOR if vec else (KERNEL_MFMA_KSPLIT if ks else KERNEL_MFMA)
     return Launch(kernel, rb, int(w or 0), int(S or 0))
 
 
 def launch_shape(N, K, T, cfg=None):
     """(kernel, rb, waves, splits) a linear of N x K at T tokens runs with for
     the Launch cfg (None: the built-in choice); kernel 1 = vector FMA, 2 =
-    bf16 MFMA (rv12_launch_shape)."""
+    bf16 MFMA with rows per wave, 3 = bf16 MFMA with K split over the waves
+    (rv12_launch_shape)."""
     c = Launch()
     check(lib().rv12_launch_shape(int(N), int(K), int(T), None if cfg is None else ctypes.byref(cfg),
                                   ctypes.byref(c)), "launch_shape")

@@ -75,10 +75,12 @@ typedef struct rv12_matrix {
 /* Launch shape of a linear.
  *   kernel  0 = built-in (rv12_launch_shape: vector up to T = 2, MFMA
  *           above), 1 = vector-FMA kernel (T <= 4), 2 = bf16-MFMA kernel
- *           (T <= 16)
+ *           (T <= 16), each wave owning its rows, 3 = the bf16-MFMA kernel
+ *           with the waves of a workgroup splitting its K steps (T <= 16)
  *   rb      vector kernel: row blocks of 16 rows per workgroup (1, 2, 4);
- *           MFMA kernel: row blocks per wave (1, 2, 4)
- *   waves   waves per workgroup (1..16)
+ *           MFMA kernel 2: row blocks per wave (1, 2, 4); kernel 3: row
+ *           blocks per workgroup (1, 2, 4; at most waves)
+ *   waves   waves per workgroup (1..16; the MFMA kernels 1..8)
  *   splits  K splits across workgroups (1..64); more than one adds a second,
  *           atomic-free pass that sums the partials in split order
  * A zero field (or a NULL pointer) selects the built-in choice for the shape

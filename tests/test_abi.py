@@ -55,7 +55,7 @@ def test_sizes():
         c = _lib.Launch()
         assert L.rv12_launch_shape(n, k, t, None if cfg is None else ctypes.byref(cfg), ctypes.byref(c)) == 0
         assert c.splits > 1 and lw(n, k, t, cfg) == L.rv12_workspace_bytes(n, k, t, c.splits)
-    assert lw(4096, 4096, 1, _lib.Launch(3, 1, 4, 2)) == 0                 # rejected: 0
+    assert lw(4096, 4096, 1, _lib.Launch(4, 1, 4, 2)) == 0                 # rejected: 0
     assert lw(4096, 100, 1) == 0 and lw(4096, 4096, 17) == 0
 
 
@@ -102,6 +102,14 @@ def test_launch_shapes():
     # the LDS (3 KB per K step at 16 tokens, 768 B at 4); an explicit split
     # whose staging does not fit is rejected
     assert shape(5120, 5120, 16, _lib.Launch(2, 2, 4, 0)) == (2, 2, 4, 11)
+    # the waves splitting K (kernel 3): row blocks per workgroup at most the
+    # waves; one workgroup stages all 5120 columns at 4 tokens (147 KB of LDS)
+    assert shape(5120, 5120, 4, _lib.Launch(3, 2, 8, 1)) == (3, 2, 8, 1)
+    c = _lib.Launch()
+    assert L.rv12_launch_shape(5120, 5120, 4, ctypes.byref(_lib.Launch(3, 4, 2, 1)),
+                               ctypes.byref(c)) == _lib.RV12_E_CONFIG     # 4 row blocks, 2 waves
+    assert L.rv12_launch_shape(5120, 5120, 8, ctypes.byref(_lib.Launch(3, 2, 8, 1)),
+                               ctypes.byref(c)) == _lib.RV12_E_CONFIG     # 8 columns: 246 KB
     assert shape(5120, 5120, 4, _lib.Launch(2, 1, 4, 1)) == (2, 1, 4, 1)    # 160 steps of 768 B
     c = _lib.Launch()
     assert L.rv12_launch_shape(5120, 5120, 16, ctypes.byref(_lib.Launch(2, 2, 4, 2)),
@@ -112,7 +120,7 @@ def test_launch_shapes():
     assert L.rv12_launch_shape(64, 100, 1, None, ctypes.byref(c)) == _lib.RV12_E_SHAPE
     assert L.rv12_launch_shape(64, 256, 17, None, ctypes.byref(c)) == _lib.RV12_E_TOKENS
     assert L.rv12_launch_shape(64, 256, 1, None, None) == _lib.RV12_E_NULL
-    assert L.rv12_launch_shape(64, 256, 1, ctypes.byref(_lib.Launch(3, 1, 4, 1)), ctypes.byref(c)) == _lib.RV12_E_CONFIG
+    assert L.rv12_launch_shape(64, 256, 1, ctypes.byref(_lib.Launch(4, 1, 4, 1)), ctypes.byref(c)) == _lib.RV12_E_CONFIG
 
 
 def _mat(n=64, k=256, tiles=0x1000, n_exc=0, rbase=0x1800):
@@ -147,7 +155,7 @@ def test_gemm_argument_errors():
     assert call(_mat(), cfg=_lib.Launch(0, 1, 17, 1)) == _lib.RV12_E_CONFIG
     assert call(_mat(), cfg=_lib.Launch(0, 1, 4, 65)) == _lib.RV12_E_CONFIG
     assert call(_mat(k=256), cfg=_lib.Launch(0, 1, 4, 9)) == _lib.RV12_E_CONFIG  # more splits than K steps
-    assert call(_mat(), cfg=_lib.Launch(3, 1, 4, 1)) == _lib.RV12_E_CONFIG       # no kernel 3
+    assert call(_mat(), cfg=_lib.Launch(4, 1, 4, 1)) == _lib.RV12_E_CONFIG       # no kernel 4
     assert call(_mat(), t=5, cfg=_lib.Launch(1, 1, 4, 1)) == _lib.RV12_E_CONFIG  # vector kernel: T <= 4
     assert call(_mat(), t=2, cfg=_lib.Launch(2, 1, 16, 1)) == _lib.RV12_E_CONFIG  # MFMA kernel: <= 8 waves
     # a split launch needs a workspace of rv12_workspace_bytes()
@@ -181,7 +189,7 @@ def test_head_argmax_argument_errors_and_workspace():
     assert call(_mat(), ii=P(0x20004)) == _lib.RV12_E_ALIGN
     assert call(_mat(), logits=P(0x50004)) == _lib.RV12_E_ALIGN
     assert call(_mat(k=100)) == _lib.RV12_E_SHAPE
-    assert call(_mat(), cfg=_lib.Launch(3, 1, 4, 1)) == _lib.RV12_E_CONFIG
+    assert call(_mat(), cfg=_lib.Launch(4, 1, 4, 1)) == _lib.RV12_E_CONFIG
     need = L.rv12_head_workspace_bytes(64, 256, 1, None)
     assert need > 0 and call(_mat(), wsb=need - 1) == _lib.RV12_E_WORKSPACE
     a = lambda b: (b + 255) // 256 * 256

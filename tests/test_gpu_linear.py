@@ -154,6 +154,14 @@ def test_shapes_and_launch_shapes(N, K):
         for T, mode, rms in ((1, 0, True), (3, 0, True), (3, 2, False), (6, 1, False), (8, 2, True), (16, 1, False),
                              (11, 2, True)):
             _check(cnp, cg, T, mode, rms, 9 + T, launch=(2, rb, w, S))
+    # the MFMA kernel with the waves splitting K (kernel 3): row blocks per
+    # workgroup up to the wave count, with and without a K split
+    for rb, w, S in [(rb, w, 0) for rb in (1, 2, 4) for w in (1, 2, 4, 8) if rb <= w] + [(1, 4, min(3, nsteps)),
+                                                                                         (2, 8, nsteps)]:
+        print("  mfma k-split-waves launch", rb, w, S, flush=True)
+        for T, mode, rms in ((1, 0, True), (3, 0, True), (4, 2, False), (6, 1, False), (8, 2, True), (16, 1, False),
+                             (11, 2, True)):
+            _check(cnp, cg, T, mode, rms, 19 + T, launch=(3, rb, w, S))
 
 
 def test_bn_must_divide_rows():
@@ -350,7 +358,8 @@ def test_activation_scale(e):
     cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
     cases = [(1, {}), (2, {}), (3, {"launch": (1, 1, 8, 0)}), (4, {"launch": (1, 1, 8, 0)}),  # vector kernel
              (3, {"launch": (2, 1, 4, 0)}), (4, {}), (6, {}), (8, {}), (16, {}),                  # MFMA kernel
-             (16, {"launch": (2, 2, 4, 0)}), (4, {"launch": (2, 1, 1, 0)})]
+             (16, {"launch": (2, 2, 4, 0)}), (4, {"launch": (2, 1, 1, 0)}),
+             (4, {"launch": (3, 2, 8, 0)}), (16, {"launch": (3, 1, 4, 0)})]                       # waves split K
     for T, kw in cases:
         use_tc = T > 1
         for mode in (0, 1, 2):
@@ -370,7 +379,7 @@ def test_activation_scale_mixed_tokens():
     W = codec.decode_f32(cnp).astype(np.float64)
     rng = np.random.default_rng(5)
     for T, kw in ((2, {}), (4, {"launch": (1, 1, 8, 0)}), (3, {"launch": (2, 1, 4, 0)}), (4, {}), (7, {}),
-                  (16, {})):
+                  (16, {}), (5, {"launch": (3, 2, 4, 0)})):
         for mode in (0, 2):
             K = cnp["K"]
             X = rng.standard_normal((T, 2 * K if mode == 2 else K))

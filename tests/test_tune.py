@@ -61,7 +61,7 @@ def test_fastest_shape_cached_and_read_back(fake, tmp_path):
 
 def test_reference_cfg_maps_back_to_the_shape():
     """wcomp._launch turns the stored (BN, w, S) back into the tuned shape."""
-    for shape, T in ((VEC[1], 1), (VEC[2], 1), (MFMA[0], 16), (MFMA[1], 16)):
+    for shape, T in ((VEC[1], 1), (VEC[2], 1), (MFMA[0], 16), (MFMA[1], 16), ((3, 2, 8, 1), 8), ((3, 1, 4, 3), 4)):
         bn, w, s = tune.as_reference_cfg(shape)
         c = wcomp._launch(bn, w, s, T)
         assert (c.kernel, c.rb, c.waves, c.splits) == shape
