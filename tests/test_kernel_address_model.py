@@ -4,7 +4,9 @@ every index a thread can compute stays inside its buffer, and every 32-bit
 byte offset or descriptor range stays below 2^32 (2^31 where the kernel
 treats it as signed).  The formulas are those of k_gemv (rv12_gemv.hip:
 steps 0-6), k_splitk_reduce, k_pick, k_rope_attn and k_attn_combine
-(rv12_attn.hip), written here from the kernels' own index expressions."""
+(rv12_attn.hip), both forms of the MFMA linear k_gemm (rv12_gemm.hip) and the
+exception epilogue of the prefill GEMM k_prefill_mm (rv12_prefill.hip),
+written here from the kernels' own index expressions."""
 import ctypes
 
 import pytest
@@ -166,3 +168,85 @@ def test_prefill_exception_epilogue_reads_inside_the_list(case):
             assert not reads
         total += len(set(reads))
     assert total == n_exc  # every entry is read, each tile its own
+
+
+def _mfma_layout_bytes(nst, TP, W, RBW, ks):
+    """End of k_gemm's LDS layout (rv12_gemm.hip): x' parts [nst][3][4 TP]
+    16-byte groups, the exception sums [W * ORB * 16 rows][16 tokens], with
+    the waves splitting K their sums [W][RBW][64] 16-byte values, then the
+    sums of squares [W][16], the range flags [W] and the slow path's
+    exponents [W][16]."""
+    G = 4 * TP
+    orb = 1 if ks else RBW
+    return nst * 3 * G * 16 + W * orb * 256 * 4 + (W * RBW * 64 * 16 if ks else 0) + W * 16 * 4 + W * 4 + W * 16 * 4
+
+
+@pytest.mark.parametrize("model", ["8b", "14b", "32b"])
+@pytest.mark.parametrize("kernel", [2, 3])
+def test_mfma_linear_addresses(model, kernel):
+    """k_gemm at the real shapes, 3..16 tokens: the built-in launch (kernel 2)
+    and kernel 3 (the waves splitting K) at every row-block count and wave
+    count the library accepts.  Every LDS index lies inside the layout, which
+    fits 160 KB; the grid covers every row block once per split; every global
+    index lies inside its buffer; the 32-bit offsets stay in range."""
+    D, H, KV, HD, FF, V = MODELS[model]
+    for name, N, K, mode, rms in _layer_linears(D, H, KV, HD, FF, V):
+        nblk, nsteps = (N + 15) // 16, K // 32
+        npad = nblk * 16
+        xs = 2 * K if mode == 2 else K
+        for T in (3, 4, 5, 8, 9, 16):
+            TP = 4 if T <= 4 else (8 if T <= 8 else 16)
+            G = 4 * TP
+            if kernel == 2:
+                shapes = [_shape(N, K, T)] if _shape(N, K, T)[0] == 2 else []
+            else:
+                shapes = []
+                for rb in (1, 2, 4):
+                    for w in (4, 8):
+                        c = _lib.Launch()
+                        if rb <= w and _lib.lib().rv12_launch_shape(N, K, T, _lib.Launch(3, rb, w, 0),
+                                                                    ctypes.byref(c)) == 0:
+                            shapes.append((c.kernel, c.rb, c.waves, c.splits))
+            for kn, RBW, W, S in shapes:
+                assert kn == kernel
+                ks = kernel == 3
+                per_wg = RBW * (1 if ks else W)
+                grid = (nblk + per_wg - 1) // per_wg
+                # every row block in exactly one workgroup of each split
+                covered = [0] * nblk
+                for bx in range(grid):
+                    for w in range(1 if ks else W):
+                        for b in range(RBW):
+                            blk = bx * per_wg + w * RBW + b
+                            if blk < nblk:
+                                covered[blk] += 1
+                assert covered == [1] * nblk, (name, T, kn, RBW, W, S)
+                for sp in range(S):
+                    s_lo, s_hi = sp * nsteps // S, (sp + 1) * nsteps // S
+                    nst = s_hi - s_lo
+                    assert (sp + 1) * nsteps < U32
+                    assert _mfma_layout_bytes(nst, TP, W, RBW, ks) <= 160 * 1024, (name, T, kn, RBW, W, S)
+                    # staging: group g < nst G at step g / G, k-group (g % G) / TP, token g % TP
+                    g_max = nst * G - 1
+                    assert (g_max // G) * 3 * G + g_max % G + 2 * G < nst * 3 * G
+                    k_max = s_lo * 32 + (g_max // G) * 32 + ((g_max % G) // TP) * 8 + 7
+                    assert k_max < K
+                    assert (T - 1) * xs + (K if mode == 2 else 0) + k_max < T * xs  # x (and u) of token T - 1
+                    # main loop: lane l reads group (l / 16) TP + l % 16 for l % 16 < TP, three parts
+                    assert 3 * TP + TP - 1 + 2 * G < 3 * G
+                    # exception x' reads: step c / 32, group ((c % 32) / 8) TP + token, element c % 8
+                    c = nst * 32 - 1
+                    o = ((c >> 5) * 3 * G + ((c & 31) >> 3) * TP + (T - 1)) * 16 + (c & 7) * 2
+                    assert o + 2 * G * 16 + 1 < nst * 3 * G * 16
+                # weights: one descriptor over the loading wave's (KS: the workgroup's) row blocks
+                blk_bytes = nsteps * 768
+                assert RBW * blk_bytes < U32 and (RBW - 1) * blk_bytes + 63 * 12 < I32
+                assert (nsteps - 1) * 768 < I32
+                # output rows: KS wave b < RBW takes row block b, its 16 rows hold every exception row index
+                orb = 1 if ks else RBW
+                assert orb * 16 * 16 <= 256 * orb  # excw [orb * 16 rows][16 tokens] of the wave
+                # y and rbase through descriptors; their 32-bit byte ranges and offsets
+                assert T * N * 4 < U32 and ((T - 1) * N + npad) * 4 < I32 and N * 4 < U32
+                if S > 1:
+                    assert ((S - 1) * T + T - 1) * npad + npad - 1 < S * T * npad
+                    assert (S + 16) * T * npad * 4 < I32
