@@ -15,12 +15,18 @@ from ._lib import Attn, check, lib
 
 
 SPAN = 80  # positions one workgroup covers at most
+LONG_SPAN = 256  # one split per kv head covers up to this many (no combine pass)
 MAX_SPLITS = 128
 
 
-def default_splits(n_kv, maxt):
-    """Position splits: each workgroup covers at most 80 positions, and there
-    are at least 256 workgroups while each keeps >= 16 positions."""
+def default_splits(n_kv, maxt, kv_bf16=True, head_dim=128):
+    """Position splits: one for a context of up to 256 positions (one
+    workgroup per kv head, no combine launch; not for float32 caches of
+    128-dim heads, whose long-span workgroup would spill registers); else
+    each workgroup covers at most 80 positions, and there are at least 256
+    workgroups while each keeps >= 16 positions."""
+    if maxt <= LONG_SPAN and (kv_bf16 or head_dim <= 64):
+        return 1
     need = -(-maxt // SPAN)
     want = min(-(-256 // n_kv), -(-maxt // 16))
     s = max(1, need, want)
@@ -35,8 +41,9 @@ class RopeAttn:
     def __init__(self, n_heads, n_kv, head_dim, maxt, kv_dtype, eps, device, splits=None):
         if kv_dtype not in (torch.float32, torch.bfloat16):
             raise ValueError("the cache must be float32 or bfloat16")
-        self.a = Attn(n_heads, n_kv, head_dim, maxt, 1 if kv_dtype == torch.bfloat16 else 0,
-                      splits or default_splits(n_kv, maxt), float(eps), float(head_dim ** -0.5))
+        bf16 = kv_dtype == torch.bfloat16
+        self.a = Attn(n_heads, n_kv, head_dim, maxt, 1 if bf16 else 0,
+                      splits or default_splits(n_kv, maxt, bf16, head_dim), float(eps), float(head_dim ** -0.5))
         need = lib().rv12_attn_workspace_bytes(ctypes.byref(self.a))
         self.ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
         need = lib().rv12_attn_batch_workspace_bytes(ctypes.byref(self.a), 16)

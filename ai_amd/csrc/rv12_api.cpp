@@ -564,9 +564,12 @@ static int check_attn(const rv12_attn* a) {
     if (g != 1 && g != 2 && g != 4 && g != 8) return RV12_E_SHAPE;
     if (a->maxt < 1) return RV12_E_SHAPE;
     if (a->splits < 1 || a->splits > kAttnMaxSplits) return RV12_E_CONFIG;
-    // a split covers at most kAttnSpan positions of 0..maxt-1
-    if ((a->maxt + a->splits - 1) / a->splits > kAttnSpan) return RV12_E_CONFIG;
-    if (attn_lds_bytes(a->head_dim, g) > kMaxLds) return RV12_E_CONFIG;
+    // a split covers at most kAttnSpan positions of 0..maxt-1; one split may
+    // cover up to kAttnLongSpan (the long-span workgroup, no combine)
+    const bool longspan = a->splits == 1 && a->maxt > kAttnSpan;
+    if (longspan ? a->maxt > kAttnLongSpan : (a->maxt + a->splits - 1) / a->splits > kAttnSpan)
+        return RV12_E_CONFIG;
+    if (attn_lds_bytes(a->head_dim, g, longspan ? kAttnLongThreads : kAttnThreads) > kMaxLds) return RV12_E_CONFIG;
     return RV12_OK;
 }
 

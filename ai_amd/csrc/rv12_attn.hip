@@ -113,16 +113,19 @@ __device__ __forceinline__ void norm_rope_wave(float a, float b, float wa, float
     }
 }
 
-template <int HD, int G, bool BF16>
-__global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
+// NT threads, 4 per position: a workgroup covers P = NT / 4 positions at
+// most (kAttnThreads = 320 over 80 positions; kAttnLongThreads = 1024 over
+// 256, one split per kv head for short contexts, so no combine pass)
+template <int HD, int G, bool BF16, int NT>
+__global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
     extern __shared__ float lds[];
-    constexpr int NW = kAttnThreads / 64;
-    constexpr int P = kAttnSpan;           // positions of one workgroup at most
+    constexpr int NW = NT / 64;
+    constexpr int P = NT / 4;              // positions of one workgroup at most
     constexpr int EB = BF16 ? 2 : 4;       // cache bytes per value
     constexpr int QD = HD / 4;             // dims per thread in the scores
     constexpr int KW = QD * EB / 16;       // 16-byte words of a thread's key quarter
     constexpr int DP = HD / 2;             // dim pairs
-    constexpr int PG = kAttnThreads / DP;  // position groups of the value sums
+    constexpr int PG = NT / DP;            // position groups of the value sums
     constexpr int PPG = P / PG;            // positions per group
     constexpr int half = HD / 2, HPW = (G + NW) / NW;
     const int g = blockIdx.x, sp = blockIdx.y, S = gridDim.y;
@@ -139,10 +142,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
     float* wacc = stat + 2 * G;     // [PG][G][HD] value sums of the position groups
     if (pos < 0 || pos >= p.maxt) {  // a position outside the cache: zeros out, no cache access
         if (S == 1) {
-            for (int o = t; o < G * HD; o += kAttnThreads) p.out[(int64_t)g * G * HD + o] = 0.0f;
+            for (int o = t; o < G * HD; o += NT) p.out[(int64_t)g * G * HD + o] = 0.0f;
         } else {  // partials that combine to zeros: acc 0, and l = 1 on split 0 only
             float* part = p.part + ((int64_t)g * S + sp) * G * (HD + 2);
-            for (int o = t; o < G * (HD + 2); o += kAttnThreads) {
+            for (int o = t; o < G * (HD + 2); o += NT) {
                 const int d = o % (HD + 2);
                 part[o] = d < HD ? 0.0f : (d == HD ? (sp == 0 ? 0.0f : -INFINITY) : (sp == 0 ? 1.0f : 0.0f));
             }
@@ -268,22 +271,31 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
     // ---- 3. softmax statistics: the scores go through LDS, then the wave
     // of each head (wave w takes the heads w, w + NW, ..) finds the split's
     // max m, the weights exp(s - m) and their sum l with wave-wide reductions
-    // only (lane j holds the positions j and j + 64)
+    // only (lane j holds the positions j, j + 64, ..)
     if (qq == 0) {
 #pragma unroll
         for (int i = 0; i < G; ++i) ss[i * P + pl] = sc[i];
     }
     __syncthreads();
-    static_assert(P > 64 && P <= 128, "two positions per lane");
+    constexpr int PL = (P + 63) / 64;  // positions per lane
+    static_assert(P > 64, "every lane holds a position");
     for (int i = wu; i < G; i += NW) {
-        const bool v1 = lane < span, v2 = lane + 64 < span;
-        const float a = ss[i * P + lane];
-        const float b = lane + 64 < P ? ss[i * P + lane + 64] : -INFINITY;
-        const float m = wave_max(fmaxf(a, b));
-        const float ea = v1 ? expf(a - m) : 0.0f, eb = v2 ? expf(b - m) : 0.0f;
-        wt[lane * G + i] = ea;
-        if (lane + 64 < P) wt[(lane + 64) * G + i] = eb;
-        const float l = wave_sum(ea + eb);
+        float a[PL];
+#pragma unroll
+        for (int j = 0; j < PL; ++j) a[j] = lane + 64 * j < P ? ss[i * P + lane + 64 * j] : -INFINITY;
+        float mx = a[0];
+#pragma unroll
+        for (int j = 1; j < PL; ++j) mx = fmaxf(mx, a[j]);
+        const float m = wave_max(mx);
+        float ls = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PL; ++j) {
+            const int jp = lane + 64 * j;
+            const float e = jp < span ? expf(a[j] - m) : 0.0f;
+            if (jp < P) wt[jp * G + i] = e;
+            ls += e;
+        }
+        const float l = wave_sum(ls);
         if (lane == 0) {
             stat[i] = m;
             stat[G + i] = l;
@@ -333,7 +345,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_rope_attn(AttnParams p) {
 
     // ---- 5. output or partials
     float* part = p.part + ((int64_t)g * S + sp) * G * (HD + 2);  // [n_kv][S][G][HD + 2]
-    for (int o = t; o < G * HD; o += kAttnThreads) {
+    for (int o = t; o < G * HD; o += NT) {
         const int i = o / HD, d = o % HD;
         float v = 0.0f;
 #pragma unroll
@@ -791,12 +803,20 @@ int launch_attn_batch(const AttnParams& p, int S, hipStream_t st) {
     return 0;
 }
 
-template <int HD, int G, bool BF16>
-static void launch_attn_t(const AttnParams& p, int S, size_t lds, hipStream_t st) {
+template <int HD, int G, bool BF16, int NT>
+static void launch_attn_nt(const AttnParams& p, int S, hipStream_t st) {
+    const size_t lds = attn_lds_bytes(HD, G, NT);
     if (lds > kDefaultLds)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_rope_attn<HD, G, BF16>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_rope_attn<HD, G, BF16, NT>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((k_rope_attn<HD, G, BF16>), dim3(p.n_kv, S), dim3(kAttnThreads), lds, st, p);
+    hipLaunchKernelGGL((k_rope_attn<HD, G, BF16, NT>), dim3(p.n_kv, S), dim3(NT), lds, st, p);
+}
+
+// one split over more than kAttnSpan positions: the long-span workgroup
+template <int HD, int G, bool BF16>
+static void launch_attn_t(const AttnParams& p, int S, size_t, hipStream_t st) {
+    if (S == 1 && p.maxt > kAttnSpan) launch_attn_nt<HD, G, BF16, kAttnLongThreads>(p, S, st);
+    else launch_attn_nt<HD, G, BF16, kAttnThreads>(p, S, st);
 }
 
 template <int HD, int G>
@@ -818,7 +838,7 @@ static int launch_attn_hd(const AttnParams& p, int G, int S, size_t lds, hipStre
 
 int launch_attn(const AttnParams& p, int S, hipStream_t st) {
     const int G = p.n_heads / p.n_kv;
-    const size_t lds = attn_lds_bytes(p.head_dim, G);
+    const size_t lds = attn_lds_bytes(p.head_dim, G, S == 1 && p.maxt > kAttnSpan ? kAttnLongThreads : kAttnThreads);
     int rc = p.head_dim == 128 ? launch_attn_hd<128>(p, G, S, lds, st)
                                : (p.head_dim == 64 ? launch_attn_hd<64>(p, G, S, lds, st) : -1);
     if (rc) return rc;

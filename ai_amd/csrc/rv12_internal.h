@@ -117,11 +117,14 @@ struct AttnParams {
 constexpr int kAttnThreads = 320;     // 4 per position of the span
 constexpr int kAttnSpan = 80;         // positions one attention workgroup covers at most
 constexpr int kAttnMaxSplits = 128;   // so the context is at most 10240 positions
-inline size_t attn_lds_bytes(int hd, int g) {
-    const size_t pg = kAttnThreads / (hd / 2);  // position groups of the value sums
-    return 4 * ((size_t)g * hd + 2 * (size_t)hd + (size_t)kAttnSpan * g + (size_t)kAttnSpan * g +
-                2 * (size_t)g +
-                pg * g * hd);
+// one split per kv head over a short context: a workgroup of 1024 threads
+// covers up to 256 positions, with no combine pass
+constexpr int kAttnLongThreads = 1024;
+constexpr int kAttnLongSpan = kAttnLongThreads / 4;
+inline size_t attn_lds_bytes(int hd, int g, int nt = kAttnThreads) {
+    const size_t pg = (size_t)nt / (hd / 2);  // position groups of the value sums
+    const size_t span = (size_t)nt / 4;
+    return 4 * ((size_t)g * hd + 2 * (size_t)hd + span * g + span * g + 2 * (size_t)g + pg * g * hd);
 }
 inline size_t attn_part_floats(int n_kv, int g, int hd, int splits) {
     return (size_t)n_kv * splits * g * (hd + 2);

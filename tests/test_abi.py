@@ -297,6 +297,8 @@ def test_attention_argument_errors():
     assert call(A(splits=129, maxt=8192)) == _lib.RV12_E_CONFIG
     assert call(A(splits=28)) == _lib.RV12_E_CONFIG          # 83 positions per split
     assert call(A(maxt=10241, splits=128)) == _lib.RV12_E_CONFIG  # 81 positions per split
+    assert call(A(maxt=257, splits=1)) == _lib.RV12_E_CONFIG    # one split covers at most 256 positions
+    assert L.rv12_attn_workspace_bytes(ctypes.byref(A(maxt=256, splits=1))) == 0  # no partials, no combine
     assert call(A(), out=None) == _lib.RV12_E_NULL
     assert call(A(), pos=None) == _lib.RV12_E_NULL
     assert call(A(), ws=0) == _lib.RV12_E_WORKSPACE

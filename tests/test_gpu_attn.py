@@ -68,6 +68,50 @@ def test_rope_attn_matches_torch(H, KV, HD, kv_dtype):
             assert torch.equal(kc[:, keep], kc0[:, keep]) and torch.equal(vc[:, keep], vc0[:, keep])
 
 
+@pytest.mark.parametrize("H,KV,HD", [(32, 8, 128), (16, 8, 128), (8, 4, 64), (64, 8, 128), (8, 8, 64)])
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16])
+def test_long_span_single_split_matches_torch(H, KV, HD, kv_dtype):
+    """A cache of up to 256 positions takes one split per kv head (the
+    1024-thread workgroup over up to 256 positions, no combine pass): against
+    the float64 reference at positions inside and past the first 80, with the
+    cache slot written as in the split kernel, and equal within float32
+    rounding to the same step over 5 splits."""
+    from ai_amd.attn import RopeAttn, default_splits
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(H * 10 + HD + 7)
+    eps = 1e-6
+    inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+    qn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    kn = (1 + 0.1 * torch.randn(HD, device=dev, generator=g))
+    for maxt in (81, 192, 256):
+        assert default_splits(KV, maxt) == 1
+        att = RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev, splits=1)
+        split = RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev, splits=5)
+        for pos in (0, 1, 63, 64, 79, 80, 130, maxt - 1):
+            if pos >= maxt:
+                continue
+            print("case", H, KV, HD, kv_dtype, maxt, pos, flush=True)
+            qkv = torch.randn((H + 2 * KV) * HD, device=dev, generator=g) * 3
+            kc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+            vc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+            kc0, vc0 = kc.clone(), vc.clone()
+            out = torch.zeros(H * HD, device=dev)
+            att(qkv, qn, kn, inv, torch.tensor([pos], device=dev), kc, vc, out)
+            k5, v5 = kc0.clone(), vc0.clone()
+            o5 = torch.zeros(H * HD, device=dev)
+            split(qkv, qn, kn, inv, torch.tensor([pos], device=dev), k5, v5, o5)
+            torch.cuda.synchronize()
+            ref, kr, vr = _torch_ref(qkv, qn, kn, inv, pos, kc0, vc0, H, KV, HD, eps, k_at_pos=kc[:, pos].clone())
+            assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), float((out - ref).abs().max())
+            assert torch.allclose(out, o5, rtol=1e-5, atol=1e-6), float((out - o5).abs().max())
+            tol = 2.0 ** -7 if kv_dtype == torch.bfloat16 else 1e-5  # one bf16 ulp
+            assert torch.allclose(kc[:, pos].float(), kr.float(), rtol=tol, atol=1e-6)
+            assert torch.equal(vc[:, pos].float(), vr.float())
+            keep = torch.ones(maxt, dtype=torch.bool)
+            keep[pos] = False
+            assert torch.equal(kc[:, keep], kc0[:, keep]) and torch.equal(vc[:, keep], vc0[:, keep])
+
+
 def test_position_outside_cache_gives_zeros():
     from ai_amd.attn import RopeAttn
     dev = "cuda"
@@ -113,7 +157,7 @@ def test_single_split_and_split_limits():
     torch.cuda.synchronize()
     assert torch.allclose(outs[0], outs[1], rtol=1e-5, atol=1e-6)
     assert torch.allclose(outs[0], outs[2], rtol=1e-5, atol=1e-6)
-    for mt, splits in ((300, 2), (10241, 128), (300, 129)):
+    for mt, splits in ((300, 2), (10241, 128), (300, 129), (257, 1)):  # one split: at most 256 positions
         with pytest.raises(ValueError):
             RopeAttn(H, KV, HD, mt, torch.float32, 1e-6, dev, splits=splits)(
                 qkv, ones, ones, inv, torch.tensor([0], device=dev), kc, vc, torch.zeros(H * HD, device=dev))

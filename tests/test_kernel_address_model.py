@@ -83,6 +83,30 @@ def test_vector_linear_addresses(model, T):
 
 
 @pytest.mark.parametrize("model", sorted(MODELS))
+def test_decode_attention_long_span_addresses(model):
+    """One split per kv head over a short cache (the 1024-thread workgroup,
+    up to 256 positions): the positions its threads address stay inside
+    the span, the cache rows inside the cache, the offsets in 32 bits."""
+    D, H, KV, HD, FF, V = MODELS[model]
+    from ai_amd.attn import LONG_SPAN, default_splits
+    NT, P = 1024, 256
+    assert P == LONG_SPAN
+    for maxt, eb in ((81, 2), (192, 2), (256, 2), (256, 4)):
+        S = default_splits(KV, maxt, eb == 2, HD)
+        if S != 1:
+            continue
+        for pos in (0, maxt // 2, maxt - 1):
+            n = pos + 1
+            lo, hi = 0, n
+            assert hi - lo <= P
+            # score threads: position t / 4 < P; value threads: group t / (HD / 2) of P / groups positions
+            groups = NT // (HD // 2)
+            assert (NT - 1) // 4 < P and (groups - 1) * (P // groups) + P // groups - 1 < P
+            assert ((lo + P - 1) * HD + HD - 1) * eb < I32 and min(hi, n - 1) * HD * eb < U32
+            assert (KV - 1) * maxt * HD + pos * HD + HD - 1 < KV * maxt * HD
+
+
+@pytest.mark.parametrize("model", sorted(MODELS))
 def test_decode_attention_addresses(model):
     D, H, KV, HD, FF, V = MODELS[model]
     from ai_amd.attn import SPAN, default_splits
