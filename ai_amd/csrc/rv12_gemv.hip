@@ -136,11 +136,13 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
 #pragma unroll
     for (int u = 0; u < D; ++u) issue_step<RB>(buf[u], rv, rnull, voff, s0 + u * W, s_hi);
 
-    // the workgroup's exception range (scalar loads of the row pointers; its
-    // first round of entries is loaded after the x' staging, so that the wait
-    // for these pointers does not hold up the staging)
-    const int32_t e_lo = p.rp[n0];
-    const int32_t e_hi = p.rp[min(n0 + RB * 16, p.N)];
+    // the workgroup's exception range, from the row pointers of step 0 (vector
+    // loads issued before the activations): in every wave lane 0 holds
+    // rp[n0] and lane 16 RB - 1 holds rp[min(n0 + 16 RB, N)].  Scalar loads of
+    // the same two words would be waited for at the barrier after the
+    // staging, and under the weight stream a scalar miss takes about 1 us.
+    const int32_t e_lo = __builtin_amdgcn_readlane(oe0, 0);
+    const int32_t e_hi = __builtin_amdgcn_readlane(oe1, RB * 16 - 1);
 
     // ---- 3. x' * 2^64 into LDS (the fast path's scale), with the exponent
     // range of the x' values and, for RMS, the sums of (x 2^-32)^2

@@ -74,3 +74,158 @@ extern "C" int rv12_probe_stream(const void* tiles, int n, int k, int rb, int wa
 #undef RV12_PROBE
     return hipGetLastError() == hipSuccess ? 0 : -20;
 }
+
+namespace rv12 {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef const __attribute__((address_space(4))) f32x16 cf32x16;
+
+// Arrival of the activations inside one launch of the vector linear's shape
+// at one token (one row block per workgroup, D = 6 weight steps in flight
+// per wave).  Every workgroup stages the K activations into LDS, then
+// streams its weights (WS) and folds them with the staged values; lane 0 of
+// each wave records the 100 MHz real-time counter at entry, after the
+// workgroup barrier that ends the staging, and at the end.
+// SC = false: vector loads, NX float4 chunks per thread issued before the
+//   weight prefetch and written to LDS after it (the linear's order);
+// SC = true: scalar loads (a uniform address in the constant address space),
+//   each wave 32-float pieces of its K / W slice, two pieces in flight (scalar
+//   loads return out of order, so the wave waits for both), each
+//   piece moved to VGPRs of lane 0 (v_mov from the SGPRs) and written with
+//   eight 16-byte LDS stores; the weight prefetch is issued after the first
+//   two pieces.
+// Host conditions: K == 4 * NX * 64 * W, K <= 16384 (LDS of K floats).
+template <bool SC, bool WS, int NX>
+__global__ __launch_bounds__(1024) void k_arrival(const uint32_t* __restrict__ tiles, int N, int K,
+                                                  const float* __restrict__ x, uint32_t* __restrict__ out,
+                                                  uint64_t* __restrict__ ts) {
+    constexpr int D = 6;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    extern __shared__ float xl[];
+    const int W = blockDim.x >> 6;
+    const int nthr = blockDim.x;
+    const int lane = threadIdx.x & 63;
+    const int wu = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nsteps = K >> 5;
+    const int64_t nblk = (N + 15) / 16;
+    const int64_t blk0 = blockIdx.x;
+    const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
+    const char* wbase = reinterpret_cast<const char*>(tiles) + blk0 * (int64_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, blk0 < nblk ? blk_bytes : 0u);
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(wbase, 0u);
+    const int voff = lane * 12;
+    const int s0 = wu;
+    u32x3 buf[D];
+    auto prefetch = [&]() {
+        if constexpr (WS) {
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                const int s = s0 + u * W;
+                buf[u] = load_group(s < nsteps ? rv : rnull, voff, (s < nsteps ? s : 0) * kStepBytes);
+            }
+        }
+    };
+    if constexpr (!SC) {
+        f32x4 xr[NX];
+#pragma unroll
+        for (int j = 0; j < NX; ++j) xr[j] = *reinterpret_cast<const f32x4*>(x + (threadIdx.x + j * nthr) * 4);
+        __builtin_amdgcn_s_barrier();
+        prefetch();
+#pragma unroll
+        for (int j = 0; j < NX; ++j) *reinterpret_cast<f32x4*>(xl + (threadIdx.x + j * nthr) * 4) = xr[j] * kXScale;
+    } else {
+        const int sl = K / W;  // floats of this wave's slice, a multiple of 64
+        const cf32x16* cx = (const cf32x16*)(x + (int64_t)wu * sl);
+        float* xw = xl + wu * sl;
+        auto put = [&](f32x16 a, f32x16 b, int c) {
+            if (lane == 0) {
+                f32x4* dst = reinterpret_cast<f32x4*>(xw + c * 32);
+#pragma unroll
+                for (int g = 0; g < 4; ++g) dst[g] = f32x4{a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]} * kXScale;
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    dst[4 + g] = f32x4{b[4 * g], b[4 * g + 1], b[4 * g + 2], b[4 * g + 3]} * kXScale;
+            }
+        };
+        const int np = sl / 32;  // even
+        // the loads are written as asm so that the compiler issues them here,
+        // before the barrier and the weight prefetch (it would sink loads of
+        // the constant address space past both); the asm wait below ties the
+        // four values, so no use of them is scheduled before it
+        f32x16 a0, b0, a1, b1;
+        auto load4 = [&](const cf32x16* src) {
+            asm volatile("s_load_dwordx16 %0, %4, 0x0\n\t"
+                         "s_load_dwordx16 %1, %4, 0x40\n\t"
+                         "s_load_dwordx16 %2, %4, 0x80\n\t"
+                         "s_load_dwordx16 %3, %4, 0xc0"
+                         : "=s"(a0), "=s"(b0), "=s"(a1), "=s"(b1)
+                         : "s"(src)
+                         : "memory");
+        };
+        load4(cx);
+        asm volatile("s_barrier" ::: "memory");
+        prefetch();
+        for (int c = 0; c < np; c += 2) {
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(a0), "+s"(b0), "+s"(a1), "+s"(b1)::"memory");
+            put(a0, b0, c);
+            put(a1, b1, c + 1);
+            if (c + 2 < np) load4(cx + 2 * c + 4);
+        }
+    }
+    __syncthreads();
+    const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+    uint32_t acc = 0;
+    if constexpr (WS) {
+        const int rounds = ((nsteps - s0 + W - 1) / W + D - 1) / D;
+        for (int rr = 0; rr < rounds; ++rr) {
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                const int s = s0 + (rr * D + u) * W;
+                acc ^= buf[u].x ^ buf[u].y ^ buf[u].z ^ __float_as_uint(xl[(s < nsteps ? s : 0) * 32 + (lane & 31)]);
+                const int sn = s + D * W;
+                buf[u] = load_group(sn < nsteps ? rv : rnull, voff, (sn < nsteps ? sn : 0) * kStepBytes);
+            }
+        }
+    } else {
+        acc = __float_as_uint(xl[threadIdx.x % K]);
+    }
+    out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+    const uint64_t t2 = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0) {
+        uint64_t* tw = ts + ((int64_t)blockIdx.x * W + wu) * 3;
+        tw[0] = t0;
+        tw[1] = t1;
+        tw[2] = t2;
+    }
+}
+
+}  // namespace rv12
+
+// mode bit 0: scalar staging; bit 1: with the weight stream.  ts receives
+// three 100 MHz counter values per wave: [workgroup][wave][entry, staged, end]
+extern "C" int rv12_probe_arrival(const void* tiles, int n, int k, int waves, int mode, const void* x, void* out,
+                                  void* ts, void* stream) {
+    using namespace rv12;
+    if (!tiles || !x || !out || !ts || n < 1 || k < 32 || k > 16384 || waves < 1 || waves > 16 ||
+        k % (64 * waves) || mode < 0 || mode > 3)
+        return -1;
+    const int nx = k / (256 * waves);  // float4 chunks per thread
+    if (nx < 1 || nx > 4 || nx * 256 * waves != k) return -1;
+    const dim3 grid((unsigned)(((int64_t)n + 15) / 16)), block((unsigned)(waves * 64));
+    const size_t lds = (size_t)k * 4;
+    hipStream_t st = (hipStream_t)stream;
+#define RV12_ARR(S, WW, X) hipLaunchKernelGGL((k_arrival<S, WW, X>), grid, block, lds, st, (const uint32_t*)tiles, n, \
+                                              k, (const float*)x, (uint32_t*)out, (uint64_t*)ts)
+#define RV12_ARR_X(S, WW)                 \
+    if (nx == 1) RV12_ARR(S, WW, 1);      \
+    else if (nx == 2) RV12_ARR(S, WW, 2); \
+    else if (nx == 3) RV12_ARR(S, WW, 3); \
+    else RV12_ARR(S, WW, 4);
+    if (mode == 0) { RV12_ARR_X(false, false) }
+    else if (mode == 1) { RV12_ARR_X(true, false) }
+    else if (mode == 2) { RV12_ARR_X(false, true) }
+    else { RV12_ARR_X(true, true) }
+#undef RV12_ARR_X
+#undef RV12_ARR
+    return hipGetLastError() == hipSuccess ? 0 : -20;
+}

@@ -408,6 +408,76 @@ def stream_ceiling(cs, N, K, reps):
     return {"stream_us": ms * 1e3, "stream_GBs": tb / ms / 1e6, "stream_frac_peak": tb / ms / 1e6 / PEAK_HBM}
 
 
+ARRIVAL_MODES = {0: "vector, alone", 1: "scalar, alone", 2: "vector, weight stream", 3: "scalar, weight stream"}
+
+
+def arrival(dev, shapes=(("q_o", 4096, 4096, 8), ("k_v", 1024, 4096, 8)), min_bytes=1.0e9):
+    """When the activations reach LDS inside one launch of the vector linear's
+    one-token shape (ai_amd/csrc/rv12_probe.hip, k_arrival): each workgroup
+    stages the K floats with vector loads (the linear's way) or with scalar
+    loads of 64 bytes (two 128-byte pieces in flight per wave), alone or
+    followed by the weight stream of its row block (6 steps in flight per
+    wave).  Weights are random bytes of the 12-bit size, distinct copies over
+    >= 1 GB; each launch reads its own activation vector, written by a copy
+    kernel just before it, as the engine's previous launch writes it.  Per
+    wave the 100 MHz real-time counter is read at entry, after the barrier
+    that ends the staging, and at the end; times are from the launch's
+    earliest entry."""
+    import ctypes
+    from ai_amd import build
+    if not os.path.exists(build.PROBE_OUT):
+        raise RuntimeError("librv12probe.so is not built")
+    P = ctypes.CDLL(build.PROBE_OUT)
+    P.rv12_probe_arrival.restype = ctypes.c_int
+    P.rv12_probe_arrival.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    out = []
+    for name, N, K, W in shapes:
+        nbytes = N * K * 3 // 2
+        ncopy = max(2, int(np.ceil(min_bytes / nbytes)))
+        g = torch.Generator(device=dev).manual_seed(11)
+        ws = [torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev, generator=g)
+              for _ in range(ncopy)]
+        xsrc = torch.randn(K, device=dev, generator=g)
+        xs = [torch.empty(K, device=dev) for _ in range(ncopy)]
+        nwg = (N + 15) // 16
+        sink = torch.empty(nwg * W * 64, dtype=torch.int32, device=dev)
+        ts = torch.zeros(ncopy, nwg, W, 3, dtype=torch.int64, device=dev)
+        for mode, what in ARRIVAL_MODES.items():
+            def fn():
+                st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                for i in range(ncopy):
+                    xs[i].copy_(xsrc)
+                    rc = P.rv12_probe_arrival(ctypes.c_void_p(ws[i].data_ptr()), N, K, W, mode,
+                                              ctypes.c_void_p(xs[i].data_ptr()), ctypes.c_void_p(sink.data_ptr()),
+                                              ctypes.c_void_p(ts[i].data_ptr()), st)
+                    assert rc == 0, rc
+
+            graph = Graph(fn)
+            for _ in range(3):
+                graph.replay()
+            torch.cuda.synchronize()
+            t = ts.cpu().numpy().astype(np.int64)
+            del graph
+            base = t[:, :, :, 0].min(axis=(1, 2))[:, None]  # earliest entry of each launch
+            arr = (t[:, :, :, 1].max(axis=2) - base) * 0.01  # per workgroup, us
+            own = (t[:, :, :, 1].max(axis=2) - t[:, :, :, 0].min(axis=2)) * 0.01
+            end = (t[:, :, :, 2].max(axis=(1, 2)) - base[:, 0]) * 0.01
+            r = {"shape": name, "N": N, "K": K, "waves": W, "workgroups": nwg, "launches": ncopy, "mode": mode,
+                 "staging": what, "arrive_us_median": round(float(np.median(arr)), 3),
+                 "arrive_us_p90": round(float(np.percentile(arr, 90)), 3),
+                 "arrive_us_max": round(float(arr.max(axis=1).mean()), 3),
+                 "arrive_from_own_entry_us_median": round(float(np.median(own)), 3),
+                 "launch_span_us_median": round(float(np.median(end)), 3)}
+            out.append(r)
+            print(f"# arrival {name} {what}: median {r['arrive_us_median']:.2f} us, p90 {r['arrive_us_p90']:.2f}, "
+                  f"last {r['arrive_us_max']:.2f}; span {r['launch_span_us_median']:.2f} us", file=sys.stderr,
+                  flush=True)
+        del ws, xs
+        torch.cuda.empty_cache()
+    return out
+
+
 def run_skinny(name, reps, dev, min_bytes=1.2e9):
     """Qwen3-14B skinny-GEMM entry: one shape at every M of SWEEP_M, weights
     N(0, 0.02) bf16 with 0.1% of output rows x20, distinct copies totalling
@@ -586,6 +656,8 @@ def main():
                     help="run only the Qwen3-8B end-to-end decode (2048-token prompt, 256 tokens; for profiling)")
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only the Qwen3-8B blocked prefill of a 2048-token prompt, 3 times (for profiling)")
+    ap.add_argument("--only-arrival", action="store_true",
+                    help="run only the activation-arrival probe (vector against scalar staging, q/o and k/v shapes)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (scale factor of the HBM byte counters)")
     args = ap.parse_args()
@@ -616,6 +688,9 @@ def main():
         return
     if args.only_prefill:
         print(json.dumps(run_prefill(dev)), flush=True)
+        return
+    if args.only_arrival:
+        print(json.dumps(arrival(dev)), flush=True)
         return
 
     tok = run_token_bench(args, dev)

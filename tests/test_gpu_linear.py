@@ -368,6 +368,53 @@ def test_activation_scale(e):
         _check_scaled(cnp, cg, T, 2, False, 90 + T, e, both_halves=True, use_tc=use_tc, **kw)
 
 
+STEP_SCALES = {"huge": {3: 70, 17: 70}, "tiny": {0: -80, 9: -80, 30: -75},
+               "mixed": {5: 70, 12: -80, 13: -30, 21: 40}}
+
+
+@pytest.mark.parametrize("pattern", sorted(STEP_SCALES))
+def test_activation_scale_in_some_steps(pattern):
+    """Activation columns outside the fast path's range in a few 32-column K
+    steps only (2^70 or 2^-80 against N(0, 1) elsewhere; in MODE 2 the u half
+    carries the scale).  In the vector kernel each wave stages the columns of
+    its own steps, so only the waves owning those steps take their own scale,
+    and the epilogue brings every wave's sum (and the exception products of
+    those columns: 2 % of the columns are outliers) to one scale.  Held to 4x
+    the fp32 forward-error bound."""
+    from ai_amd import wcomp
+    print("pattern", pattern, flush=True)
+    bits = _random_matrix(300, 1024, 4242, out_rows=0.01, out_cols=0.02)
+    cnp = codec.compress(bits)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    K, N = cnp["K"], cnp["N"]
+    colexp = np.zeros(K)
+    for s, e in STEP_SCALES[pattern].items():
+        colexp[32 * s:32 * s + 32] = e
+    W = codec.decode_f32(cnp).astype(np.float64)
+    cases = [(1, {}), (2, {}), (1, {"launch": (1, 1, 16, 0)}), (3, {"launch": (1, 1, 8, 0)}),
+             (4, {"launch": (1, 1, 4, 0)}), (2, {"launch": (1, 1, 4, 2)}), (1, {"launch": (1, 2, 8, 3)})]
+    for i, (T, kw) in enumerate(cases):
+        for mode in (0, 1, 2):
+            for rms in (False, True):
+                rng = np.random.default_rng(1000 * i + 10 * mode + rms)
+                X = rng.standard_normal((T, 2 * K if mode == 2 else K))
+                X[:, -K:] *= 2.0 ** colexp
+                X = X.astype(np.float32)
+                lnw = codec.f32_to_bf16_rne((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)) if rms else None
+                lw = None if lnw is None else codec.bf16_to_f32(lnw)
+                xp = linear.prologue(X, K, mode, lw)
+                typ = float(np.abs(xp @ W.T).mean()) or 1.0
+                Y0 = (rng.standard_normal((T, N)) * typ).astype(np.float32)
+                ref = linear.linear(cnp, X, mode, Y0, lnw=lw, W=W)
+                bound = linear.error_bound(cnp, X, mode, lnw=lw, W=W)
+                y = _run(cg, X, Y0, mode, T, lnw=lnw, use_tc=T > 1, **kw).astype(np.float64)
+                assert np.all(np.isfinite(y)) and np.all(np.isfinite(ref)), (T, kw, mode, rms)
+                err = np.abs(y - ref)
+                tight = 4 * bound + 2.0 ** -23 * np.abs(ref) + 1e-300
+                bad = err > tight
+                assert not bad.any(), (pattern, T, kw, mode, rms, float(err[bad].max()), float(tight[bad].min()))
+
+
 def test_activation_scale_mixed_tokens():
     """Tokens of very different scales in one batch (2^-50, 1, 2^50, and one
     token of zeros): each keeps the fp32 bound (the MFMA kernel's scale is
