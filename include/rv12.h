@@ -262,8 +262,10 @@ int rv12_decode_rows(const rv12_matrix* w, int first, int last, void* out, int o
  * *pos is read on the device, so a captured graph can advance it; a *pos
  * outside [0, maxt) gives zeros and touches no cache.  The positions are spread
  * over `splits` workgroups per kv head, each covering at most 80 of them (so
- * splits >= maxt / 80, at most 128: maxt <= 10240); splits > 1 adds a combine
- * pass over partials in the workspace (rv12_attn_workspace_bytes).  Calls
+ * splits >= maxt / 80, at most 128: maxt <= 10240), or, with splits == 1 and
+ * maxt <= 256, one workgroup of 1024 threads per kv head covering them all;
+ * splits > 1 adds a combine pass over partials in the workspace
+ * (rv12_attn_workspace_bytes).  Calls
  * sharing a workspace must be ordered on one stream.  Replaces rope_attn_k,
  * ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213. */
 typedef struct rv12_attn {
