@@ -368,6 +368,47 @@ def test_activation_scale(e):
         _check_scaled(cnp, cg, T, 2, False, 90 + T, e, both_halves=True, use_tc=use_tc, **kw)
 
 
+def test_random_draws_of_the_launch_space():
+    """64 seeded draws of matrix, token count (1-16), MODE, RMS prologue and
+    launch (kernel 0-3, row blocks, waves, splits, each possibly left to the
+    library): every draw rv12_launch_shape accepts runs through rv12_gemm and
+    is held to the oracle's closed form and the fp32 bound; a draw it rejects
+    is skipped.  Matrices of odd row counts (one partial row block) and 2%
+    outlier rows and columns."""
+    import ctypes
+    from ai_amd import _lib, wcomp
+    L = _lib.lib()
+    rng = np.random.default_rng(2026)
+    pool = []
+    for i, (N, K) in enumerate([(37, 256), (300, 512), (129, 1024), (513, 768), (64, 2048), (250, 1536)]):
+        bits = _random_matrix(N, K, 900 + i, out_rows=0.02, out_cols=0.02)
+        cnp = codec.compress(bits)
+        cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+        pool.append((cnp, cg, codec.decode_f32(cnp).astype(np.float64)))
+    ran, kernels = 0, set()
+    for d in range(64):
+        cnp, cg, W = pool[int(rng.integers(len(pool)))]
+        N, K = cnp["N"], cnp["K"]
+        T = int(rng.integers(1, 17))
+        mode = int(rng.integers(0, 3))
+        rms = bool(rng.integers(0, 2))
+        launch = (int(rng.choice([0, 1, 2, 3])), int(rng.choice([0, 1, 2, 4])), int(rng.choice([0, 1, 2, 4, 8, 16])),
+                  int(rng.choice([0, 0, 1, 2, 3, 5, 8])))
+        out = _lib.Launch()
+        if L.rv12_launch_shape(N, K, T, ctypes.byref(_lib.Launch(*launch)), ctypes.byref(out)):
+            continue
+        print("draw", d, N, K, T, mode, rms, launch, "->", (out.kernel, out.rb, out.waves, out.splits), flush=True)
+        X, Y0, lnw = _inputs(cnp, T, mode, 5000 + d, rms)
+        lw = None if lnw is None else codec.bf16_to_f32(lnw)
+        ref = linear.linear(cnp, X, mode, Y0, lnw=lw, W=W)
+        bound = linear.error_bound(cnp, X, mode, lnw=lw, W=W)
+        y = _run(cg, X, Y0, mode, T, lnw=lnw, launch=launch)
+        _close(y, ref, bound, (d, N, K, T, mode, rms, launch))
+        ran += 1
+        kernels.add(out.kernel)
+    assert ran >= 32 and kernels == {1, 2, 3}, (ran, kernels)
+
+
 STEP_SCALES = {"huge": {3: 70, 17: 70}, "tiny": {0: -80, 9: -80, 30: -75},
                "mixed": {5: 70, 12: -80, 13: -30, 21: 40}}
 
