@@ -163,6 +163,46 @@ def test_single_split_and_split_limits():
                 qkv, ones, ones, inv, torch.tensor([0], device=dev), kc, vc, torch.zeros(H * HD, device=dev))
 
 
+def test_random_draws_of_positions_and_splits():
+    """48 seeded draws of head layout, head size, cache dtype, cache length
+    (1-2048), position and split count over the range the library accepts
+    (one split up to 256 positions, else at most 80 positions per split and
+    at most 128 splits), each against the float64 reference; the step's
+    value lands in its cache slot."""
+    import numpy as np
+    from ai_amd.attn import RopeAttn, default_splits
+    dev = "cuda"
+    eps = 1e-6
+    rng = np.random.default_rng(77)
+    layouts = [(32, 8, 128), (16, 8, 128), (8, 4, 64), (64, 8, 128), (8, 8, 64), (4, 1, 128), (16, 2, 64)]
+    for d in range(48):
+        H, KV, HD = layouts[int(rng.integers(len(layouts)))]
+        kv_dtype = torch.bfloat16 if rng.integers(2) else torch.float32
+        maxt = int(rng.integers(1, 2049))
+        lo = -(-maxt // 80)
+        choices = [default_splits(KV, maxt, kv_dtype == torch.bfloat16, HD), lo, min(128, lo + int(rng.integers(0, 40)))]
+        if maxt <= 256:
+            choices.append(1)
+        splits = int(choices[int(rng.integers(len(choices)))])
+        pos = int(rng.integers(0, maxt))
+        print("draw", d, H, KV, HD, kv_dtype, maxt, splits, pos, flush=True)
+        g = torch.Generator(device=dev).manual_seed(700 + d)
+        inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+        qn = 1 + 0.1 * torch.randn(HD, device=dev, generator=g)
+        kn = 1 + 0.1 * torch.randn(HD, device=dev, generator=g)
+        qkv = torch.randn((H + 2 * KV) * HD, device=dev, generator=g) * 3
+        kc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+        vc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+        kc0, vc0 = kc.clone(), vc.clone()
+        out = torch.zeros(H * HD, device=dev)
+        RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev, splits=splits)(
+            qkv, qn, kn, inv, torch.tensor([pos], device=dev), kc, vc, out)
+        torch.cuda.synchronize()
+        ref, kr, vr = _torch_ref(qkv, qn, kn, inv, pos, kc0, vc0, H, KV, HD, eps, k_at_pos=kc[:, pos].clone())
+        assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), (d, float((out - ref).abs().max()))
+        assert torch.equal(vc[:, pos].float(), vr.float()), d
+
+
 def test_long_cache_many_splits():
     """10240 positions over 128 splits, bf16 cache, against the float64
     reference at a few positions."""
