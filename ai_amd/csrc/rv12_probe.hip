@@ -54,7 +54,60 @@ __global__ __launch_bounds__(1024) void k_stream(const uint32_t* __restrict__ ti
     out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
 }
 
+// The same stream with 16-byte loads: the row block's bytes in 3 KB chunks
+// (four steps of 768 bytes), chunk c read by wave c % W as three 1 KB loads
+// (lane l the 16 bytes at 16 l of each), D chunks in flight per wave (D = 2
+// holds the bytes of 8 steps).  Host condition: K % 128 == 0.
+template <int D>
+__global__ __launch_bounds__(1024) void k_stream16(const uint32_t* __restrict__ tiles, int N, int K,
+                                                   uint32_t* __restrict__ out) {
+    const int W = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wu = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nchunk = K >> 7;
+    const int64_t nblk = (N + 15) / 16;
+    const int64_t blk0 = blockIdx.x;
+    const uint32_t blk_bytes = (uint32_t)(K >> 5) * kStepBytes;
+    const char* wbase = reinterpret_cast<const char*>(tiles) + blk0 * (int64_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, blk0 < nblk ? blk_bytes : 0u);
+    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(wbase, 0u);
+    u32x4 buf[D][3];
+    auto issue = [&](u32x4 (&b)[3], int c) {
+        const __amdgpu_buffer_rsrc_t r = c < nchunk ? rv : rnull;
+        const int soff = (c < nchunk ? c : 0) * 3072;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            b[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, i * 1024 + lane * 16, soff,
+                                                                                   kNonTemporal));
+    };
+#pragma unroll
+    for (int u = 0; u < D; ++u) issue(buf[u], wu + u * W);
+    uint32_t acc = 0;
+    const int rounds = ((nchunk - wu + W - 1) / W + D - 1) / D;
+    for (int rr = 0; rr < rounds; ++rr) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+#pragma unroll
+            for (int i = 0; i < 3; ++i) acc ^= buf[u][i].x ^ buf[u][i].y ^ buf[u][i].z ^ buf[u][i].w;
+            issue(buf[u], wu + (rr * D + u + D) * W);
+        }
+    }
+    out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
 }  // namespace rv12
+
+extern "C" int rv12_probe_stream16(const void* tiles, int n, int k, int waves, int depth, void* out, void* stream) {
+    using namespace rv12;
+    if (!tiles || !out || n < 1 || k < 128 || k % 128 || waves < 1 || waves > 16) return -1;
+    const dim3 grid((unsigned)(((int64_t)n + 15) / 16)), block((unsigned)(waves * 64));
+    hipStream_t st = (hipStream_t)stream;
+    if (depth == 1) hipLaunchKernelGGL((k_stream16<1>), grid, block, 0, st, (const uint32_t*)tiles, n, k, (uint32_t*)out);
+    else if (depth == 2) hipLaunchKernelGGL((k_stream16<2>), grid, block, 0, st, (const uint32_t*)tiles, n, k, (uint32_t*)out);
+    else if (depth == 3) hipLaunchKernelGGL((k_stream16<3>), grid, block, 0, st, (const uint32_t*)tiles, n, k, (uint32_t*)out);
+    else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -20;
+}
 
 extern "C" int rv12_probe_stream(const void* tiles, int n, int k, int rb, int waves, int depth, void* out,
                                  void* stream) {

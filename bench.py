@@ -478,6 +478,61 @@ def arrival(dev, shapes=(("q_o", 4096, 4096, 8), ("k_v", 1024, 4096, 8)), min_by
     return out
 
 
+LOAD_WIDTH_SHAPES = (("q_o", 4096, 4096, 8), ("qkv", 6144, 4096, 8), ("down", 4096, 12288, 16),
+                     ("gu", 24576, 4096, 4), ("lm_head", 151936, 4096, 8))
+
+
+def load_width(dev, reps=10, min_bytes=1.2e9):
+    """The pure weight stream of one row block per workgroup read with the
+    layout's 12-byte loads (k_stream: 6 of them, 768 bytes, per wave and K
+    step) against 16-byte loads of the same bytes (k_stream16: the row
+    block's bytes in 3 KB chunks, three 1 KB loads each), at 3, 4.5-6 and
+    6-9 KB in flight per wave, over >= 1.2 GB of distinct random byte
+    copies per shape (ai_amd/csrc/rv12_probe.hip)."""
+    import ctypes
+    from ai_amd import build
+    P = ctypes.CDLL(build.PROBE_OUT)
+    for f in (P.rv12_probe_stream, P.rv12_probe_stream16):
+        f.restype = ctypes.c_int
+    P.rv12_probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    P.rv12_probe_stream16.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_void_p, ctypes.c_void_p]
+    res = []
+    for name, N, K, W in LOAD_WIDTH_SHAPES:
+        nb = N * K * 3 // 2
+        ncopy = max(2, int(np.ceil(min_bytes / nb)))
+        g = torch.Generator(device=dev).manual_seed(21)
+        ws = [torch.randint(-2**31, 2**31 - 1, (nb // 4,), dtype=torch.int32, device=dev, generator=g)
+              for _ in range(ncopy)]
+        out = torch.empty(((N + 15) // 16) * 16 * 64, dtype=torch.int32, device=dev)
+        for kind, depths in (("12-byte", (4, 6, 8)), ("16-byte", (1, 2, 3))):
+            for d in depths:
+                def fn():
+                    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                    for w in ws:
+                        if kind == "12-byte":
+                            rc = P.rv12_probe_stream(ctypes.c_void_p(w.data_ptr()), N, K, 1, W, d,
+                                                     ctypes.c_void_p(out.data_ptr()), st)
+                        else:
+                            rc = P.rv12_probe_stream16(ctypes.c_void_p(w.data_ptr()), N, K, W, d,
+                                                       ctypes.c_void_p(out.data_ptr()), st)
+                        assert rc == 0, rc
+
+                graph = Graph(fn)
+                us = time_graph(graph, reps) / ncopy * 1e3
+                del graph
+                r = {"shape": name, "loads": kind, "waves": W, "depth": d,
+                     "KB_in_flight_per_wave": round((768 * d if kind == "12-byte" else 3072 * d) / 1024, 1),
+                     "us": round(us, 2), "frac_peak": round(nb / us / 1e3 / PEAK_HBM, 4)}
+                res.append(r)
+                print(f"# load width {name} {kind} depth {d}: {us:.2f} us ({r['frac_peak']:.1%})", file=sys.stderr,
+                      flush=True)
+        del ws
+        torch.cuda.empty_cache()
+    return res
+
+
 def run_skinny(name, reps, dev, min_bytes=1.2e9):
     """Qwen3-14B skinny-GEMM entry: one shape at every M of SWEEP_M, weights
     N(0, 0.02) bf16 with 0.1% of output rows x20, distinct copies totalling
@@ -656,6 +711,8 @@ def main():
                     help="run only the Qwen3-8B end-to-end decode (2048-token prompt, 256 tokens; for profiling)")
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only the Qwen3-8B blocked prefill of a 2048-token prompt, 3 times (for profiling)")
+    ap.add_argument("--only-load-width", action="store_true",
+                    help="run only the pure-stream probe with 12-byte against 16-byte loads (five Qwen3-8B shapes)")
     ap.add_argument("--only-arrival", action="store_true",
                     help="run only the activation-arrival probe (vector against scalar staging, q/o and k/v shapes)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -691,6 +748,9 @@ def main():
         return
     if args.only_arrival:
         print(json.dumps(arrival(dev)), flush=True)
+        return
+    if args.only_load_width:
+        print(json.dumps(load_width(dev)), flush=True)
         return
 
     tok = run_token_bench(args, dev)
