@@ -707,8 +707,9 @@ def main():
     ap.add_argument("--no-32b", action="store_true", help="skip the Qwen3-32B end-to-end decode")
     ap.add_argument("--only-14b", action="store_true", help="run only the Qwen3-14B skinny-GEMM sweep (for profiling)")
     ap.add_argument("--only-attn", action="store_true", help="run only the Qwen3-8B decode attention (for profiling)")
-    ap.add_argument("--only-e2e", action="store_true",
-                    help="run only the Qwen3-8B end-to-end decode (2048-token prompt, 256 tokens; for profiling)")
+    ap.add_argument("--only-e2e", nargs="?", const="8b", choices=("8b", "0.6b"),
+                    help="run only one end-to-end decode (for profiling): 8b (the default: 2048-token prompt, 256 "
+                         "tokens) or 0.6b (128-token prompt, 64 tokens, as in the default run)")
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only the Qwen3-8B blocked prefill of a 2048-token prompt, 3 times (for profiling)")
     ap.add_argument("--only-load-width", action="store_true",
@@ -741,7 +742,8 @@ def main():
         print(json.dumps(run_attn(dev, args.reps)), flush=True)
         return
     if args.only_e2e:
-        print(json.dumps(run_e2e(dev)), flush=True)
+        r = run_e2e(dev) if args.only_e2e == "8b" else run_e2e(dev, "0.6b", prompt_len=128, new=64)
+        print(json.dumps(r), flush=True)
         return
     if args.only_prefill:
         print(json.dumps(run_prefill(dev)), flush=True)
