@@ -95,7 +95,39 @@ __global__ __launch_bounds__(1024) void k_stream16(const uint32_t* __restrict__ 
     out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
 }
 
+// The first `depth` weight steps of every wave of the vector linear's
+// one-row-block launch (the bytes its prefetch asks for first), read with
+// ordinary (temporal) loads, so that a launch right after it finds them in
+// the caches if the caches keep them across the kernel boundary.
+__global__ __launch_bounds__(1024) void k_warm(const uint32_t* __restrict__ tiles, int N, int K, int depth,
+                                               uint32_t* __restrict__ out) {
+    const int W = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wu = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nsteps = K >> 5;
+    const int64_t nblk = (N + 15) / 16;
+    const int64_t blk0 = blockIdx.x;
+    const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
+    const char* wbase = reinterpret_cast<const char*>(tiles) + blk0 * (int64_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, blk0 < nblk ? blk_bytes : 0u);
+    uint32_t acc = 0;
+    for (int u = 0; u < depth; ++u) {
+        const int s = wu + u * W;
+        const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rv, lane * 12, (s < nsteps ? s : 0) * kStepBytes, 0);
+        acc ^= v.x ^ v.y ^ v.z;
+    }
+    out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
 }  // namespace rv12
+
+extern "C" int rv12_probe_warm(const void* tiles, int n, int k, int waves, int depth, void* out, void* stream) {
+    using namespace rv12;
+    if (!tiles || !out || n < 1 || k < 32 || k % 32 || waves < 1 || waves > 16 || depth < 1 || depth > 64) return -1;
+    const dim3 grid((unsigned)(((int64_t)n + 15) / 16)), block((unsigned)(waves * 64));
+    hipLaunchKernelGGL(k_warm, grid, block, 0, (hipStream_t)stream, (const uint32_t*)tiles, n, k, depth, (uint32_t*)out);
+    return hipGetLastError() == hipSuccess ? 0 : -20;
+}
 
 extern "C" int rv12_probe_stream16(const void* tiles, int n, int k, int waves, int depth, void* out, void* stream) {
     using namespace rv12;

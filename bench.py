@@ -478,6 +478,57 @@ def arrival(dev, shapes=(("q_o", 4096, 4096, 8), ("k_v", 1024, 4096, 8)), min_by
     return out
 
 
+def cache_warm(dev, reps=10, rounds=5):
+    """What the next launch gains from its first weight bytes in the caches:
+    per shape, 40 distinct copies, each linear (built-in launch) preceded by
+    a probe (ai_amd/csrc/rv12_probe.hip, k_warm) that reads, with ordinary
+    loads, the first 6 (or 16) steps per wave of the same matrix or of
+    another copy (same cost); us per pair, median of interleaved rounds."""
+    import ctypes
+    import statistics
+    from ai_amd import build, wcomp
+    P = ctypes.CDLL(build.PROBE_OUT)
+    P.rv12_probe_warm.restype = ctypes.c_int
+    P.rv12_probe_warm.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_void_p, ctypes.c_void_p]
+    out = []
+    for name, N, K, mode, W in (("q_o", 4096, 4096, 1, 8), ("qkv", 6144, 4096, 0, 8), ("down", 4096, 12288, 2, 16)):
+        gen = torch.Generator().manual_seed(9)
+        ncopy = 40
+        cs = [wcomp.compact(wcomp.compress(make_matrix(N, K, gen, dev))) for _ in range(ncopy)]
+        x = torch.randn(K * (2 if mode == 2 else 1), device=dev).bfloat16().float()
+        y = torch.zeros(N, device=dev)
+        sink = torch.empty(((N + 15) // 16) * 1024, dtype=torch.int32, device=dev)
+
+        def graph(shift, depth):
+            def fn():
+                st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                for i, c in enumerate(cs):
+                    if depth:
+                        w = cs[(i + shift) % ncopy]
+                        rc = P.rv12_probe_warm(ctypes.c_void_p(w["q16_tiles"].data_ptr()), N, K, W, depth,
+                                               ctypes.c_void_p(sink.data_ptr()), st)
+                        assert rc == 0, rc
+                    wcomp.gemvc1(x, c, y, mode)
+            return Graph(fn)
+
+        gs = {"linear alone": graph(0, 0)}
+        for depth in (6, 16):
+            gs[f"same matrix, {depth} steps per wave"] = graph(0, depth)
+            gs[f"other matrix, {depth} steps per wave"] = graph(ncopy // 2, depth)
+        t = {k: [] for k in gs}
+        for _ in range(rounds):
+            for k, g in gs.items():
+                t[k].append(time_graph(g, reps) / ncopy * 1e3)
+        r = {"shape": name, "N": N, "K": K, "us_per_pair": {k: round(statistics.median(v), 3) for k, v in t.items()}}
+        out.append(r)
+        print(f"# cache warm {name}: " + ", ".join(f"{k} {v:.2f}" for k, v in r["us_per_pair"].items()), file=sys.stderr,
+              flush=True)
+        del gs, cs
+        torch.cuda.empty_cache()
+    return out
+
+
 LOAD_WIDTH_SHAPES = (("q_o", 4096, 4096, 8), ("qkv", 6144, 4096, 8), ("down", 4096, 12288, 16),
                      ("gu", 24576, 4096, 4), ("lm_head", 151936, 4096, 8))
 
@@ -712,6 +763,8 @@ def main():
                          "tokens) or 0.6b (128-token prompt, 64 tokens, as in the default run)")
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only the Qwen3-8B blocked prefill of a 2048-token prompt, 3 times (for profiling)")
+    ap.add_argument("--only-cache-warm", action="store_true",
+                    help="run only the probe of a linear preceded by a read of its first weight bytes (three shapes)")
     ap.add_argument("--only-load-width", action="store_true",
                     help="run only the pure-stream probe with 12-byte against 16-byte loads (five Qwen3-8B shapes)")
     ap.add_argument("--only-arrival", action="store_true",
@@ -753,6 +806,9 @@ def main():
         return
     if args.only_load_width:
         print(json.dumps(load_width(dev)), flush=True)
+        return
+    if args.only_cache_warm:
+        print(json.dumps(cache_warm(dev)), flush=True)
         return
 
     tok = run_token_bench(args, dev)
