@@ -191,6 +191,30 @@ def test_step_counts_off_the_ring(K):
         _check(cnp, T, K + T + 7, False, mode=0, rms=True)
 
 
+def test_random_draws_of_shapes_tokens_and_modes():
+    """24 seeded draws of row count (1-600), K (128-2048 in steps of 32,
+    codec chunks of 32), token count (1-400), MODE, the RMS prologue (MODES 0
+    and 1), outlier rows and exceptions (3e4, -1e-30 or 1e-35 at random
+    positions), each against the float64 closed form and the fp32 bound."""
+    rng = np.random.default_rng(4242)
+    for d in range(24):
+        N = int(rng.integers(1, 601))
+        K = 32 * int(rng.integers(4, 65))
+        T = int(rng.integers(1, 401))
+        mode = int(rng.integers(0, 3))
+        rms = bool(rng.integers(0, 2)) and mode != 2
+        w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        nout = int(rng.integers(0, 4))
+        if nout:
+            w[rng.choice(N, min(N, nout), replace=False)] *= 20
+        nexc = int(rng.integers(0, 1 + N * K // 500))
+        if nexc:
+            w.reshape(-1)[rng.choice(w.size, nexc, replace=False)] = float(rng.choice([3e4, -1e-30, 1e-35]))
+        cnp = codec.compress(codec.f32_to_bf16_rne(w), CH=32)
+        print("draw", d, N, K, T, mode, rms, int(cnp["er"].size), flush=True)
+        _check(cnp, T, 9000 + d, mode != 0, mode=mode, rms=rms)
+
+
 @pytest.mark.parametrize("case", ["special_values", "all_zero"])
 def test_matrix_on_golden_special_values(golden, case):
     """Golden matrices with infinities, NaNs, subnormals and zeros among the
