@@ -341,6 +341,50 @@ def test_batch_attention_matches_torch(H, KV, HD, kv_dtype):
                 assert torch.equal(kc[:, keep], kc0[:, keep]) and torch.equal(vc[:, keep], vc0[:, keep])
 
 
+def test_random_draws_of_batches():
+    """32 seeded draws of the batched pass (rv12_rope_attn_batch): head
+    layout, head size, cache dtype, cache length (16-2048), token count
+    (1-16), first position and split count, each against the float64
+    restatement; the T cache slots written, the others untouched."""
+    import numpy as np
+    from ai_amd.attn import RopeAttn, default_splits
+    dev = "cuda"
+    eps = 1e-6
+    rng = np.random.default_rng(1616)
+    layouts = [(32, 8, 128), (16, 8, 128), (8, 4, 64), (64, 8, 128), (8, 8, 64), (4, 1, 128), (16, 2, 64)]
+    for d in range(32):
+        H, KV, HD = layouts[int(rng.integers(len(layouts)))]
+        kv_dtype = torch.bfloat16 if rng.integers(2) else torch.float32
+        maxt = int(rng.integers(16, 2049))
+        T = int(rng.integers(1, 17))
+        p0 = int(rng.integers(0, maxt - T + 1))
+        lo = -(-maxt // 80)
+        choices = [default_splits(KV, maxt, kv_dtype == torch.bfloat16, HD), lo, min(128, lo + int(rng.integers(0, 40)))]
+        if maxt <= 256:
+            choices.append(1)
+        splits = int(choices[int(rng.integers(len(choices)))])
+        print("draw", d, H, KV, HD, kv_dtype, maxt, T, p0, splits, flush=True)
+        g = torch.Generator(device=dev).manual_seed(1600 + d)
+        inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+        qn = 1 + 0.1 * torch.randn(HD, device=dev, generator=g)
+        kn = 1 + 0.1 * torch.randn(HD, device=dev, generator=g)
+        qkv = torch.randn(T, (H + 2 * KV) * HD, device=dev, generator=g) * 3
+        kc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+        vc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+        kc0, vc0 = kc.clone(), vc.clone()
+        out = torch.zeros(T, H * HD, device=dev)
+        RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev, splits=splits).batch(
+            qkv, qn, kn, inv, torch.tensor([p0], device=dev), kc, vc, out, T)
+        torch.cuda.synchronize()
+        ref, kr, vr = _torch_batch_ref(qkv, qn, kn, inv, p0, kc0, vc0, H, KV, HD, eps,
+                                       k_new=kc[:, p0:p0 + T].transpose(0, 1).clone())
+        assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), (d, float((out - ref).abs().max()))
+        assert torch.equal(vc[:, p0:p0 + T].float(), vr.float().transpose(0, 1)), d
+        keep = torch.ones(maxt, dtype=torch.bool)
+        keep[p0:p0 + T] = False
+        assert torch.equal(kc[:, keep], kc0[:, keep]) and torch.equal(vc[:, keep], vc0[:, keep]), d
+
+
 def test_batch_equals_single_steps_and_graph_replays():
     """A batch of 8 equals 8 single-token steps from the same cache (each step
     sees the keys the previous ones wrote), and a captured batch replayed with
