@@ -511,6 +511,54 @@ def test_prefill_attention_matches_float64(H, KV, HD, kv_dtype):
             assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), float((out - ref).abs().max())
 
 
+def test_random_draws_of_prompt_blocks():
+    """24 seeded draws of the blocked prefill's attention
+    (rv12_prefill_rope_attn): head layout, head size, cache dtype, block of
+    1-600 tokens at a random first position of a cache of up to 2048, each
+    against the float64 causal attention over the keys the kernel stored;
+    the block's cache slots written, the others untouched."""
+    import numpy as np
+    from ai_amd.attn import RopeAttn
+    dev = "cuda"
+    eps = 1e-6
+    rng = np.random.default_rng(6006)
+    layouts = [(32, 8, 128), (16, 8, 128), (8, 4, 64), (64, 8, 128), (8, 8, 64), (4, 1, 128), (16, 2, 64)]
+    for d in range(24):
+        H, KV, HD = layouts[int(rng.integers(len(layouts)))]
+        kv_dtype = torch.bfloat16 if rng.integers(2) else torch.float32
+        T = int(rng.integers(1, 601))
+        maxt = int(rng.integers(T, 2049))
+        p0 = int(rng.integers(0, maxt - T + 1))
+        print("draw", d, H, KV, HD, kv_dtype, T, maxt, p0, flush=True)
+        g = torch.Generator(device=dev).manual_seed(6000 + d)
+        inv = (1.0 / (1e6 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))).to(dev)
+        qn = 1 + 0.1 * torch.randn(HD, device=dev, generator=g)
+        kn = 1 + 0.1 * torch.randn(HD, device=dev, generator=g)
+        qkv = torch.randn(T, (H + 2 * KV) * HD, device=dev, generator=g) * 3
+        kc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+        vc = torch.randn(KV, maxt, HD, device=dev, generator=g).to(kv_dtype)
+        kc0, vc0 = kc.clone(), vc.clone()
+        out = torch.full((T, H * HD), 7.0, device=dev)
+        RopeAttn(H, KV, HD, maxt, kv_dtype, eps, dev).prefill(
+            qkv, qn, kn, inv, torch.tensor([p0], device=dev), kc, vc, out, T)
+        torch.cuda.synchronize()
+        q = qkv[:, :H * HD].view(T, H, HD)
+        rms = lambda x, w: w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+        q = rms(q, qn)
+        pos = torch.arange(p0, p0 + T, device=dev, dtype=torch.float32)
+        ang = (pos[:, None] * inv[None]).double()
+        cos = torch.cat([ang, ang], -1).cos().float()[:, None]
+        sin = torch.cat([ang, ang], -1).sin().float()[:, None]
+        q = q * cos + torch.cat([-q[..., HD // 2:], q[..., :HD // 2]], -1) * sin
+        v = qkv[:, (H + KV) * HD:].view(T, KV, HD)
+        assert torch.equal(vc[:, p0:p0 + T].float(), v.to(kv_dtype).float().transpose(0, 1)), d
+        keep = torch.ones(maxt, dtype=torch.bool)
+        keep[p0:p0 + T] = False
+        assert torch.equal(kc[:, keep], kc0[:, keep]) and torch.equal(vc[:, keep], vc0[:, keep]), d
+        ref = _prefill_ref(q, kc, vc, p0, T, H, KV, HD)
+        assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), (d, float((out - ref).abs().max()))
+
+
 def test_prefill_attention_equals_batch_and_rejects_bad_blocks():
     """A prompt block of 16 equals the batch kernel's 16 tokens from the same
     cache (both within 1e-4 of each other); a block past the cache's end
