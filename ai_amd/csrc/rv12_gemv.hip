@@ -11,16 +11,17 @@
 //      (the prologue variants are template arguments); a bare barrier puts
 //      every wave's activation loads ahead of the weight loads;
 //   2. each wave issues the loads of its first D weight steps (buffer
-//      loads; a step past the split's end goes through a 0-byte descriptor,
-//      which returns zeros without a memory access);
+//      loads; a step past the split's end takes an offset past the
+//      descriptor's range, which returns zeros without a memory access);
 //   3. the activation loads are waited for (the weight loads stay in flight)
 //      and x' * 2^64 is written to LDS: the MODE / RMS transform, the sum of
 //      squares for RMS and the exponent range of x'; one barrier; if any
 //      nonzero |x'| lies outside [2^-64, 2^63), x' is staged again with a
 //      per-token scale (the activation scaling of rv12_device.h);
-//   4. main loop: per step each wave decodes 8 weights per lane and row block
-//      and does 8 FMAs per token into fp32 accumulators, and issues the load
-//      D steps ahead (D: the prefetch depth chosen per variant below);
+//   4. main loop: per step each wave unpacks its 12-byte words, issues the
+//      load D steps ahead into the same registers (D: the prefetch depth
+//      chosen per variant below) and does 8 FMAs per token and row block into
+//      fp32 accumulators; D loads stay in flight across the rounds;
 //   5. epilogue: one thread per output sums the lane quarters and waves in a
 //      fixed order (no atomics), rescales by 2^(sc - P) of its row, adds the
 //      products ev * x' of its row's exceptions whose column lies in the split
@@ -36,13 +37,18 @@
 
 namespace rv12 {
 
+// an offset past any weight descriptor (<= 2^31 - 1 bytes), which
+// wraps no 32-bit sum with a row-block offset
+constexpr uint32_t kPastEnd = 0x80000000u;
+
 template <int RB>
-__device__ __forceinline__ void issue_step(u32x3 (&dst)[RB], __amdgpu_buffer_rsrc_t rv, __amdgpu_buffer_rsrc_t rnull,
-                                           const int (&voff)[RB], int s, int s_hi) {
-    const __amdgpu_buffer_rsrc_t r = s < s_hi ? rv : rnull;
-    const int soff = (s < s_hi ? s : 0) * kStepBytes;
+__device__ __forceinline__ void issue_step(u32x3 (&dst)[RB], __amdgpu_buffer_rsrc_t rv, const int (&voff)[RB], int s,
+                                           int s_hi) {
+    // a step past the end takes an offset beyond every descriptor's range
+    // (the range check covers the vector offset, not the scalar one)
+    const uint32_t off = s < s_hi ? (uint32_t)s * kStepBytes : kPastEnd;
 #pragma unroll
-    for (int b = 0; b < RB; ++b) dst[b] = load_group(r, voff[b], soff);
+    for (int b = 0; b < RB; ++b) dst[b] = load_group(rv, (int)((uint32_t)voff[b] + off), 0);
 }
 
 // NXM = float4 chunks of activations per thread loaded in step 1, before the
@@ -69,15 +75,21 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4;
     const int wu = __builtin_amdgcn_readfirstlane(wave);
     const int S = gridDim.y, sp = blockIdx.y;
+    // the workgroup size, the split count and the exception count in SGPRs
+    // now: their loads then join the other kernel arguments' and are waited
+    // for with them, not after the first global loads
+    asm volatile("" : : "s"(nthr), "s"(S), "s"(p.n_exc));
     const int nsteps = p.K >> 5;
     // split bounds in 32 bits: nsteps <= 2^15 and S <= 64
-    const int s_lo = (int)((uint32_t)(sp * nsteps) / (uint32_t)S);
-    const int s_hi = (int)((uint32_t)((sp + 1) * nsteps) / (uint32_t)S);
+    int s_lo = 0, s_hi = nsteps;
+    if (S > 1) {
+        s_lo = (int)((uint32_t)(sp * nsteps) / (uint32_t)S);
+        s_hi = (int)((uint32_t)((sp + 1) * nsteps) / (uint32_t)S);
+    }
     const int k_lo = s_lo * 32, krange = (s_hi - s_lo) * 32;
     const int64_t blk0 = (int64_t)blockIdx.x * RB;
     const int n0 = (int)(blk0 * 16);
-    const int64_t nblk = (p.N + 15) / 16;
-    const int nvalid = (int)min((int64_t)RB, nblk - blk0);
+    const int nvalid = min(RB, (int)(((uint32_t)p.N + 15u) >> 4) - (int)blockIdx.x * RB);
 
     float* xl = smem;                    // [T][krange]  x' * 2^P[t]
     float* red = xl + T * krange;        // [W][RB][T][16]
@@ -100,16 +112,16 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     const int32_t oe0 = p.rp[onc], oe1 = p.rp[onc + 1];
     const float oy = p.y[(int64_t)min(otok, T - 1) * p.N + onc];
 
-    // ---- 1. activations of this thread: the chunks j < nxm hold the split's
-    // columns (lanes past its end load column k_lo again, unused)
-    const int nxm = min(NXM, (krange + 4 * nthr - 1) / (4 * nthr));
+    // ---- 1. activations of this thread: the chunks j with 4 j nthr < krange
+    // hold the split's columns (lanes past its end load its last 4 columns
+    // again, unused)
     f32x4 xr[NXM][T], ur[NXM][T];
     uint2 lr[NXM];
 #pragma unroll
     for (int j = 0; j < NXM; ++j) {
-        if (j < nxm) {
+        if (j * 4 * nthr < krange) {
             const int i = (threadIdx.x + j * nthr) * 4;
-            const int k = k_lo + (i < krange ? i : 0);
+            const uint32_t k = (uint32_t)(k_lo + min(i, krange - 4));
             if constexpr (LN) lr[j] = *reinterpret_cast<const uint2*>(p.lnw + k);
 #pragma unroll
             for (int t = 0; t < T; ++t) {
@@ -127,14 +139,13 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
     const char* wbase = reinterpret_cast<const char*>(p.tiles) + blk0 * (int64_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, (uint32_t)nvalid * blk_bytes);
-    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(wbase, 0u);
     int voff[RB];
 #pragma unroll
     for (int b = 0; b < RB; ++b) voff[b] = (int)(b * blk_bytes) + lane * 12;
     const int s0 = s_lo + wu;
     u32x3 buf[D][RB];
 #pragma unroll
-    for (int u = 0; u < D; ++u) issue_step<RB>(buf[u], rv, rnull, voff, s0 + u * W, s_hi);
+    for (int u = 0; u < D; ++u) issue_step<RB>(buf[u], rv, voff, s0 + u * W, s_hi);
 
     // the workgroup's exception range, from the row pointers of step 0 (vector
     // loads issued before the activations): in every wave lane 0 holds
@@ -162,8 +173,9 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     };
 #pragma unroll
     for (int j = 0; j < NXM; ++j) {
+        if (j * 4 * nthr >= krange) break;  // chunk j was not loaded
         const int i = (threadIdx.x + j * nthr) * 4;
-        if (j < nxm && i < krange) {
+        if (i < krange) {
             f32x4 lw = {1.0f, 1.0f, 1.0f, 1.0f};
             if constexpr (LN) lw = bf16x4_to_f32(lr[j]);
 #pragma unroll
@@ -218,9 +230,8 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     int P[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) P[t] = kXScaleExp;
-    int anybad = 0;
-    for (int w = 0; w < W; ++w) anybad |= wflag[w];
-    if (anybad) {
+    // the W flags in one LDS read, lane w reading wave w's
+    if (__ballot(lane < W && wflag[lane] != 0) != 0) {
         auto xprime = [&](int t, int k) {
             const float* xt = p.x + (int64_t)t * p.xs;
             f32x4 v = *reinterpret_cast<const f32x4*>(xt + k);
@@ -273,20 +284,24 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
 #pragma unroll
         for (int t = 0; t < T; ++t) acc[b][t] = 0.0f;
 
-    const int per_wave = (s_hi - s_lo + W - 1) / W;
-    const int rounds = (per_wave + D - 1) / D;
-    for (int r = 0; r < rounds; ++r) {
+    // rounds of D of this wave's steps s0, s0 + W, ...; a wave stops after
+    // its last step (the steps after it are all past s_hi)
+    for (int sr = s0; sr < s_hi; sr += D * W) {
 #pragma unroll
         for (int u = 0; u < D; ++u) {
-            const int s = s0 + (r * D + u) * W;
-            u32x3 cur[RB];
+            const int s = sr + u * W;
+            // the step's words are unpacked before the load D steps ahead
+            // reuses their registers: no copy of the loaded registers at the
+            // loop's back edge, so no wait there for the loads in flight
+            uint32_t pr[RB][4];
 #pragma unroll
-            for (int b = 0; b < RB; ++b) cur[b] = buf[u][b];
-            issue_step<RB>(buf[u], rv, rnull, voff, s + D * W, s_hi);
+            for (int b = 0; b < RB; ++b) {
+                unpack_pairs(buf[u][b].x, buf[u][b].y, buf[u][b].z, pr[b]);
+                // (kept ahead of the load by the compiler's scheduler)
+                asm volatile("" : "+v"(pr[b][0]), "+v"(pr[b][1]), "+v"(pr[b][2]), "+v"(pr[b][3])::"memory");
+            }
+            issue_step<RB>(buf[u], rv, voff, s + D * W, s_hi);
             if (s < s_hi) {
-                uint32_t pr[RB][4];
-#pragma unroll
-                for (int b = 0; b < RB; ++b) unpack_pairs(cur[b].x, cur[b].y, cur[b].z, pr[b]);
                 const float* xs = xl + (s - s_lo) * 32 + q * 8;
 #pragma unroll
                 for (int t = 0; t < T; ++t) {
@@ -334,10 +349,29 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
     auto add_round = [&](int32_t j0) {
         if (oval) {
             const int32_t a = max(oe0, j0), z = min(oe1, j0 + nthr);
-            for (int32_t j = a; j < z; ++j) eacc += excv[(j - j0) * T + otok];
+            // four entries per LDS round trip, added in list order
+            for (int32_t j = a; j < z; j += 4) {
+                float e[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) e[i] = excv[(min(j + i, z - 1) - j0) * T + otok];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (j + i < z) eacc += e[i];
+            }
         }
     };
     if (e_lo < e_hi) stage_round(e_lo, ec0, ev0);
+    // the owner's RMS scale, from the waves' sums staged before the loop:
+    // formed before the barrier, where the waves that end their loop early
+    // would only wait
+    float rs = 1.0f;
+    if constexpr (LN) {
+        if (S == 1 && oval) {
+            float sqs = 0.0f;
+            for (int w = 0; w < W; ++w) sqs += ssq[w * T + otok];
+            rs = rms_scale(sqs, p.K, p.eps);
+        }
+    }
     __syncthreads();
     float v = 0.0f;
     if (owner) {
@@ -366,11 +400,7 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
         for (int t = 1; t < T; ++t) Po = otok == t ? P[t] : Po;
         v = ldexpf(v, scale_exp(obase) - Po) + eacc;
         if (S == 1) {
-            if constexpr (LN) {
-                float sqs = 0.0f;
-                for (int w = 0; w < W; ++w) sqs += ssq[w * T + otok];
-                v *= rms_scale(sqs, p.K, p.eps);
-            }
+            if constexpr (LN) v *= rs;
             yv = p.mode == 0 ? v : oy + v;
             if (p.store_y) p.y[(int64_t)otok * p.N + on] = yv;
         } else {

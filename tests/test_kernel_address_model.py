@@ -66,10 +66,14 @@ def test_vector_linear_addresses(model, T):
             assert k + 3 < K and (T - 1) * xs + (K if mode == 2 else 0) + k + 3 < T * xs
             if rms:
                 assert k + 3 < K  # lnw (4 bf16 per chunk)
-        # step 2: weights through one descriptor per workgroup: its row blocks' bytes
+        # step 2: weights through one descriptor per workgroup over its row
+        # blocks' bytes; a step's offset is all in the 32-bit vector offset,
+        # and a step past the split's end takes 2^31 plus the row-block
+        # offset, past the descriptor's range without wrapping
         blk_bytes = nsteps * 768
-        assert RB * blk_bytes < U32 and (RB - 1) * blk_bytes + 63 * 12 < I32  # voff is a signed int
-        assert (nsteps - 1) * 768 < I32  # soff
+        assert RB * blk_bytes < I32  # the descriptor's range, below 2^31
+        assert (RB - 1) * blk_bytes + (nsteps - 1) * 768 + 63 * 12 + 12 <= RB * blk_bytes
+        assert I32 + (RB - 1) * blk_bytes + 63 * 12 + 12 <= U32
         # step 3: the exception entries through descriptors of min(n_exc, 2^28) * 4 bytes
         assert min(n_exc, 1 << 28) * 4 < U32 and (n_exc - 1) * 4 < 0xFFFFFFF0
         # step 5/6: stores and partials
