@@ -16,8 +16,9 @@
 // W * RBW row blocks; wave w owns row blocks w*RBW .. w*RBW + RBW - 1.
 //   1. every thread loads the activations of its B-operand groups (one group
 //      = one step x one lane: token l%16, k = 8(l/16) + 0..7);
-//   2. each wave issues the loads of its first D weight steps (D = kDepth, half
-//      that with four row blocks per wave: the same bytes in flight);
+//   2. each wave issues the loads of its first D weight steps (buffer loads;
+//      a step past the split's end takes an offset past the descriptor's
+//      range, which returns zeros without a memory access);
 //   3. x' is formed (MODE / RMS transform), scaled by 2^64 and split into
 //      hi/mid/lo, and written to LDS in B-operand lane order (tokens >= T are
 //      zeros); barrier.  The scale lifts the products of the Q16 values
@@ -26,9 +27,11 @@
 //      nonzero |x'| of the split lies outside [2^-64, 2^63) (found by a ballot
 //      and an LDS flag per wave), the parts are staged again with x' * 2^P,
 //      P = 100 - the exponent of the split's largest |x'| per token;
-//   4. main loop: per step three ds_read_b128 fetch the B parts, each of the
-//      wave's row blocks is unpacked once and meets the three parts in three
-//      MFMAs into three independent accumulators;
+//   4. main loop: per step each of the wave's row blocks is unpacked once,
+//      the load D steps ahead is issued into the same registers (D loads stay
+//      in flight across the rounds), three ds_read_b128 fetch the B parts and
+//      each row block meets the three parts in three MFMAs into three
+//      independent accumulators;
 //   5. epilogue per wave: the exceptions of the wave's rows whose column is
 //      inside the split are added per (row, token) in list order (the entries
 //      found by a ballot, one at a time), x' taken from the LDS parts times
@@ -49,13 +52,18 @@ namespace rv12 {
 
 constexpr int kGroupsPerThread = 4;  // B-operand groups a thread loads before the weight prefetch
 
+// an offset past any weight descriptor (<= 2^31 - 1 bytes), which
+// wraps no 32-bit sum with a row-block offset
+constexpr uint32_t kPastEnd = 0x80000000u;
+
 template <int RBW>
-__device__ __forceinline__ void issue_rows(u32x3 (&dst)[RBW], __amdgpu_buffer_rsrc_t rv,
-                                           __amdgpu_buffer_rsrc_t rnull, const int (&voff)[RBW], int s, int s_hi) {
-    const __amdgpu_buffer_rsrc_t r = s < s_hi ? rv : rnull;
-    const int soff = (s < s_hi ? s : 0) * kStepBytes;
+__device__ __forceinline__ void issue_rows(u32x3 (&dst)[RBW], __amdgpu_buffer_rsrc_t rv, const int (&voff)[RBW], int s,
+                                           int s_hi) {
+    // a step past the end takes an offset beyond every descriptor's range
+    // (the range check covers the vector offset, not the scalar one)
+    const uint32_t off = s < s_hi ? (uint32_t)s * kStepBytes : kPastEnd;
 #pragma unroll
-    for (int b = 0; b < RBW; ++b) dst[b] = load_group(r, voff[b], soff);
+    for (int b = 0; b < RBW; ++b) dst[b] = load_group(rv, (int)((uint32_t)voff[b] + off), 0);
 }
 
 
@@ -80,10 +88,17 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wu = __builtin_amdgcn_readfirstlane(wave);
     const int S = gridDim.y, sp = blockIdx.y;
+    // the workgroup size, the split count and the exception count in SGPRs
+    // now: their loads then join the other kernel arguments' and are waited
+    // for with them, not after the first global loads
+    asm volatile("" : : "s"(nthr), "s"(S), "s"(p.n_exc));
     const int nsteps = p.K >> 5;
     // split bounds in 32 bits: nsteps <= 2^15 and S <= 64
-    const int s_lo = (int)((uint32_t)(sp * nsteps) / (uint32_t)S);
-    const int s_hi = (int)((uint32_t)((sp + 1) * nsteps) / (uint32_t)S);
+    int s_lo = 0, s_hi = nsteps;
+    if (S > 1) {
+        s_lo = (int)((uint32_t)(sp * nsteps) / (uint32_t)S);
+        s_hi = (int)((uint32_t)((sp + 1) * nsteps) / (uint32_t)S);
+    }
     const int nst = s_hi - s_lo, k_lo = s_lo * 32, krange = nst * 32;
     const int ngr = nst * G;  // B-operand groups of the split
     const int64_t nblk = (p.N + 15) / 16;
@@ -128,12 +143,13 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     // weight load (a bare barrier: it orders the issue, it waits for no data)
     __builtin_amdgcn_s_barrier();
 
-    // ---- 2. first D weight steps of this wave's row blocks
-    constexpr int D = RBW >= 4 ? kDepth / 2 : kDepth;
+    // ---- 2. first D weight steps of this wave's row blocks.  D per row
+    // blocks of a wave, measured on the Qwen3-14B shapes at 4-16 tokens: 2 row
+    // blocks (qkv, o) 4 (qkv M4 17.2 us at 8, 15.8 at 4), one 6, four 3
+    constexpr int D = RBW >= 4 ? 3 : (RBW == 2 ? 4 : 6);
     const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
     const char* wbase = reinterpret_cast<const char*>(p.tiles) + wblk * (int64_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, (uint32_t)nvalid * blk_bytes);
-    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(wbase, 0u);
     int voff[RBW];
 #pragma unroll
     for (int b = 0; b < RBW; ++b) voff[b] = (int)(b * blk_bytes) + lane * 12;
@@ -141,7 +157,7 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     const int s0 = s_lo + (KS ? wu : 0);  // this wave's first step
     const int stride = KS ? W : 1;        // steps between this wave's consecutive steps
 #pragma unroll
-    for (int u = 0; u < D; ++u) issue_rows<RBW>(buf[u], rv, rnull, voff, s0 + u * stride, s_hi);
+    for (int u = 0; u < D; ++u) issue_rows<RBW>(buf[u], rv, voff, s0 + u * stride, s_hi);
 
     // what the epilogue reads, loaded now so that it arrives during the main
     // loop: the wave's exception range (its first 64 entries are loaded after
@@ -265,9 +281,8 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     // token jj (this lane's outputs and exception sums), Pg that of token tg
     // (this thread's staged groups).
     int Pj = kXScaleExp;
-    int anybad = 0;
-    for (int w = 0; w < W; ++w) anybad |= wflag[w];
-    if (anybad) {
+    // the W flags in one LDS read, lane w reading wave w's
+    if (__ballot(lane < W && wflag[lane] != 0) != 0) {
         auto xprime = [&](int k, float (&v)[8]) {
             const f32x4 a0 = *reinterpret_cast<const f32x4*>(xrow + k);
             const f32x4 a1 = *reinterpret_cast<const f32x4*>(xrow + k + 4);
@@ -335,17 +350,26 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
     for (int b = 0; b < RBW; ++b)
 #pragma unroll
         for (int c = 0; c < 3; ++c) acc[b][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int per_wave = KS ? (nst + W - 1) / W : nst;
-    const int rounds = (per_wave + D - 1) / D;
-    for (int r = 0; r < rounds; ++r) {
+    // rounds of D of this wave's steps s0, s0 + stride, ...; a wave stops
+    // after its last step (the steps after it are all past s_hi)
+    for (int sb = s0; sb < s_hi; sb += D * stride) {
 #pragma unroll
         for (int u = 0; u < D; ++u) {
-            const int s = s0 + (r * D + u) * stride;
+            const int s = sb + u * stride;
             const int sr = s - s_lo;  // step within the split
-            u32x3 cur[RBW];
+            // the step's words are unpacked before the load D steps ahead
+            // reuses their registers: no copy of the loaded registers at the
+            // loop's back edge, so no wait there for the loads in flight
+            u32x4 a[RBW];
 #pragma unroll
-            for (int b = 0; b < RBW; ++b) cur[b] = buf[u][b];
-            issue_rows<RBW>(buf[u], rv, rnull, voff, s + D * stride, s_hi);
+            for (int b = 0; b < RBW; ++b) {
+                uint32_t pr[4];
+                unpack_pairs(buf[u][b].x, buf[u][b].y, buf[u][b].z, pr);
+                a[b] = u32x4{pr[0], pr[1], pr[2], pr[3]};
+                // (kept ahead of the load by the compiler's scheduler)
+                asm volatile("" : "+v"(a[b])::"memory");
+            }
+            issue_rows<RBW>(buf[u], rv, voff, s + D * stride, s_hi);
             if (s < s_hi) {
                 u32x4 b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0}, b2 = {0, 0, 0, 0};
                 if (TP == 16 || bl >= 0) {
@@ -356,12 +380,9 @@ __global__ __launch_bounds__(kGemmMaxWaves * 64) void k_gemm(LinearParams p, int
                 }
 #pragma unroll
                 for (int b = 0; b < RBW; ++b) {
-                    uint32_t pr[4];
-                    unpack_pairs(cur[b].x, cur[b].y, cur[b].z, pr);
-                    const u32x4 a = {pr[0], pr[1], pr[2], pr[3]};
-                    acc[b][0] = mfma(a, b0, acc[b][0]);
-                    acc[b][1] = mfma(a, b1, acc[b][1]);
-                    acc[b][2] = mfma(a, b2, acc[b][2]);
+                    acc[b][0] = mfma(a[b], b0, acc[b][0]);
+                    acc[b][1] = mfma(a[b], b1, acc[b][1]);
+                    acc[b][2] = mfma(a[b], b2, acc[b][2]);
                 }
             }
         }

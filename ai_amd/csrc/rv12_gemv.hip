@@ -55,20 +55,14 @@ __device__ __forceinline__ void issue_step(u32x3 (&dst)[RB], __amdgpu_buffer_rsr
 // weight prefetch; columns beyond 4 * NXM * blockDim.x are staged after it.
 // M2: silu(g) * u prologue (MODE 2); LN: RMSNorm weight.  Both are template
 // arguments so that the loads of step 1 are straight-line code, issued without
-// waiting for any kernel argument test.
+// waiting for any kernel argument test.  SH: the shallow prefetch (one token).
 // The host guarantees blockDim.x >= 16 * RB * T (one thread per output).
-template <int T, int RB, bool M2, bool LN>
+template <int T, int RB, bool M2, bool LN, bool SH>
 __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p) {
     constexpr int NXM = gemv_chunks(T);
     constexpr int NO = RB * 16 * T;  // outputs of the workgroup
-    // weight steps in flight per wave: deeper prefetch delays the activation
-    // loads, which the memory system serves behind the weight stream.  At one
-    // token 6 steps beat 8, and 4 with the 2K silu(g)*u activations (Qwen3-8B
-    // qkv 11.02 -> 10.67 us, o 7.64 -> 7.46, down 16.59 -> 15.9; 32B down
-    // 38.8 -> 37.45); the one-row-block RMS variant (gu: many rounds of
-    // workgroups per CU) keeps 8 (8B gu 28.3 at 8, 28.9 at 6).  At two tokens
-    // 6 beat 8 on every shape (14B o 12.28 -> 11.93, gate/up 28.7 -> 28.1)
-    constexpr int D = T > 2 ? kDepth : (T == 2 ? 6 : (M2 ? 4 : (LN && RB == 1 ? kDepth : 6)));
+    // weight steps in flight per wave
+    constexpr int D = gemv_depth(T, RB, M2, LN, SH);
     extern __shared__ float smem[];
     const int W = blockDim.x >> 6;
     const int nthr = blockDim.x;
@@ -606,21 +600,27 @@ void launch_decode_advance(const int64_t* ids, const uint16_t* emb, int64_t voca
 }
 
 // ------------------------------------------------------------------ launch
-template <int T, int RB, bool M2, bool LN>
+template <int T, int RB, bool M2, bool LN, bool SH>
 static void launch_t(const LinearParams& p, dim3 grid, int threads, size_t lds, hipStream_t st) {
     if (lds > kDefaultLds)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<T, RB, M2, LN>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<T, RB, M2, LN, SH>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((k_gemv<T, RB, M2, LN>), grid, dim3(threads), lds, st, p);
+    hipLaunchKernelGGL((k_gemv<T, RB, M2, LN, SH>), grid, dim3(threads), lds, st, p);
+}
+
+template <int T, int RB, bool M2, bool LN>
+static void launch_depth(const LinearParams& p, dim3 grid, int threads, size_t lds, hipStream_t st) {
+    if (T == 1 && gemv_shallow(T, RB, threads / 64, M2, LN)) launch_t<T, RB, M2, LN, T == 1>(p, grid, threads, lds, st);
+    else launch_t<T, RB, M2, LN, false>(p, grid, threads, lds, st);
 }
 
 template <int T, int RB>
 static void launch_pro(const LinearParams& p, dim3 grid, int threads, size_t lds, hipStream_t st) {
     const bool m2 = p.mode == 2, ln = p.lnw != nullptr;
-    if (m2 && ln) launch_t<T, RB, true, true>(p, grid, threads, lds, st);
-    else if (m2) launch_t<T, RB, true, false>(p, grid, threads, lds, st);
-    else if (ln) launch_t<T, RB, false, true>(p, grid, threads, lds, st);
-    else launch_t<T, RB, false, false>(p, grid, threads, lds, st);
+    if (m2 && ln) launch_depth<T, RB, true, true>(p, grid, threads, lds, st);
+    else if (m2) launch_depth<T, RB, true, false>(p, grid, threads, lds, st);
+    else if (ln) launch_depth<T, RB, false, true>(p, grid, threads, lds, st);
+    else launch_depth<T, RB, false, false>(p, grid, threads, lds, st);
 }
 
 template <int RB>

@@ -60,6 +60,21 @@ inline size_t gemv_lds_bytes(int K, int T, int rb, int waves, int splits) {
 // waves per workgroup the kernel is built for (its register budget)
 __host__ __device__ constexpr int gemv_max_waves(int rb) { return rb == 1 ? 16 : 8; }
 
+// weight steps in flight per wave.  At one token 6, 4 with the 2K
+// silu(g)*u activations and 8 for the one-row-block RMS variant (many rounds
+// of workgroups per CU), measured per Qwen3-8B shape; the shallow form (4)
+// where a workgroup's prefetch would pass kGemvPrefetchMax: its late waves
+// wait at the issue of their first loads, behind the CU's misses in flight
+// (8B qkv, 2 row blocks x 8 waves: 9.63 us at 6, 9.02 at 4).  At two tokens
+// 6 beat 8 on every shape (14B o 12.28 -> 11.93, gate/up 28.7 -> 28.1).
+__host__ __device__ constexpr int gemv_depth(int T, int rb, bool m2, bool ln, bool shallow) {
+    return T > 2 ? kDepth : (T == 2 ? 6 : (shallow || m2 ? 4 : (ln && rb == 1 ? kDepth : 6)));
+}
+constexpr size_t kGemvPrefetchMax = 48 * 1024;  // bytes of one workgroup's first weight loads
+inline bool gemv_shallow(int T, int rb, int waves, bool m2, bool ln) {
+    return T == 1 && (size_t)waves * rb * gemv_depth(T, rb, m2, ln, false) * 768 /* one step tile */ > kGemvPrefetchMax;
+}
+
 // launch shape fits the kernel's register budget and LDS
 inline bool gemv_fits(int K, int T, int rb, int waves, int splits) {
     return waves <= gemv_max_waves(rb) && waves * 64 >= rb * 16 * T &&

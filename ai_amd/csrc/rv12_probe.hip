@@ -25,30 +25,35 @@ __global__ __launch_bounds__(1024) void k_stream(const uint32_t* __restrict__ ti
     const uint32_t blk_bytes = (uint32_t)nsteps * kStepBytes;
     const char* wbase = reinterpret_cast<const char*>(tiles) + blk0 * (int64_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(wbase, (uint32_t)nvalid * blk_bytes);
-    const __amdgpu_buffer_rsrc_t rnull = make_rsrc(wbase, 0u);
     int voff[RB];
 #pragma unroll
     for (int b = 0; b < RB; ++b) voff[b] = (int)(b * blk_bytes) + lane * 12;
+    // the linear's addressing: the step's offset in the vector offset, a step
+    // past the end at 2^31 + the row-block offset (past the descriptor: zeros,
+    // no memory access)
+    auto issue = [&](u32x3 (&dst)[RB], int s) {
+        const uint32_t off = s < nsteps ? (uint32_t)s * kStepBytes : 0x80000000u;
+#pragma unroll
+        for (int b = 0; b < RB; ++b) dst[b] = load_group(rv, (int)((uint32_t)voff[b] + off), 0);
+    };
     u32x3 buf[D][RB];
     const int s0 = wu;
 #pragma unroll
     for (int u = 0; u < D; ++u) {
-        const int s = s0 + u * W;
-        const __amdgpu_buffer_rsrc_t r = s < nsteps ? rv : rnull;
-#pragma unroll
-        for (int b = 0; b < RB; ++b) buf[u][b] = load_group(r, voff[b], (s < nsteps ? s : 0) * kStepBytes);
+        issue(buf[u], s0 + u * W);
+        asm volatile("" ::: "memory");  // issued in step order, as the linear's
     }
     uint32_t acc = 0;
-    const int rounds = ((nsteps - s0 + W - 1) / W + D - 1) / D;
-    for (int rr = 0; rr < rounds; ++rr) {
+    // the linear's loop: a step's words are used before the load D steps
+    // ahead reuses their registers (the fence keeps the compiler's scheduler
+    // from hoisting the load), so D loads stay in flight across the rounds
+    for (int sr = s0; sr < nsteps; sr += D * W) {
 #pragma unroll
         for (int u = 0; u < D; ++u) {
 #pragma unroll
             for (int b = 0; b < RB; ++b) acc ^= buf[u][b].x ^ buf[u][b].y ^ buf[u][b].z;
-            const int s = s0 + (rr * D + u + D) * W;
-            const __amdgpu_buffer_rsrc_t r = s < nsteps ? rv : rnull;
-#pragma unroll
-            for (int b = 0; b < RB; ++b) buf[u][b] = load_group(r, voff[b], (s < nsteps ? s : 0) * kStepBytes);
+            asm volatile("" : "+v"(acc)::"memory");
+            issue(buf[u], sr + (u + D) * W);
         }
     }
     out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;

@@ -376,9 +376,10 @@ def run_shape(name, reps, dev, min_bytes=1.2e9, outliers="rows"):
 
 def stream_ceiling(cs, N, K, reps):
     """The pure weight stream of the same launch (ai_amd/csrc/rv12_probe.hip:
-    the vector linear's grid, waves, step order, loads and prefetch depth at
-    one token, without decode, activations, FMAs or exceptions) over the same
-    copies: what a launch of this shape can reach on its 12-bit bytes."""
+    the vector linear's grid, waves, step order, loads and loop at one token,
+    without decode, activations, FMAs or exceptions) over the same copies, at
+    4, 6 and 8 steps in flight per wave: the fastest is what a launch of this
+    shape can reach on its 12-bit bytes."""
     import ctypes
     from ai_amd import _lib, build
     if not os.path.exists(build.PROBE_OUT):
@@ -392,20 +393,24 @@ def stream_ceiling(cs, N, K, reps):
         return None
     nblk = (N + 15) // 16
     out = torch.empty(((nblk + c.rb - 1) // c.rb) * c.waves * 64, dtype=torch.int32, device="cuda")
-    depth = 6  # the vector kernel's prefetch depth at one token without prologue
+    best = None
+    for depth in (4, 6, 8):
+        def fn(depth=depth):
+            for m in cs:
+                rc = P.rv12_probe_stream(ctypes.c_void_p(m["q16_tiles"].data_ptr()), N, K, c.rb, c.waves, depth,
+                                         ctypes.c_void_p(out.data_ptr()),
+                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                assert rc == 0, rc
 
-    def fn():
-        for m in cs:
-            rc = P.rv12_probe_stream(ctypes.c_void_p(m["q16_tiles"].data_ptr()), N, K, c.rb, c.waves, depth,
-                                     ctypes.c_void_p(out.data_ptr()),
-                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-            assert rc == 0, rc
-
-    graph = Graph(fn)
-    ms = time_graph(graph, reps) / len(cs)
+        graph = Graph(fn)
+        ms = time_graph(graph, reps) / len(cs)
+        del graph
+        if best is None or ms < best[0]:
+            best = (ms, depth)
+    ms, depth = best
     tb = 1.5 * ((N + 15) // 16 * 16) * K
-    del graph
-    return {"stream_us": ms * 1e3, "stream_GBs": tb / ms / 1e6, "stream_frac_peak": tb / ms / 1e6 / PEAK_HBM}
+    return {"stream_us": ms * 1e3, "stream_GBs": tb / ms / 1e6, "stream_frac_peak": tb / ms / 1e6 / PEAK_HBM,
+            "stream_depth": depth}
 
 
 ARRIVAL_MODES = {0: "vector, alone", 1: "scalar, alone", 2: "vector, weight stream", 3: "scalar, weight stream"}

@@ -266,10 +266,14 @@ def test_mfma_linear_addresses(model, kernel):
                     c = nst * 32 - 1
                     o = ((c >> 5) * 3 * G + ((c & 31) >> 3) * TP + (T - 1)) * 16 + (c & 7) * 2
                     assert o + 2 * G * 16 + 1 < nst * 3 * G * 16
-                # weights: one descriptor over the loading wave's (KS: the workgroup's) row blocks
+                # weights: one descriptor over the loading wave's (KS: the
+                # workgroup's) row blocks; a step's offset is all in the 32-bit
+                # vector offset, a step past the split's end takes 2^31 plus the
+                # row-block offset, past the descriptor's range without wrapping
                 blk_bytes = nsteps * 768
-                assert RBW * blk_bytes < U32 and (RBW - 1) * blk_bytes + 63 * 12 < I32
-                assert (nsteps - 1) * 768 < I32
+                assert RBW * blk_bytes < I32
+                assert (RBW - 1) * blk_bytes + (nsteps - 1) * 768 + 63 * 12 + 12 <= RBW * blk_bytes
+                assert I32 + (RBW - 1) * blk_bytes + 63 * 12 + 12 <= U32
                 # output rows: KS wave b < RBW takes row block b, its 16 rows hold every exception row index
                 orb = 1 if ks else RBW
                 assert orb * 16 * 16 <= 256 * orb  # excw [orb * 16 rows][16 tokens] of the wave
