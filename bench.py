@@ -33,7 +33,7 @@ PEAK_HBM = 8000.0  # GB/s, MI355X HBM3E
 # layer matrices of a Qwen3-8B token, mean per launch) from the rocprofv3
 # FETCH_SIZE and WRITE_SIZE counters, each scaled by what it reads for a 1 GiB
 # device copy (--copy-calibration): profiles/k_gemv_qwen3-8b_token.md
-TRAFFIC_BYTES_PER_LAUNCH = 73326841
+TRAFFIC_BYTES_PER_LAUNCH = 73326808
 D, FF, L, V = 4096, 12288, 36, 151936
 QKV = (32 + 2 * 8) * 128
 LAYER = [("qkv", QKV, D, 0, True), ("o", D, 32 * 128, 1, False), ("gu", 2 * FF, D, 0, True),
