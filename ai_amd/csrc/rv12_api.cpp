@@ -83,21 +83,26 @@ Shape vector_shape(int N, int K, int T) {
 // weight bytes at the smaller of the HBM rate and a per-CU rate (the bytes
 // one CU keeps in flight over the memory latency); a K split adds the reduce
 // pass, a launch plus a cost per MB of partials.  The constants are fitted to
-// a sweep of every launch shape the model considers on 14 Qwen3-8B/14B/32B
-// shapes (RMS and silu prologues as the engine runs them) at 4, 8 and 16
-// tokens on MI355X: the model's pick lies 1.7 % above the measured best on
-// average and 11 % at worst (Qwen3-32B gu at 4 tokens).
-constexpr double kModelRoundUs = 1.5;
+// a sweep of the launch shapes the model considers (kernel 2: 1, 2 or 4 row
+// blocks per wave, 4 or 8 waves, the first 10 splits that fit; 3284 timed
+// launches) on 13 Qwen3-8B/14B/32B shapes at 4, 8 and 16 tokens on MI355X,
+// with the kernel's per-row-block prefetch depths: the model's pick lies
+// 1.3 % above the measured best on average and 9.5 % at worst (Qwen3-32B o at
+// 4 tokens); the per-CU rate depends on the row blocks and waves of a wave's
+// workgroup (one row block of 8 waves streams best, four of 4 worst).
+constexpr double kModelRoundUs = 1.0;
 constexpr double kModelStepUs = 0.2;
 constexpr double kModelHbmGBs = 6500.0;
 constexpr double kModelCuGBs = 30.0;
+constexpr double kModelCuGBs1x8 = 35.0;  // one row block per wave, 8 waves
+constexpr double kModelCuGBs4x4 = 10.0;  // four row blocks per wave, 4 waves
 // kernel 3 (the waves split K): the per-CU rate fitted to the same sweep with
 // its shapes added; it is slower than kernel 2 on all but 2 of the 42 cases
 // (Qwen3-8B down and 32B o at 4 tokens, by 1-4 %), so the built-in choice is
 // kernel 2 and kernel 3 a candidate of the tuner and of explicit launches
 constexpr double kModelKsCuGBs = 10.0;
 constexpr double kModelReduceUs = 0.5;
-constexpr double kModelReduceUsPerMB = 1.0;
+constexpr double kModelReduceUsPerMB = 2.0;
 constexpr int kModelCUs = 256;
 constexpr double kModelStepBytes = 768.0;  // one (row block, step) tile
 
@@ -108,7 +113,10 @@ double mfma_model_us(int64_t nblk, int N, int K, int T, int rb, int waves, int s
     const int64_t wgs = (nblk + per_wg - 1) / per_wg * splits;
     const int steps = split_steps(K, splits);
     const double wg_bytes = (double)per_wg * steps * kModelStepBytes;
-    const double cu_rate = kernel == 3 ? kModelKsCuGBs : kModelCuGBs;
+    const double cu_rate = kernel == 3 ? kModelKsCuGBs
+                           : rb == 1 && waves == 8 ? kModelCuGBs1x8
+                           : rb == 4 && waves == 4 ? kModelCuGBs4x4
+                                                   : kModelCuGBs;
     double t = 0.0;
     for (int64_t left = wgs; left > 0;) {
         const int64_t n = std::min<int64_t>(left, (int64_t)kModelCUs);
@@ -139,12 +147,13 @@ Shape mfma_shape(int N, int K, int T, int kernel = 2) {
             for (int w : {4, 8}) {
                 const int wv = std::min(w, nsteps);  // no more waves than K steps
                 if (kn == 3 && wv < rb) continue;
-                // kernel 2's built-in shapes keep every staged group in
-                // registers (4 per thread: 64 waves / TP steps), so no
-                // staging load waits behind the weight prefetch
+                // (shapes whose activation groups do not all fit the four
+                // registers per thread stage the rest after the weight
+                // prefetch; the sweep the constants are fitted to timed them
+                // as fast, and a rule that kept them out doubled the model's
+                // mean miss: 2.0 against 1.3 %)
                 auto fits = [&](int s) {
-                    return kn == 3 ? gemm_ks_fits(K, T, rb, wv, s)
-                                   : split_steps(K, s) <= 64 * wv / gemm_tokens(T) && gemm_fits(K, T, rb, wv, s);
+                    return kn == 3 ? gemm_ks_fits(K, T, rb, wv, s) : gemm_fits(K, T, rb, wv, s);
                 };
                 int s0 = 1;
                 while (s0 < std::min(kMaxSplits, nsteps) && !fits(s0)) ++s0;

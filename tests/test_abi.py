@@ -92,16 +92,16 @@ def test_launch_shapes():
     assert shape(4096, 4096, 4)[0] == 2                   # 4 tokens: MFMA
     # the MFMA kernel's time model picks the shapes the MI355X sweeps found best
     assert shape(4096, 4096, 8) == (2, 1, 8, 8)           # 8B o: 256 workgroups of 16 K steps
-    assert shape(6144, 4096, 4) == (2, 2, 8, 10)          # 8B qkv: 240 workgroups
-    assert shape(1024, 5120, 16) == (2, 1, 4, 16)         # 14B k/v: 64 row blocks, 16 splits of 10 steps
-    assert shape(5120, 5120, 4) == (2, 2, 8, 11)          # 14B o: 220 workgroups of 15 K steps
-    assert shape(5120, 17408, 16)[:3] == (2, 4, 8)        # 14B down: four row blocks per wave
-    assert shape(5120, 8192, 16) == (2, 2, 8, 12)         # 32B o
-    assert shape(5120, 25600, 8) == (2, 4, 8, 23)         # 32B down
+    assert shape(6144, 4096, 4) == (2, 1, 8, 5)           # 8B qkv: 240 workgroups of one row block per wave
+    assert shape(1024, 5120, 16) == (2, 1, 4, 14)         # 14B k/v: 64 row blocks, 14 splits of 12 steps
+    assert shape(5120, 5120, 4) == (2, 1, 8, 6)           # 14B o: 240 workgroups of 27 K steps
+    assert shape(5120, 17408, 16) == (2, 2, 8, 12)        # 14B down: two row blocks per wave
+    assert shape(5120, 8192, 16) == (2, 2, 8, 11)         # 32B o
+    assert shape(5120, 25600, 8) == (2, 2, 8, 12)         # 32B down
     # a partial configuration keeps the built-in split where its staging fits
     # the LDS (3 KB per K step at 16 tokens, 768 B at 4); an explicit split
     # whose staging does not fit is rejected
-    assert shape(5120, 5120, 16, _lib.Launch(2, 2, 4, 0)) == (2, 2, 4, 11)
+    assert shape(5120, 5120, 16, _lib.Launch(2, 2, 4, 0)) == (2, 2, 4, 6)
     # the waves splitting K (kernel 3): row blocks per workgroup at most the
     # waves; one workgroup stages all 5120 columns at 4 tokens (147 KB of LDS)
     assert shape(5120, 5120, 4, _lib.Launch(3, 2, 8, 1)) == (3, 2, 8, 1)
