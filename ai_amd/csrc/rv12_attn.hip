@@ -132,31 +132,10 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wu = __builtin_amdgcn_readfirstlane(wave);
     const int H = p.n_kv * G;
-    const int64_t pos = *p.pos;
-    float* qs = lds;                // [G][HD]
-    float* kn = qs + G * HD;        // [HD] step key (normed, roped, rounded)
-    float* vn = kn + HD;            // [HD] step value (rounded)
-    float* wt = vn + HD;            // [P][G] weights exp(s - m)
-    float* ss = wt + P * G;         // [G][P] scaled scores (-inf beyond the span)
-    float* stat = ss + G * P;       // [2 G] m, l
-    float* wacc = stat + 2 * G;     // [PG][G][HD] value sums of the position groups
-    if (pos < 0 || pos >= p.maxt) {  // a position outside the cache: zeros out, no cache access
-        if (S == 1) {
-            for (int o = t; o < G * HD; o += NT) p.out[(int64_t)g * G * HD + o] = 0.0f;
-        } else {  // partials that combine to zeros: acc 0, and l = 1 on split 0 only
-            float* part = p.part + ((int64_t)g * S + sp) * G * (HD + 2);
-            for (int o = t; o < G * (HD + 2); o += NT) {
-                const int d = o % (HD + 2);
-                part[o] = d < HD ? 0.0f : (d == HD ? (sp == 0 ? 0.0f : -INFINITY) : (sp == 0 ? 1.0f : 0.0f));
-            }
-        }
-        return;
-    }
-    const int n = (int)pos + 1;  // n <= 10240 and S <= 128: 32-bit products
-    const int lo = (int)((uint32_t)(sp * n) / (uint32_t)S), hi = (int)((uint32_t)((sp + 1) * n) / (uint32_t)S);
-    const int span = hi - lo;  // <= P (host)
-    const int64_t row0 = (int64_t)g * p.maxt * HD;
-
+    // every kernel argument in SGPRs now: their loads then form one batch and
+    // one wait, not a chain of them after the position's
+    asm volatile("" : : "s"(p.maxt), "s"(p.n_kv), "s"(p.smul), "s"(__float_as_uint(p.eps)),
+                 "s"(__float_as_uint(p.scale)));
     // ---- 0. the step's values: wave w the heads w, w + NW, .. of q (0..G-1)
     // and k (G), lane l < HD/2 the pair (l, l + HD/2), thread d < HD v[d]
     const int la = lane < half ? lane : 0;
@@ -173,6 +152,28 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
     const float vown = __uint_as_float(
         __builtin_amdgcn_raw_buffer_load_b32(qr, ((H + p.n_kv + g) * HD + (t < HD ? t : 0)) * 4, 0, 0));
     const float wqa = p.qn[la], wqb = p.qn[la + half], wka = p.kn[la], wkb = p.kn[la + half], iv = p.inv[la];
+
+    // a position outside the cache is computed as position 0 with nothing
+    // cached (every cache load reads zeros) and no cache write, and its
+    // outputs are zeros (partials that combine to zeros): no branch before
+    // the loads, so the position's load and the step's q/k/v loads leave
+    // together
+    const int64_t pos_in = *p.pos;
+    const bool bad = pos_in < 0 || pos_in >= p.maxt;
+    const int64_t pos = bad ? 0 : pos_in;
+    float* qs = lds;                // [G][HD]
+    float* kn = qs + G * HD;        // [HD] step key (normed, roped, rounded)
+    float* vn = kn + HD;            // [HD] step value (rounded)
+    float* wt = vn + HD;            // [P][G] weights exp(s - m)
+    float* ss = wt + P * G;         // [G][P] scaled scores (-inf beyond the span)
+    float* stat = ss + G * P;       // [2 G] m, l
+    float* wacc = stat + 2 * G;     // [PG][G][HD] value sums of the position groups
+    const int n = (int)pos + 1;  // n <= 10240 and S <= 128: 32-bit products below 2^21
+    // (selects, not a branch: one split takes all n positions)
+    const int lo = S > 1 ? (int)__umulhi((uint32_t)(sp * n), p.smul) : 0;
+    const int hi = S > 1 ? (int)__umulhi((uint32_t)((sp + 1) * n), p.smul) : n;
+    const int span = hi - lo;  // <= P (host)
+    const int64_t row0 = (int64_t)g * p.maxt * HD;
 
     // the cache values: positions [0, min(hi, pos)) are in range
     const uint32_t cbytes = (uint32_t)min(hi, n - 1) * HD * EB;
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
         if (i < G) {
             norm_rope_wave<HD>(qa[j], qb[j], wqa, wqb, cs, sn, p.eps, qs + i * HD, lane);
         } else if (i == G) {  // k, rounded to the cache dtype; split 0 writes it at pos
-            void* krow = sp == 0 ? static_cast<char*>(p.kc) + (row0 + pos * HD) * EB : nullptr;
+            void* krow = sp == 0 && !bad ? static_cast<char*>(p.kc) + (row0 + pos * HD) * EB : nullptr;
             norm_rope_wave<HD, BF16>(qa[j], qb[j], wka, wkb, cs, sn, p.eps, kn, lane, krow);
         }
     }
@@ -214,8 +215,8 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
         if constexpr (BF16) {
             const uint16_t vb = f2bf16(v);
             v = bf16f(vb);
-            if (sp == 0) reinterpret_cast<uint16_t*>(p.vc)[row0 + pos * HD + t] = vb;
-        } else if (sp == 0) {
+            if (sp == 0 && !bad) reinterpret_cast<uint16_t*>(p.vc)[row0 + pos * HD + t] = vb;
+        } else if (sp == 0 && !bad) {
             reinterpret_cast<float*>(p.vc)[row0 + pos * HD + t] = v;
         }
         vn[t] = v;
@@ -350,12 +351,12 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < PG; ++w) v += wacc[(w * G + i) * HD + d];
-        if (S == 1) p.out[((int64_t)g * G + i) * HD + d] = v / stat[G + i];
-        else part[i * (HD + 2) + d] = v;
+        if (S == 1) p.out[((int64_t)g * G + i) * HD + d] = bad ? 0.0f : v / stat[G + i];
+        else part[i * (HD + 2) + d] = bad ? 0.0f : v;
     }
-    if (S > 1 && t < G) {
-        part[t * (HD + 2) + HD] = stat[t];
-        part[t * (HD + 2) + HD + 1] = stat[G + t];
+    if (S > 1 && t < G) {  // (a position outside the cache: l = 1 on split 0 only)
+        part[t * (HD + 2) + HD] = bad ? (sp == 0 ? 0.0f : -INFINITY) : stat[t];
+        part[t * (HD + 2) + HD + 1] = bad ? (sp == 0 ? 1.0f : 0.0f) : stat[G + t];
     }
 }
 
@@ -372,14 +373,16 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
 // R rows per kv head (G at one token, T G for a batch: row i is token i / G,
 // head i % G of the group); out is [T][n_heads][HD].
 // HD is a template argument, so the loops over the workgroup's waves unroll.
+// rmul, gmul: floor(2^32 / R) + 1 and floor(2^32 / G) + 1 (R, G >= 2), so
+// that the quotients of the row indexes (below 2^16) are mulhi products.
 template <int HD, int CB>
 __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, float* __restrict__ out, int S,
-                                                      int G, int R, int H) {
+                                                      int G, int R, int H, uint32_t rmul, uint32_t gmul) {
     constexpr int nw = HD >> 6;
     __shared__ float wts[kAttnMaxSplits];
     __shared__ float red[2][nw];
     const int h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
-    const int g = h / R, i = h % R;
+    const int g = R > 1 ? (int)__umulhi((uint32_t)h, rmul) : h, i = h - g * R;
     const int stride = R * (HD + 2) * 4;  // bytes from one split's partial of row i to the next
     const __amdgpu_buffer_rsrc_t r =
         attn_rsrc(part + ((int64_t)g * S * R + i) * (HD + 2), (uint32_t)((S - 1) * stride + (HD + 2) * 4));
@@ -426,21 +429,25 @@ __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ 
         for (int u = 0; u < CB; ++u)
             num = fmaf(a[u], s0 + u < S ? wts[min(s0 + u, kAttnMaxSplits - 1)] : 0.0f, num);
     }
-    out[((int64_t)(i / G) * H + g * G + i % G) * HD + d] = num / den;
+    const int tk = G > 1 ? (int)__umulhi((uint32_t)i, gmul) : i;  // token i / G, head g G + i % G
+    out[((int64_t)tk * H + g * G + (i - tk * G)) * HD + d] = num / den;
 }
 
 // the combine pass over R rows per kv head (nothing to do for one split)
+static uint32_t div_mul(int v) { return v > 1 ? (uint32_t)((uint64_t(1) << 32) / (uint64_t)v + 1) : 0u; }
+
 static void launch_combine(const AttnParams& p, int S, int G, int R, hipStream_t st) {
     const dim3 grid((unsigned)(p.n_kv * R)), block((unsigned)p.head_dim);
     if (S <= 1) return;
+    const uint32_t rm = div_mul(R), gm = div_mul(G);
     if (p.head_dim == 128) {
-        if (S <= 16) hipLaunchKernelGGL((k_attn_combine<128, 16>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
-        else if (S <= 32) hipLaunchKernelGGL((k_attn_combine<128, 32>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
-        else hipLaunchKernelGGL((k_attn_combine<128, 64>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
+        if (S <= 16) hipLaunchKernelGGL((k_attn_combine<128, 16>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads, rm, gm);
+        else if (S <= 32) hipLaunchKernelGGL((k_attn_combine<128, 32>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads, rm, gm);
+        else hipLaunchKernelGGL((k_attn_combine<128, 64>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads, rm, gm);
     } else {
-        if (S <= 16) hipLaunchKernelGGL((k_attn_combine<64, 16>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
-        else if (S <= 32) hipLaunchKernelGGL((k_attn_combine<64, 32>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
-        else hipLaunchKernelGGL((k_attn_combine<64, 64>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads);
+        if (S <= 16) hipLaunchKernelGGL((k_attn_combine<64, 16>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads, rm, gm);
+        else if (S <= 32) hipLaunchKernelGGL((k_attn_combine<64, 32>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads, rm, gm);
+        else hipLaunchKernelGGL((k_attn_combine<64, 64>), grid, block, 0, st, p.part, p.out, S, G, R, p.n_heads, rm, gm);
     }
 }
 
@@ -836,7 +843,9 @@ static int launch_attn_hd(const AttnParams& p, int G, int S, size_t lds, hipStre
     return -1;
 }
 
-int launch_attn(const AttnParams& p, int S, hipStream_t st) {
+int launch_attn(const AttnParams& pa, int S, hipStream_t st) {
+    AttnParams p = pa;
+    p.smul = div_mul(S);
     const int G = p.n_heads / p.n_kv;
     const size_t lds = attn_lds_bytes(p.head_dim, G, S == 1 && p.maxt > kAttnSpan ? kAttnLongThreads : kAttnThreads);
     int rc = p.head_dim == 128 ? launch_attn_hd<128>(p, G, S, lds, st)

@@ -128,6 +128,9 @@ struct AttnParams {
     float eps, scale;
     float* qo = nullptr;  // batch: the T tokens' normed, roped q rows [T][n_heads][HD]
     int T = 1;            // batch: tokens at positions *pos .. *pos + T - 1
+    // decode: floor(2^32 / splits) + 1, so that a / splits rounds down to
+    // mulhi(a, smul) for every a < 2^32 / splits (the split bounds: a <= 2^21)
+    uint32_t smul = 0;
 };
 constexpr int kAttnThreads = 320;     // 4 per position of the span
 constexpr int kAttnSpan = 80;         // positions one attention workgroup covers at most

@@ -282,3 +282,23 @@ def test_mfma_linear_addresses(model, kernel):
                 if S > 1:
                     assert ((S - 1) * T + T - 1) * npad + npad - 1 < S * T * npad
                     assert (S + 16) * T * npad * 4 < I32
+
+
+def test_attention_split_bounds_by_multiplier():
+    """The attention kernels divide by a multiplier the host computes,
+    floor(2^32 / v) + 1 (v >= 2), and a mulhi: the decode step's split bounds
+    (sp n) / S for n <= 10240 positions and S <= 128 splits (a < 2^21), and
+    the combine's row quotients h / R and i / G (below 2^16, R and G up to
+    1024).  Exhaustive against integer division over those ranges."""
+    import numpy as np
+
+    def mulhi_div(a, v):
+        m = np.uint64((1 << 32) // v + 1)
+        return (a.astype(np.uint64) * m) >> np.uint64(32)
+
+    a = np.arange(1 << 21, dtype=np.uint64)
+    for S in range(2, 129):
+        assert np.array_equal(mulhi_div(a, S), a // np.uint64(S)), S
+    h = np.arange(1 << 16, dtype=np.uint64)
+    for v in range(2, 1025):
+        assert np.array_equal(mulhi_div(h, v), h // np.uint64(v)), v
