@@ -434,14 +434,13 @@ __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p
 // before any is added, CB at a time through a descriptor over the partials
 // (one memory round trip for up to CB splits, where a load-add loop paid one
 // per split); the sum runs in split order.  CB = 8 where the splits fit,
-// else 16 (kReduceBatchMax).
+// else 16 (kReduceBatchMax).  Grid (rows / 256, tokens): no index division.
 template <int CB, bool RMS>
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, const float* __restrict__ ssq,
                                                        float* __restrict__ y, int N, int npad, int T, int S,
                                                        int mode, float eps, int K) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)T * N) return;
-    const int t = (int)(idx / N), n = (int)(idx % N);
+    const int t = blockIdx.y, n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= N) return;
     float* o = y + (int64_t)t * N + n;
     const float old = mode == 0 ? 0.0f : *o;
     // byte offsets in 32 bits: the host rejects (S + 16) T npad 4 >= 2^31
@@ -636,8 +635,7 @@ static int launch_rb(const LinearParams& p, int T, dim3 grid, int threads, size_
 
 template <int CB, bool RMS>
 static void launch_reduce_t(const LinearParams& p, int T, int splits, hipStream_t st) {
-    const int64_t tot = (int64_t)T * p.N;
-    hipLaunchKernelGGL((k_splitk_reduce<CB, RMS>), dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, p.part,
+    hipLaunchKernelGGL((k_splitk_reduce<CB, RMS>), dim3((unsigned)((p.N + 255) / 256), (unsigned)T), dim3(256), 0, st, p.part,
                        p.ssq, p.y, p.N, p.npad, T, splits, p.mode, p.eps, p.K);
 }
 
