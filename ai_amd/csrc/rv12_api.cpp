@@ -34,18 +34,21 @@ bool shape_fits(int K, int T, const Shape& c) {
 // linear shapes on MI355X.
 //   vector kernel: one row block per workgroup and 8 waves (16 for
 //     K >= 8192); two row blocks and 4 waves beyond 4096 row blocks; two
-//     row blocks and 8 waves for 257-512 row blocks (at 2 tokens only for
-//     K <= 6144); at one token 4 waves above 512 row blocks for K <= 6144
-//     and at most one wave per 8 K steps.  K is split at 2 tokens when
+//     row blocks and 8 waves for 257-512 row blocks, and from 3 tokens on
+//     for more; at one token 4 waves above 512 row blocks for K <= 6144
+//     and at most one wave per 8 K steps.  K is split from 2 tokens on when
 //     there are fewer than 128 row blocks, so the grid still covers the 256
-//     CUs, and wherever the activations would not fit in registers;
+//     CUs, and at one token wherever the activations would not fit in
+//     registers;
 //   MFMA kernel: the shape with the least time in a model of its rounds of
-//     workgroups (mfma_model_us);
-// The MFMA kernel is the built-in choice from 3 tokens on, except at 3
-// tokens on small matrices (up to 512 row blocks, K <= 6144), where the
-// vector kernel's FMAs still hide behind its weight stream; and at 2 tokens
-// where the vector kernel would have to split K to hold its activations in
-// registers (Qwen3-14B down: 35 vs 37.5 us).
+//     workgroups (mfma_model_us).
+// Which kernel: the vector kernel at 1 token; from 2 to 4 tokens where its
+// activations fit the LDS without a K split (a split adds rounds of
+// workgroups and the reduce pass) and, at 3 tokens, on up to 512 row blocks
+// or K <= 4096 (below 4096 row blocks), at 4 tokens on up to 512 row blocks
+// whose grid keeps at least 192 workgroups (or that split K to fill the CUs):
+// there its FMAs still hide behind the weight stream (vector_wins); the MFMA
+// kernel elsewhere.
 Shape vector_shape(int N, int K, int T) {
     const int64_t nblk = nblocks(N);
     Shape c;
@@ -55,11 +58,13 @@ Shape vector_shape(int N, int K, int T) {
     if (nblk >= 4096) {
         c.rb = 2;
         c.waves = 4;
-    } else if ((T == 1 || K <= 6144) && nblk > 256 && nblk <= 512) {
+    } else if (nblk > 256 && (nblk <= 512 || T >= 3)) {
         // 257-512 row blocks: two row blocks of 8 waves per workgroup
         // (Qwen3-8B qkv 11.0 -> 10.4 us, 14B o 12.3 -> 11.6, 32B o
         // 17.5 -> 15.6, 14B down 33.1 -> 27.7 with 3 splits; at 2 tokens
-        // 14B o 12.9 -> 11.1, 8B qkv 11.2 -> 10.1)
+        // 14B o 12.9 -> 11.1, 8B qkv 11.2 -> 10.1, 32B o 16.3 -> 14.4); from
+        // 3 tokens on also above (8B gate/up 24576x4096 at 3 tokens 32.2 ->
+        // 27.7, at 4 36.9 -> 30.6)
         c.rb = 2;
         c.waves = 8;
     } else if (T == 1 && nblk > 512 && K <= 6144) {
@@ -175,28 +180,43 @@ Shape mfma_shape(int N, int K, int T, int kernel = 2) {
     return best;
 }
 
+// 2 to 4 tokens: the vector kernel against the MFMA kernel's best shape, from
+// a sweep of 18 Qwen3-0.6B/8B/14B/32B linear shapes on MI355X (median of
+// interleaved timings).  Unsplit activations in LDS at every token count (at
+// 2 tokens Qwen3-14B down 5120x17408: 26.5 against 27.6 us; 32B down, whose
+// activations need a split, 43.8 against 37.6).  At 3 tokens up to 512 row
+// blocks (32B o 5120x8192: 15.9 against 17.1, 8B down 16.6-17.4 against
+// 18.3) or K <= 4096 below 4096 row blocks (8B gate/up 27.7 against 31.6;
+// the 8B head 151936x4096: 175.9 against 168.0), but not the wide K = 5120
+// matrices (14B gate/up 30.0 against 28.6, 32B qkv 20.1 against 18.6; 32B
+// gate/up 51200x5120 the exception, 70.7 against 74.5).  At 4 tokens the vector kernel's time grows with the tokens while the
+// MFMA kernel's stays: only where the grid keeps 3/4 of the CUs busy (8B qkv
+// 11.8 against 12.7, 14B qkv 14.4 against 15.9, 0.6B gate/up 5.7 against 8.4;
+// but 14B o, 160 workgroups of two row blocks: 13.4 against 12.8) or K is
+// split to fill them (14B k/v 7.2 against 8.1).
+bool vector_wins(int N, int K, int T, const Shape& v) {
+    if (T <= 1) return true;
+    if (T > kMaxVectorTokens || gemv_lds_bytes(K, T, v.rb, v.waves, 1) > kMaxLds) return false;
+    const int64_t nblk = nblocks(N);
+    if (T == 3) return nblk <= 512 || (K <= 4096 && nblk < 4096);
+    if (T == 4) return nblk <= 512 && (v.splits > 1 || (nblk + v.rb - 1) / v.rb >= 192);
+    return true;
+}
+
 Shape default_shape(int N, int K, int T) {
     const int nsteps = K / 32;
-    bool vec = T <= kVectorDefaultTokens;
-    if (T == 2 && !gemv_prefetch_all(K, T, vector_shape(N, K, T).waves, 1)) vec = false;
-    // 3 tokens on up to 512 row blocks of K <= 6144: the vector kernel,
-    // unsplit unless below 128 row blocks, matches or beats the MFMA kernel's
-    // best shape (MI355X: Qwen3-8B qkv 12.1 against 12.8 us, o 9.6 against
-    // 10.6; Qwen3-14B o, qkv, k/v within 1 %); at 4 tokens the MFMA kernel
-    // wins (14B o 13.6 against 14.8 us, k/v 7.9 against 8.2), and larger or
-    // longer matrices keep it (14B down 32.5 against 43.5, gate/up 29.9
-    // against 34.7 at 3 tokens)
-    const bool vec3 = T == 3 && K <= 6144 && nblocks(N) <= 512;
-    vec = vec || vec3;
-    Shape c = vec ? vector_shape(N, K, T) : mfma_shape(N, K, T);
+    const Shape v = vector_shape(N, K, T);
+    Shape c = vector_wins(N, K, T, v) ? v : mfma_shape(N, K, T);
     while (c.kernel != 3 && c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
     // at one token the vector kernel's waves want at least 8 K steps each
     // (Qwen3-0.6B qkv 4096x1024: 4.6 us at 4 waves, 5.1 at 8)
     while (c.kernel == 1 && T == 1 && c.waves > 2 && split_steps(K, c.splits) < 8 * c.waves) c.waves >>= 1;
     while (c.splits < kMaxSplits && c.splits < nsteps && !shape_fits(K, T, c)) ++c.splits;
-    // the vector kernel streams best with all activations loaded before the weights
+    // at one token the vector kernel streams best with all activations loaded
+    // before the weights; from 2 tokens on the unsplit launch that stages the
+    // rest after the weight prefetch is faster (32B o at 2 tokens: 14.4 us)
     const int s_fit = c.splits;
-    while (c.kernel == 1 && !vec3 && c.splits < kMaxSplits && c.splits < nsteps &&
+    while (c.kernel == 1 && T == 1 && c.splits < kMaxSplits && c.splits < nsteps &&
            !gemv_prefetch_all(K, T, c.waves, c.splits))
         ++c.splits;
     if (c.splits > s_fit) {

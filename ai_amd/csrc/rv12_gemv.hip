@@ -55,7 +55,7 @@ __device__ __forceinline__ void issue_step(u32x3 (&dst)[RB], __amdgpu_buffer_rsr
 // weight prefetch; columns beyond 4 * NXM * blockDim.x are staged after it.
 // M2: silu(g) * u prologue (MODE 2); LN: RMSNorm weight.  Both are template
 // arguments so that the loads of step 1 are straight-line code, issued without
-// waiting for any kernel argument test.  SH: the shallow prefetch (one token).
+// waiting for any kernel argument test.  SH: the shallow prefetch (4 steps).
 // The host guarantees blockDim.x >= 16 * RB * T (one thread per output).
 template <int T, int RB, bool M2, bool LN, bool SH>
 __global__ __launch_bounds__(gemv_max_waves(RB) * 64) void k_gemv(LinearParams p) {
@@ -609,7 +609,7 @@ static void launch_t(const LinearParams& p, dim3 grid, int threads, size_t lds, 
 
 template <int T, int RB, bool M2, bool LN>
 static void launch_depth(const LinearParams& p, dim3 grid, int threads, size_t lds, hipStream_t st) {
-    if (T == 1 && gemv_shallow(T, RB, threads / 64, M2, LN)) launch_t<T, RB, M2, LN, T == 1>(p, grid, threads, lds, st);
+    if (gemv_shallow(T, RB, threads / 64, M2, LN)) launch_t<T, RB, M2, LN, true>(p, grid, threads, lds, st);
     else launch_t<T, RB, M2, LN, false>(p, grid, threads, lds, st);
 }
 

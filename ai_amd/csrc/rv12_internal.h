@@ -41,8 +41,7 @@ constexpr size_t kMaxLds = 163840;  // LDS bytes of one gfx950 workgroup (160 KB
 constexpr size_t kDefaultLds = 65536;  // above this a kernel needs hipFuncAttributeMaxDynamicSharedMemorySize
 constexpr int kMaxK = 1 << 20;             // keeps every 32-bit buffer offset of a workgroup in range
 constexpr int64_t kMaxExc = (int64_t)1 << 28;  // exception entries of one matrix (read through 32-bit buffer ranges)
-constexpr int kMaxVectorTokens = 4;      // k_gemv (vector FMA) serves 1..4 tokens
-constexpr int kVectorDefaultTokens = 2;  // the built-in shape runs k_gemm from 3 tokens on
+constexpr int kMaxVectorTokens = 4;  // k_gemv (vector FMA) serves 1..4 tokens
 
 // --- vector-FMA linear (k_gemv), 1..4 tokens
 // K steps of the largest split
@@ -62,17 +61,24 @@ __host__ __device__ constexpr int gemv_max_waves(int rb) { return rb == 1 ? 16 :
 
 // weight steps in flight per wave.  At one token 6, 4 with the 2K
 // silu(g)*u activations and 8 for the one-row-block RMS variant (many rounds
-// of workgroups per CU), measured per Qwen3-8B shape; the shallow form (4)
-// where a workgroup's prefetch would pass kGemvPrefetchMax: its late waves
-// wait at the issue of their first loads, behind the CU's misses in flight
-// (8B qkv, 2 row blocks x 8 waves: 9.63 us at 6, 9.02 at 4).  At two tokens
-// 6 beat 8 on every shape (14B o 12.28 -> 11.93, gate/up 28.7 -> 28.1).
+// of workgroups per CU), measured per Qwen3-8B shape; at two tokens 6 (it beat
+// 8 on every shape: 14B o 12.28 -> 11.93, gate/up 28.7 -> 28.1), above 8.
+// The shallow form (4) for workgroups of 8 or more waves, at one token where
+// their first weight loads reach kGemvPrefetchMax: the late waves wait at the
+// issue of their first loads, behind the CU's misses in flight (8B qkv, 2 row
+// blocks x 8 waves: one token 9.63 us at 6, 9.02 at 4; two tokens 9.61 ->
+// 8.81; 14B o at three tokens 12.96 -> 11.10, 16 waves at four 20.27 ->
+// 17.44; one row block of 8 waves: 14B gate/up at two tokens 27.8 -> 26.0, 8B
+// o at three 8.89 -> 7.79, 0.6B qkv with RMS at one 4.79 -> 4.09).  With 4
+// waves the deep form stays (2 row blocks at four tokens: 14B o 18.1 us deep,
+// 20.2 shallow).
 __host__ __device__ constexpr int gemv_depth(int T, int rb, bool m2, bool ln, bool shallow) {
-    return T > 2 ? kDepth : (T == 2 ? 6 : (shallow || m2 ? 4 : (ln && rb == 1 ? kDepth : 6)));
+    return shallow ? 4 : (T > 2 ? kDepth : (T == 2 ? 6 : (m2 ? 4 : (ln && rb == 1 ? kDepth : 6))));
 }
 constexpr size_t kGemvPrefetchMax = 48 * 1024;  // bytes of one workgroup's first weight loads
 inline bool gemv_shallow(int T, int rb, int waves, bool m2, bool ln) {
-    return T == 1 && (size_t)waves * rb * gemv_depth(T, rb, m2, ln, false) * 768 /* one step tile */ > kGemvPrefetchMax;
+    return waves >= 8 && (T > 1 || (size_t)waves * rb * gemv_depth(T, rb, m2, ln, false) * 768 /* one step tile */ >=
+                                       kGemvPrefetchMax);
 }
 
 // launch shape fits the kernel's register budget and LDS

@@ -263,8 +263,9 @@ def _launch(BN, w, S, T):
     BN covers at least one row block per wave, else BN / 16 row blocks shared
     by the waves, which split K between them (kernel 3).  A given BN names its
     kernel; without one the library picks (rv12_launch_shape: the vector
-    kernel up to 2 tokens, except where it would have to split K at 2 tokens,
-    and at 3 tokens on small matrices)."""
+    kernel at one token, and at 2 to 4 tokens where its activations fit the
+    LDS unsplit and, at 3 and 4 tokens, on matrices small enough for its FMAs
+    to hide behind the weight stream)."""
     rb = kernel = 0
     if BN:
         vec = T <= VECTOR_TOKENS
@@ -274,6 +275,16 @@ def _launch(BN, w, S, T):
         rb = 1 if per <= 1 else (2 if per <= 2 else 4)
         kernel = KERNEL_VECTOR if vec else (KERNEL_MFMA_KSPLIT if ks else KERNEL_MFMA)
     return Launch(kernel, rb, int(w or 0), int(S or 0))
+
+
+_BUILTIN_KERNEL = {}  # (N, K, T) -> the kernel of the built-in launch shape
+
+
+def _builtin_kernel(N, K, T):
+    k = _BUILTIN_KERNEL.get((N, K, T))
+    if k is None:
+        k = _BUILTIN_KERNEL[(N, K, T)] = launch_shape(N, K, T)[0]
+    return k
 
 
 def launch_shape(N, K, T, cfg=None):
@@ -402,10 +413,12 @@ def gemvc_tc(x, c, y, mode, T, BN=None, w=None, S=None, lnw=None, eps=1e-6):
     (an addition: bf16 [K]) fuses each row's RMSNorm into the prologue, as
     gemvc1 does at one token, in place of a separate rmsg_k pass."""
     N, K = int(c["N"]), int(c["K"])
-    if BN is None and int(T) > VECTOR_TOKENS:  # CFGT is tuned at 16 tokens, for the MFMA kernel
+    if not 1 <= int(T) <= 16:
+        raise ValueError("T must be in [1, 16]")
+    # CFGT is tuned at 16 tokens, for the MFMA kernel: it applies from 3
+    # tokens on where the built-in choice is that kernel too
+    if BN is None and int(T) > VECTOR_TOKENS and _builtin_kernel(N, K, int(T)) != KERNEL_VECTOR:
         cfg = CFGT.get((N, K, mode))
         if cfg:
             BN, w, S = cfg
-    if not 1 <= int(T) <= 16:
-        raise ValueError("T must be in [1, 16]")
     _linear(x, c, y, mode, int(T), BN, w, S, lnw, eps, "gemvc_tc")

@@ -593,8 +593,10 @@ def run_skinny(name, reps, dev, min_bytes=1.2e9):
     """Qwen3-14B skinny-GEMM entry: one shape at every M of SWEEP_M, weights
     N(0, 0.02) bf16 with 0.1% of output rows x20, distinct copies totalling
     > 1 GB replayed round-robin, with the library's built-in kernel choice:
-    the vector kernel up to 2 tokens where its activations fit unsplit, else
-    the bf16 MFMA kernel (3 MFMAs per tile: the hi/mid/lo split of x)."""
+    the vector kernel at one token and, up to 4 tokens, where its activations
+    fit the LDS unsplit on the smaller matrices (qkv and k/v at 4 tokens, o at
+    2 and 3, down and gate/up at 2), else the bf16 MFMA kernel (3 MFMAs per
+    tile: the hi/mid/lo split of x)."""
     from ai_amd import wcomp
     N, K = SWEEP_14B[name]
     gen = torch.Generator().manual_seed(200 + sorted(SWEEP_14B).index(name))

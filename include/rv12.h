@@ -90,10 +90,11 @@ typedef struct rv12_launch {
 } rv12_launch;
 
 /* The launch shape a linear of n rows, k columns and t tokens runs with for
- * cfg (NULL or all-zero: the built-in choice — the vector kernel up to 2
- * tokens, at 2 only while its activations fit in registers without splitting
- * K, and at 3 tokens on matrices of up to 512 row blocks and k <= 6144;
- * the MFMA kernel otherwise, with waves, row blocks and splits from
+ * cfg (NULL or all-zero: the built-in choice — the vector kernel at 1 token,
+ * from 2 to 4 tokens where its activations fit the LDS without splitting K,
+ * at 3 tokens on up to 512 row blocks or k <= 4096 (below 4096 row blocks)
+ * and at 4 tokens on up to 512 row blocks that keep 192 workgroups or split
+ * K; the MFMA kernel otherwise, with waves, row blocks and splits from
  * launch-shape sweeps on MI355X; zero fields of a partial cfg are filled in,
  * with K split further where the given fields need it).  Fills *out and
  * returns RV12_OK, or the status rv12_gemm would return for the shape and

@@ -60,10 +60,11 @@ def test_sizes():
 
 
 def test_launch_shapes():
-    """The built-in launch table (host code only): the vector kernel up to 2
-    tokens while its activations fit unsplit, the MFMA kernel beyond; a
-    partial configuration is completed, with K split further where it needs
-    it."""
+    """The built-in launch table (host code only): the vector kernel at one
+    token, and from 2 to 4 tokens where its activations fit the LDS unsplit
+    and (3 and 4 tokens) the matrix is small enough for its FMAs to hide
+    behind the weight stream; the MFMA kernel beyond; a partial configuration
+    is completed, with K split further where it needs it."""
     from ai_amd import _lib
     L = _lib.lib()
 
@@ -82,17 +83,28 @@ def test_launch_shapes():
     assert shape(5120, 25600, 1) == (1, 2, 8, 3)          # 32B down
     assert shape(4096, 12288, 1) == (1, 1, 16, 1)         # down: 16 waves for K >= 8192
     assert shape(151936, 4096, 1) == (1, 2, 4, 1)         # lm_head: two row blocks per workgroup
-    assert shape(5120, 17408, 2)[0] == 2                  # Qwen3-14B down at 2 tokens: MFMA
-    assert shape(7168, 5120, 2) == (1, 2, 8, 1)           # 14B qkv at 2 tokens: vector, unsplit, 2 row blocks
-    assert shape(5120, 8192, 2) == (1, 1, 16, 1)          # 32B o at 2 tokens: K > 6144 keeps one row block
-    # 3 tokens on up to 512 row blocks of K <= 6144: the vector kernel
+    # 2 tokens: the vector kernel wherever its activations fit the LDS unsplit
+    assert shape(5120, 17408, 2) == (1, 2, 8, 1)          # Qwen3-14B down: 17408 columns x 2 tokens staged
+    assert shape(5120, 25600, 2)[0] == 2                  # 32B down: they need a split: MFMA
+    assert shape(7168, 5120, 2) == (1, 2, 8, 1)           # 14B qkv: unsplit, 2 row blocks
+    assert shape(5120, 8192, 2) == (1, 2, 8, 1)           # 32B o: 2 row blocks of 8 waves
+    assert shape(151936, 4096, 2) == (1, 2, 4, 1)         # 8B lm_head
+    # 3 tokens: up to 512 row blocks, or K <= 4096 below 4096 row blocks
     assert shape(6144, 4096, 3) == (1, 2, 8, 1)           # 8B qkv: two row blocks, unsplit
     assert shape(1024, 5120, 3) == (1, 1, 8, 4)           # 14B k/v: split below 128 row blocks
-    assert shape(5120, 17408, 3)[0] == 2                  # 14B down: MFMA
-    assert shape(4096, 4096, 4)[0] == 2                   # 4 tokens: MFMA
+    assert shape(24576, 4096, 3) == (1, 2, 8, 1)          # 8B gate/up: two row blocks of 8 waves
+    assert shape(5120, 17408, 3)[0] == 2                  # 14B down: its activations need a split: MFMA
+    assert shape(17408, 5120, 3)[0] == 2                  # 14B gate/up: MFMA
+    assert shape(151936, 4096, 3)[0] == 2                 # 8B lm_head: MFMA
+    # 4 tokens: up to 512 row blocks where the grid keeps >= 192 workgroups
+    assert shape(4096, 4096, 4) == (1, 1, 8, 1)           # 8B o: 256 workgroups
+    assert shape(6144, 4096, 4) == (1, 2, 8, 1)           # 8B qkv: 192 workgroups of two row blocks
+    assert shape(1024, 5120, 4) == (1, 1, 8, 4)           # 14B k/v: K split to fill the CUs
+    assert shape(5120, 5120, 4)[0] == 2                   # 14B o: 160 workgroups of two row blocks: MFMA
+    assert shape(4096, 12288, 4)[0] == 2                  # 8B down: its activations need a split: MFMA
     # the MFMA kernel's time model picks the shapes the MI355X sweeps found best
     assert shape(4096, 4096, 8) == (2, 1, 8, 8)           # 8B o: 256 workgroups of 16 K steps
-    assert shape(6144, 4096, 4) == (2, 1, 8, 5)           # 8B qkv: 240 workgroups of one row block per wave
+    assert shape(10240, 5120, 4) == (2, 2, 8, 6)          # 32B qkv: 640 row blocks, two per wave
     assert shape(1024, 5120, 16) == (2, 1, 4, 14)         # 14B k/v: 64 row blocks, 14 splits of 12 steps
     assert shape(5120, 5120, 4) == (2, 1, 8, 6)           # 14B o: 240 workgroups of 27 K steps
     assert shape(5120, 17408, 16) == (2, 2, 8, 12)        # 14B down: two row blocks per wave

@@ -103,8 +103,9 @@ def test_golden_matrices_all_modes(golden, case):
 
 @pytest.mark.parametrize("case", ["prefill_seed7", "outliers_rows_cols", "subnormal_heavy"])
 def test_rms_prologue_batched(golden, case):
-    """rv12_gemm with an RMSNorm weight at 2..16 tokens: the vector kernel at
-    2 tokens, the MFMA kernel from 3 on, one split and several."""
+    """rv12_gemm with an RMSNorm weight at 2..16 tokens with the built-in
+    kernel (on these small matrices the vector kernel at 2 and 3 tokens, the
+    MFMA kernel at 8 and 16), one split and several."""
     from ai_amd import wcomp
     print("case", case, flush=True)
     cnp = ref_dict(golden[case])
@@ -128,6 +129,28 @@ def _random_matrix(N, K, seed, sigma=0.02, out_rows=0.0, out_cols=0.0):
     return w.bfloat16().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
+@pytest.mark.parametrize("N,K", [(200, 1024), (520, 2560)])
+def test_vector_kernel_prefetch_depths(N, K):
+    """The vector kernel at 1-4 tokens in both of its prefetch depths, straight
+    through the C ABI: workgroups of 4 waves keep the deep form (6 or 8 steps),
+    of 8 or 16 waves the shallow one (4 steps; at one token where their first
+    weight loads reach 48 KB), one and two row blocks, a partial last row
+    block, with every prologue (RMS, accumulate, silu(g)*u, both), K split
+    (the built-in fill split below 128 row blocks from 2 tokens on) and
+    unsplit."""
+    from ai_amd import wcomp
+    print("shape", N, K, flush=True)
+    bits = _random_matrix(N, K, N + 3 * K, out_rows=0.01, out_cols=0.01)
+    cnp = codec.compress(bits)
+    cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+    for T in (1, 2, 3, 4):
+        for rb, w in ((1, 4), (1, 8), (1, 16), (2, 4), (2, 8)):
+            for S in ((0, 1) if T > 1 and w == 8 else (0,)):
+                print("  T", T, "rb", rb, "waves", w, "splits", S, flush=True)
+                for mode, rms in ((0, True), (1, False), (2, False), (2, True)):
+                    _check(cnp, cg, T, mode, rms, 40 + 7 * T + rb + w + mode, launch=(1, rb, w, S))
+
+
 @pytest.mark.parametrize("N,K", [(1, 256), (15, 256), (16, 512), (33, 1024), (100, 768), (1000, 2048)])
 def test_shapes_and_launch_shapes(N, K):
     from ai_amd import wcomp
@@ -136,7 +159,7 @@ def test_shapes_and_launch_shapes(N, K):
     cnp = codec.compress(bits)
     cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
     nsteps = K // 32
-    # vector kernel (the built-in choice up to 2 tokens): BN rows per workgroup
+    # vector kernel (the built-in choice at one token): BN rows per workgroup
     for BN, w, S in ((16, 1, 1), (16, 4, 1), (32, 2, 2), (64, 4, 1), (16, 3, min(5, nsteps)), (16, 4, nsteps)):
         if N % BN:
             BN = None  # the reference's N % BN rule; the default row tiling handles any N
@@ -144,7 +167,7 @@ def test_shapes_and_launch_shapes(N, K):
         for mode in (0, 2):
             _check(cnp, cg, 1, mode, mode == 0, 7, BN=BN, w=w)
             _check(cnp, cg, 2, mode, False, 8, BN=BN, w=w, S=S, use_tc=True)
-    # MFMA kernel (the built-in choice from 3 tokens): every row-block count
+    # MFMA kernel (the built-in choice on the larger matrices): every row-block count
     # per wave and wave count it takes (the split count left to the library:
     # the fewest splits whose staging fits the LDS, so long splits stage
     # groups past the 4 per thread held in registers), straight through the
