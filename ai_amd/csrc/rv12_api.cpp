@@ -35,8 +35,8 @@ bool shape_fits(int K, int T, const Shape& c) {
 //   vector kernel: one row block per workgroup and 8 waves (16 for
 //     K >= 8192); two row blocks and 4 waves beyond 4096 row blocks; two
 //     row blocks and 8 waves for 257-512 row blocks, and from 3 tokens on
-//     for more; at one token 4 waves above 512 row blocks for K <= 6144
-//     and at most one wave per 8 K steps.  K is split from 2 tokens on when
+//     for more; at one token 4 waves above 512 row blocks for K <= 6144.
+//     K is split from 2 tokens on when
 //     there are fewer than 128 row blocks, so the grid still covers the 256
 //     CUs, and at one token wherever the activations would not fit in
 //     registers;
@@ -207,10 +207,12 @@ Shape default_shape(int N, int K, int T) {
     const int nsteps = K / 32;
     const Shape v = vector_shape(N, K, T);
     Shape c = vector_wins(N, K, T, v) ? v : mfma_shape(N, K, T);
+    // (a former rule, at most one wave per 8 K steps at one token, no longer
+    // holds with the 4-step prefetch of 8-wave workgroups: at K = 1024, 8
+    // waves beat 4 with every prologue, Qwen3-0.6B qkv 4.12 against 4.53 us,
+    // gate/up with two row blocks 5.02 against 5.51, 1024x1024 3.55 against
+    // 3.91)
     while (c.kernel != 3 && c.waves > 1 && split_steps(K, c.splits) < c.waves) c.waves >>= 1;
-    // at one token the vector kernel's waves want at least 8 K steps each
-    // (Qwen3-0.6B qkv 4096x1024: 4.6 us at 4 waves, 5.1 at 8)
-    while (c.kernel == 1 && T == 1 && c.waves > 2 && split_steps(K, c.splits) < 8 * c.waves) c.waves >>= 1;
     while (c.splits < kMaxSplits && c.splits < nsteps && !shape_fits(K, T, c)) ++c.splits;
     // at one token the vector kernel streams best with all activations loaded
     // before the weights; from 2 tokens on the unsplit launch that stages the

@@ -77,7 +77,8 @@ def test_launch_shapes():
     assert shape(4096, 4096, 1) == (1, 1, 8, 1)           # o: 256 row blocks, one per workgroup
     assert shape(1024, 4096, 1) == (1, 1, 8, 1)           # k/v: 64 row blocks, K unsplit at one token
     assert shape(1024, 4096, 2) == (1, 1, 8, 4)           # ... split at two
-    assert shape(4096, 1024, 1) == (1, 1, 4, 1)           # Qwen3-0.6B qkv: 32 K steps, 4 waves
+    assert shape(4096, 1024, 1) == (1, 1, 8, 1)           # Qwen3-0.6B qkv: 32 K steps over 8 waves
+    assert shape(6144, 1024, 1) == (1, 2, 8, 1)           # 0.6B gate/up: 384 row blocks, two per workgroup
     assert shape(5120, 8192, 1) == (1, 2, 8, 1)           # 32B o: 320 row blocks of K 8192, two per workgroup
     assert shape(5120, 17408, 1) == (1, 2, 8, 3)          # 14B down: 3 splits fill the last round (480 workgroups)
     assert shape(5120, 25600, 1) == (1, 2, 8, 3)          # 32B down
