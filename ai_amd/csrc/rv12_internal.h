@@ -76,9 +76,11 @@ __host__ __device__ constexpr int gemv_depth(int T, int rb, bool m2, bool ln, bo
     return shallow ? 4 : (T > 2 ? kDepth : (T == 2 ? 6 : (m2 ? 4 : (ln && rb == 1 ? kDepth : 6))));
 }
 constexpr size_t kGemvPrefetchMax = 48 * 1024;  // bytes of one workgroup's first weight loads
+// (only where it changes the depth, so that a variant whose deep form is
+// already 4 steps keeps one instantiation)
 inline bool gemv_shallow(int T, int rb, int waves, bool m2, bool ln) {
-    return waves >= 8 && (T > 1 || (size_t)waves * rb * gemv_depth(T, rb, m2, ln, false) * 768 /* one step tile */ >=
-                                       kGemvPrefetchMax);
+    const int d = gemv_depth(T, rb, m2, ln, false);
+    return d > 4 && waves >= 8 && (T > 1 || (size_t)waves * rb * d * 768 /* one step tile */ >= kGemvPrefetchMax);
 }
 
 // launch shape fits the kernel's register budget and LDS
