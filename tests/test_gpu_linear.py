@@ -249,10 +249,11 @@ def test_lm_head_full_size():
 
 @pytest.mark.parametrize("N,K,shape1,shape2", [
     (1000, 2048, (1, 1, 8, 1), (1, 1, 8, 4)),    # 63 row blocks: unsplit at one token, split at two
-    (4100, 1024, (1, 2, 4, 1), (1, 2, 8, 1)),    # 257 row blocks of 32 K steps: two per workgroup
+    (4100, 1024, (1, 2, 8, 1), (1, 2, 8, 1)),    # 257 row blocks of 32 K steps: two per workgroup of 8 waves
     (6000, 4096, (1, 2, 8, 1), (1, 2, 8, 1)),    # 375 row blocks
     (8300, 1024, (1, 1, 4, 1), (1, 1, 8, 1)),    # 519 row blocks, ragged: 4 waves at one token
-    (5000, 17408, (1, 2, 8, 3), None),           # 313 row blocks of a long K: 3 splits fill the round
+    (5000, 17408, (1, 2, 8, 3), (1, 2, 8, 1)),   # 313 row blocks of a long K: 3 splits fill the round at
+                                                  # one token; unsplit at two (the activations fit the LDS)
 ])
 def test_default_launch_shape_families(N, K, shape1, shape2):
     """The built-in launch shape of each row-block range (asserted), every
