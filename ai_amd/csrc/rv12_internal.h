@@ -47,8 +47,13 @@ constexpr int kMaxVectorTokens = 4;  // k_gemv (vector FMA) serves 1..4 tokens
 // K steps of the largest split
 inline int split_steps(int K, int splits) { return (K / 32 + splits - 1) / splits; }
 
-// float4 activation chunks per thread the kernel keeps in registers
-__host__ __device__ constexpr int gemv_chunks(int T) { return T == 1 ? 6 : (T == 2 ? 3 : 1); }
+// float4 activation chunks per thread the kernel keeps in registers (loaded
+// before the weight prefetch; the rest of the split's columns are staged
+// after it).  Two from 3 tokens on (one before: 8B qkv at 4 tokens 11.41 ->
+// 10.21 us, 8B o 8.79 -> 7.94, 14B qkv 14.36 -> 13.43; no spill, the
+// one-row-block variants at most 120 VGPRs of their 128); three at 3 tokens
+// measured within a few percent either way.
+__host__ __device__ constexpr int gemv_chunks(int T) { return T == 1 ? 6 : (T == 2 ? 3 : 2); }
 
 inline size_t gemv_lds_bytes(int K, int T, int rb, int waves, int splits) {
     const size_t krange = (size_t)split_steps(K, splits) * 32;
