@@ -277,6 +277,37 @@ def test_default_launch_shape_families(N, K, shape1, shape2):
         assert float((err / (np.abs(ref) + 1.0)).max()) < 1e-4, (N, K, T, mode, float(err.max()))
 
 
+def test_builtin_launch_random_shapes():
+    """Seeded random shapes (ragged N, K from 256 to 12288) at 1-4 tokens with
+    every prologue, each through the launch the library picks for it (vector
+    kernel, either prefetch depth, split or not, or the MFMA kernel), against
+    the C oracle: the launch rules' every branch meets the same bar."""
+    from ai_amd import wcomp
+    rng = np.random.default_rng(2026)
+    seen = set()
+    for case in range(24):
+        N = int(rng.integers(1, 9000))
+        K = 256 * int(rng.integers(1, 49))
+        T = int(rng.integers(1, 5))
+        mode = int(rng.integers(0, 3))
+        rms = bool(rng.integers(0, 2))
+        shape = wcomp.launch_shape(N, K, T)
+        seen.add(shape[0])
+        print("case", case, N, K, T, mode, rms, shape, flush=True)
+        bits = _random_matrix(N, K, 100 + case, out_rows=0.002, out_cols=0.002)
+        cnp = cref.compress(bits)
+        cg = wcomp.compress(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda())
+        X, Y0, lnw = _inputs(cnp, T, mode, 200 + case, rms)
+        ref = Y0.copy()
+        cref.gemv_12bit(cnp, X, ref, mode, lnw=lnw)
+        y = _run(cg, X, Y0, mode, T, lnw=lnw, use_tc=T > 1)
+        err = np.abs(y.astype(np.float64) - ref)
+        assert np.all(err <= ATOL + RTOL * np.abs(ref)), (case, N, K, T, mode, rms, shape, float(err.max()))
+        assert float((err / (np.abs(ref) + 1.0)).max()) < 1e-4, (case, N, K, T, mode, rms, shape, float(err.max()))
+        del cg
+    assert seen == {1, 2}, seen  # both kernels were picked
+
+
 def test_tuned_launch_shapes_keep_parity(tmp_path):
     """tune() fills CFG1 / CFGT on the GPU; the linears then run with those
     launch shapes and still match the closed form: a plain MODE 0 shape,
