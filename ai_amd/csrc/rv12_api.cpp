@@ -600,7 +600,9 @@ static int check_attn(const rv12_attn* a) {
     const bool longspan = a->splits == 1 && a->maxt > kAttnSpan;
     if (longspan ? a->maxt > kAttnLongSpan : (a->maxt + a->splits - 1) / a->splits > kAttnSpan)
         return RV12_E_CONFIG;
-    if (attn_lds_bytes(a->head_dim, g, longspan ? kAttnLongThreads : kAttnThreads) > kMaxLds) return RV12_E_CONFIG;
+    // (the long-span workgroup takes one q head)
+    if (attn_lds_bytes(a->head_dim, longspan ? 1 : g, longspan ? kAttnLongThreads : kAttnThreads) > kMaxLds)
+        return RV12_E_CONFIG;
     return RV12_OK;
 }
 

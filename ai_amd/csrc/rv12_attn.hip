@@ -2,8 +2,10 @@
 // the 12-bit linears in a decode step (replaces rope_attn_k,
 // ramvi/engine/ramvi_engine/kernels/tkernels.py:164-213).
 //
-// Grid (KV heads, splits), 320 threads.  Workgroup (g, sp) covers the
-// positions [lo, hi) of 0..pos, at most 80 of them:
+// Grid (KV heads, splits), 320 threads (a short cache: one split, 1024
+// threads and one workgroup per q head instead, QH below).  Workgroup (g, sp)
+// covers the positions [lo, hi) of 0..pos, at most 80 of them (256 at 1024
+// threads):
 //   0. first the step's own q/k/v values, then every cache value the
 //      workgroup reads are loaded: a quarter key row (HD/4 dims) per thread,
 //      4 threads per position, and the values of 16 (8) positions at a dim
@@ -115,9 +117,14 @@ __device__ __forceinline__ void norm_rope_wave(float a, float b, float wa, float
 
 // NT threads, 4 per position: a workgroup covers P = NT / 4 positions at
 // most (kAttnThreads = 320 over 80 positions; kAttnLongThreads = 1024 over
-// 256, one split per kv head for short contexts, so no combine pass)
-template <int HD, int G, bool BF16, int NT>
+// 256, one split per kv head for short contexts, so no combine pass).  GK q
+// heads share a kv head.  QH (one split only): one workgroup per q head
+// instead of per kv head, the grid over the q heads; the first q head of each
+// kv head writes the step's key and value into the cache (the others read
+// only the positions before it, which the write does not touch).
+template <int HD, int GK, bool BF16, int NT, bool QH = false>
 __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
+    constexpr int G = QH ? 1 : GK;  // q heads of this workgroup
     extern __shared__ float lds[];
     constexpr int NW = NT / 64;
     constexpr int P = NT / 4;              // positions of one workgroup at most
@@ -128,10 +135,12 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
     constexpr int PG = NT / DP;            // position groups of the value sums
     constexpr int PPG = P / PG;            // positions per group
     constexpr int half = HD / 2, HPW = (G + NW) / NW;
-    const int g = blockIdx.x, sp = blockIdx.y, S = gridDim.y;
+    const int g = QH ? (int)blockIdx.x / GK : (int)blockIdx.x, sp = blockIdx.y, S = gridDim.y;
+    const int qh0 = QH ? (int)blockIdx.x : g * G;            // the workgroup's first q head
+    const bool writer = !QH || (int)blockIdx.x == g * GK;  // writes the step's k and v
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wu = __builtin_amdgcn_readfirstlane(wave);
-    const int H = p.n_kv * G;
+    const int H = p.n_kv * GK;
     // every kernel argument in SGPRs now: their loads then form one batch and
     // one wait, not a chain of them after the position's
     asm volatile("" : : "s"(p.maxt), "s"(p.n_kv), "s"(p.smul), "s"(__float_as_uint(p.eps)),
@@ -145,7 +154,7 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
         const int i = min(wave + j * NW, G);
-        const int off = ((i < G ? g * G + i : H + g) * HD + la) * 4;
+        const int off = ((i < G ? qh0 + i : H + g) * HD + la) * 4;
         qa[j] = msk * __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(qr, off, 0, 0));
         qb[j] = msk * __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(qr, off + half * 4, 0, 0));
     }
@@ -206,7 +215,7 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
         if (i < G) {
             norm_rope_wave<HD>(qa[j], qb[j], wqa, wqb, cs, sn, p.eps, qs + i * HD, lane);
         } else if (i == G) {  // k, rounded to the cache dtype; split 0 writes it at pos
-            void* krow = sp == 0 && !bad ? static_cast<char*>(p.kc) + (row0 + pos * HD) * EB : nullptr;
+            void* krow = sp == 0 && !bad && writer ? static_cast<char*>(p.kc) + (row0 + pos * HD) * EB : nullptr;
             norm_rope_wave<HD, BF16>(qa[j], qb[j], wka, wkb, cs, sn, p.eps, kn, lane, krow);
         }
     }
@@ -215,8 +224,8 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
         if constexpr (BF16) {
             const uint16_t vb = f2bf16(v);
             v = bf16f(vb);
-            if (sp == 0 && !bad) reinterpret_cast<uint16_t*>(p.vc)[row0 + pos * HD + t] = vb;
-        } else if (sp == 0 && !bad) {
+            if (sp == 0 && !bad && writer) reinterpret_cast<uint16_t*>(p.vc)[row0 + pos * HD + t] = vb;
+        } else if (sp == 0 && !bad && writer) {
             reinterpret_cast<float*>(p.vc)[row0 + pos * HD + t] = v;
         }
         vn[t] = v;
@@ -345,13 +354,14 @@ __global__ __launch_bounds__(NT) void k_rope_attn(AttnParams p) {
     __syncthreads();
 
     // ---- 5. output or partials
-    float* part = p.part + ((int64_t)g * S + sp) * G * (HD + 2);  // [n_kv][S][G][HD + 2]
+    // [n_kv][S][G][HD + 2] (S > 1 only, which the one-q-head form never runs with)
+    float* part = p.part + ((int64_t)g * S + sp) * G * (HD + 2);
     for (int o = t; o < G * HD; o += NT) {
         const int i = o / HD, d = o % HD;
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < PG; ++w) v += wacc[(w * G + i) * HD + d];
-        if (S == 1) p.out[((int64_t)g * G + i) * HD + d] = bad ? 0.0f : v / stat[G + i];
+        if (S == 1) p.out[((int64_t)qh0 + i) * HD + d] = bad ? 0.0f : v / stat[G + i];
         else part[i * (HD + 2) + d] = bad ? 0.0f : v;
     }
     if (S > 1 && t < G) {  // (a position outside the cache: l = 1 on split 0 only)
@@ -810,20 +820,24 @@ int launch_attn_batch(const AttnParams& p, int S, hipStream_t st) {
     return 0;
 }
 
-template <int HD, int G, bool BF16, int NT>
+template <int HD, int G, bool BF16, int NT, bool QH>
 static void launch_attn_nt(const AttnParams& p, int S, hipStream_t st) {
-    const size_t lds = attn_lds_bytes(HD, G, NT);
+    const size_t lds = attn_lds_bytes(HD, QH ? 1 : G, NT);
     if (lds > kDefaultLds)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_rope_attn<HD, G, BF16, NT>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_rope_attn<HD, G, BF16, NT, QH>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((k_rope_attn<HD, G, BF16, NT>), dim3(p.n_kv, S), dim3(NT), lds, st, p);
+    hipLaunchKernelGGL((k_rope_attn<HD, G, BF16, NT, QH>), dim3(QH ? p.n_heads : p.n_kv, S), dim3(NT), lds, st, p);
 }
 
-// one split over more than kAttnSpan positions: the long-span workgroup
+// one split over more than kAttnSpan positions: the long-span workgroup, one
+// per q head (Qwen3-0.6B shape, 16 q over 8 kv heads at a 192-position cache:
+// 5.10-5.15 us per layer at position 100 against 5.82 with one workgroup per
+// kv head, 5.86-5.91 against 5.93-6.04 at 190; the 0.6B decode 1292 -> 1330
+// tokens/s)
 template <int HD, int G, bool BF16>
 static void launch_attn_t(const AttnParams& p, int S, size_t, hipStream_t st) {
-    if (S == 1 && p.maxt > kAttnSpan) launch_attn_nt<HD, G, BF16, kAttnLongThreads>(p, S, st);
-    else launch_attn_nt<HD, G, BF16, kAttnThreads>(p, S, st);
+    if (S == 1 && p.maxt > kAttnSpan) launch_attn_nt<HD, G, BF16, kAttnLongThreads, true>(p, S, st);
+    else launch_attn_nt<HD, G, BF16, kAttnThreads, false>(p, S, st);
 }
 
 template <int HD, int G>
@@ -847,7 +861,8 @@ int launch_attn(const AttnParams& pa, int S, hipStream_t st) {
     AttnParams p = pa;
     p.smul = div_mul(S);
     const int G = p.n_heads / p.n_kv;
-    const size_t lds = attn_lds_bytes(p.head_dim, G, S == 1 && p.maxt > kAttnSpan ? kAttnLongThreads : kAttnThreads);
+    const bool longspan = S == 1 && p.maxt > kAttnSpan;  // one workgroup per q head
+    const size_t lds = attn_lds_bytes(p.head_dim, longspan ? 1 : G, longspan ? kAttnLongThreads : kAttnThreads);
     int rc = p.head_dim == 128 ? launch_attn_hd<128>(p, G, S, lds, st)
                                : (p.head_dim == 64 ? launch_attn_hd<64>(p, G, S, lds, st) : -1);
     if (rc) return rc;

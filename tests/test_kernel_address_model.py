@@ -88,13 +88,29 @@ def test_vector_linear_addresses(model, T):
 
 @pytest.mark.parametrize("model", sorted(MODELS))
 def test_decode_attention_long_span_addresses(model):
-    """One split per kv head over a short cache (the 1024-thread workgroup,
-    up to 256 positions): the positions its threads address stay inside
-    the span, the cache rows inside the cache, the offsets in 32 bits."""
+    """One split over a short cache (the 1024-thread workgroup, up to 256
+    positions, one workgroup per q head): the positions its threads address
+    stay inside the span, the cache rows inside the cache, the offsets in 32
+    bits; workgroup h reads q row h, the k and v rows of kv head h / G and
+    that head's cache, writes output row h, and only the first q head of each
+    kv head writes the cache (one writer per kv head)."""
     D, H, KV, HD, FF, V = MODELS[model]
     from ai_amd.attn import LONG_SPAN, default_splits
     NT, P = 1024, 256
+    G = H // KV
     assert P == LONG_SPAN
+    qkv_floats = (H + 2 * KV) * HD
+    writers = {}
+    for h in range(H):  # grid over the q heads
+        g = h // G
+        assert 0 <= g < KV
+        assert (h * HD + HD - 1) < H * HD                                   # q row h (its own head)
+        assert ((H + g) * HD + HD - 1) < qkv_floats                         # k row of kv head g
+        assert ((H + KV + g) * HD + HD - 1) < qkv_floats                    # v row of kv head g
+        assert h * HD + HD - 1 < H * HD                                     # output row h
+        if h == g * G:
+            writers[g] = writers.get(g, 0) + 1
+    assert writers == {g: 1 for g in range(KV)}
     for maxt, eb in ((81, 2), (192, 2), (256, 2), (256, 4)):
         S = default_splits(KV, maxt, eb == 2, HD)
         if S != 1:
