@@ -71,11 +71,11 @@ def test_rope_attn_matches_torch(H, KV, HD, kv_dtype):
 @pytest.mark.parametrize("H,KV,HD", [(32, 8, 128), (16, 8, 128), (8, 4, 64), (64, 8, 128), (8, 8, 64)])
 @pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16])
 def test_long_span_single_split_matches_torch(H, KV, HD, kv_dtype):
-    """A cache of up to 256 positions takes one split per kv head (the
-    1024-thread workgroup over up to 256 positions, no combine pass): against
-    the float64 reference at positions inside and past the first 80, with the
-    cache slot written as in the split kernel, and equal within float32
-    rounding to the same step over 5 splits."""
+    """A cache of up to 256 positions takes one split (the 1024-thread
+    workgroup over up to 256 positions, one per q head, no combine pass):
+    against the float64 reference at positions inside and past the first 80,
+    with the cache slot written once per kv head as in the split kernel, and
+    equal within float32 rounding to the same step over 5 splits."""
     from ai_amd.attn import RopeAttn, default_splits
     dev = "cuda"
     g = torch.Generator(device=dev).manual_seed(H * 10 + HD + 7)
