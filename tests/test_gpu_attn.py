@@ -112,11 +112,15 @@ def test_long_span_single_split_matches_torch(H, KV, HD, kv_dtype):
             assert torch.equal(kc[:, keep], kc0[:, keep]) and torch.equal(vc[:, keep], vc0[:, keep])
 
 
-def test_position_outside_cache_gives_zeros():
+@pytest.mark.parametrize("maxt,splits", [(32, 4), (100, 1)])
+def test_position_outside_cache_gives_zeros(maxt, splits):
+    """A position outside the cache writes no cache row and gives zeros; with
+    the split kernel (4 splits) and with the short-cache workgroup per q head
+    (one split over 100 positions); then a position inside the cache."""
     from ai_amd.attn import RopeAttn
     dev = "cuda"
-    H, KV, HD, maxt = 8, 4, 64, 32
-    att = RopeAttn(H, KV, HD, maxt, torch.float32, 1e-6, dev, splits=4)
+    H, KV, HD = 8, 4, 64
+    att = RopeAttn(H, KV, HD, maxt, torch.float32, 1e-6, dev, splits=splits)
     kc = torch.randn(KV, maxt, HD, device=dev)
     vc = torch.randn(KV, maxt, HD, device=dev)
     kc0, vc0 = kc.clone(), vc.clone()
@@ -133,6 +137,9 @@ def test_position_outside_cache_gives_zeros():
     torch.cuda.synchronize()
     ref, _, _ = _torch_ref(qkv, ones, ones, inv, maxt - 1, kc0, vc0, H, KV, HD, 1e-6, k_at_pos=kc[:, maxt - 1].clone())
     assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5), float((out - ref).abs().max())
+    keep = torch.ones(maxt, dtype=torch.bool)
+    keep[maxt - 1] = False
+    assert torch.equal(kc[:, keep], kc0[:, keep]) and torch.equal(vc[:, keep], vc0[:, keep])
 
 
 def test_single_split_and_split_limits():
